@@ -1,0 +1,118 @@
+/* Internal definitions shared by the HIP sources of libaotx_hip.so. */
+#ifndef AOTX_INTERNAL_H
+#define AOTX_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <stdint.h>
+
+#include "../../include/aotx_hip.h"
+
+/* A failing runtime call ends the process with its site, as the reference's check does
+ * (cuda/boot/check.h:13-33). */
+#define AOTX_CHECK(call)                                                                  \
+    do {                                                                                  \
+        hipError_t aotx_err_ = (call);                                                    \
+        if (aotx_err_ != hipSuccess) {                                                    \
+            fprintf(stderr, "aotx: %s failed at %s:%d: %s\n", #call, __FILE__, __LINE__,  \
+                    hipGetErrorString(aotx_err_));                                        \
+            exit(1);                                                                      \
+        }                                                                                 \
+    } while (0)
+
+#define AOTX_LAUNCH_CHECK() AOTX_CHECK(hipGetLastError())
+
+/* Device-resident state of the runtime: the page table and request queue, every slot's
+ * cache position and draw counter, and the fault count. The reference keeps these as
+ * device symbols (aotx_kv, aotx_model_seen, aotx_model_draw, aotx_model_faults:
+ * cuda/kvcache/kvcache.cuh:66, cuda/model/forward.cuh:180-191); here they are one
+ * allocation whose address every kernel takes as an argument. */
+struct aotx_state {
+    aotx_kv_table kv;
+    unsigned int seen[AOTX_SLOTS];
+    unsigned int draw[AOTX_SLOTS];
+    unsigned int faults;
+};
+
+/* The device state of the current device, allocated and zeroed on first use. */
+aotx_state *aotx_state_device(void);
+
+/* Per-call scratch of the library (partial sums, arrival counters). One growable buffer
+ * per use; counters are zeroed once at allocation and every kernel that uses one puts
+ * it back to zero before it exits. */
+void *aotx_scratch(int which, size_t bytes);
+enum {
+    AOTX_SCRATCH_GEMV_PARTIAL = 0,
+    AOTX_SCRATCH_GEMV_COUNT,
+    AOTX_SCRATCH_ATTN_PARTIAL,
+    AOTX_SCRATCH_ATTN_COUNT,
+    AOTX_SCRATCH_EXPERT,
+    AOTX_SCRATCH_KINDS
+};
+
+static inline hipStream_t aotx_stream(void *s) { return (hipStream_t)s; }
+
+/* ---- paged layout (cuda/model/kv_layout.cuh:37-163), one layer kind: every layer owns
+ * KV pages. ---- */
+struct aotx_kvl_shape {
+    unsigned int layers;
+    unsigned int kv_heads;
+    unsigned int head_dim;
+    unsigned int head_bytes;    /* 16 positions of one head */
+    unsigned int block_bytes;   /* K heads then V heads */
+    unsigned int blocks_page;
+};
+
+static inline __host__ __device__ aotx_kvl_shape aotx_kvl_make(unsigned int layers,
+                                                               unsigned int kv_heads,
+                                                               unsigned int head_dim)
+{
+    aotx_kvl_shape s;
+    s.layers = layers;
+    s.kv_heads = kv_heads;
+    s.head_dim = head_dim;
+    s.head_bytes = AOTX_KVL_BLOCK * head_dim * 2u;
+    s.block_bytes = 2u * kv_heads * s.head_bytes;
+    s.blocks_page = s.block_bytes == 0u ? 0u
+        : (unsigned int)((AOTX_KV_PAGE_BYTES - AOTX_KVL_HEADER) / s.block_bytes);
+    return s;
+}
+
+static inline __host__ __device__ unsigned int aotx_kvl_pages(const aotx_kvl_shape &s,
+                                                              unsigned int context)
+{
+    if (s.blocks_page == 0u) return 0u;
+    unsigned int blocks = ((context + AOTX_KVL_BLOCK - 1u) / AOTX_KVL_BLOCK) * s.layers;
+    return (blocks + s.blocks_page - 1u) / s.blocks_page;
+}
+
+/* First byte of the layout block holding (layer, position) of one slot, or null. */
+static inline __device__ unsigned char *aotx_kvl_block(const aotx_kvl_shape &s,
+                                                       const aotx_kv_table *kv,
+                                                       unsigned int agent,
+                                                       unsigned int layer,
+                                                       unsigned int position)
+{
+    if (s.blocks_page == 0u || agent >= AOTX_SLOTS) return nullptr;
+    unsigned int block = (position / AOTX_KVL_BLOCK) * s.layers + layer;
+    unsigned int index = block / s.blocks_page;
+    if (index >= AOTX_KV_PAGES_EACH) return nullptr;
+    unsigned long long page = kv->page[agent][index];
+    if (page == 0ull) return nullptr;
+    return (unsigned char *)(page + AOTX_KVL_HEADER
+                             + (unsigned long long)(block % s.blocks_page) * s.block_bytes);
+}
+
+/* fp16 <-> fp32 on raw bits */
+static inline __device__ float aotx_h2f(unsigned short h)
+{
+    return __half2float(__ushort_as_half(h));
+}
+static inline __device__ unsigned short aotx_f2h(float f)
+{
+    return __half_as_ushort(__float2half(f));
+}
+
+#endif

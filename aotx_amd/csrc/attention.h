@@ -1,0 +1,21 @@
+/* Paged decode attention (attention.hip): launch interface for the model runtime. */
+#ifndef AOTX_ATTENTION_H
+#define AOTX_ATTENTION_H
+
+#include "aotx_internal.h"
+
+/* Chunks per (token, KV head) for a launch of `tokens` rows. */
+unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
+                              unsigned int max_context);
+/* Bytes of the chunk partials of such a launch. */
+size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned int splits,
+                         unsigned int group, unsigned int head_dim);
+/* q/out fp16 [tokens][heads][d]; m_dev = device token count (or null); partial = the
+ * caller's chunk buffer (or null for the library scratch). */
+int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsigned int *pos,
+                       const unsigned int *agent, const unsigned int *m_dev,
+                       unsigned int tokens, unsigned int heads, unsigned int kv_heads,
+                       unsigned int head_dim, unsigned int layer, unsigned int layers,
+                       unsigned int max_context, float *partial, hipStream_t stream);
+
+#endif

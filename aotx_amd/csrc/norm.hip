@@ -1,0 +1,305 @@
+/* Row kernels of the step: cache positions, embedding gather, residual + RMSNorm, the
+ * rotary turn with the page write (general path), and the weighted expert sum.
+ *
+ * Reference: cuda/model/gather.cu:8-105 (request, open/shut rows, gather, select),
+ * cuda/model/norm.cu:49-105 (norm, residual, SwiGLU), cuda/model/rope.cu:128-234 (turn +
+ * page write), cuda/model/experts.cu:77-98 (ordered weighted sum). The residual add that
+ * follows a projection, the expert sum and the norm that reads the residual are one
+ * kernel here: the split partial tiles of the projection are added in split order, then
+ * the residual row is normed, so the residual makes one trip through HBM per layer half.
+ */
+#include "aotx_internal.h"
+#include "norm.h"
+
+/* Sum over a 256-thread block: per-wave butterfly, then the 4 wave sums in order. */
+static __device__ __forceinline__ float aotx_block_sum(float v, float *share)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const unsigned int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0u) share[wave] = v;
+    __syncthreads();
+    float total = 0.0f;
+    const unsigned int waves = (blockDim.x + 63u) >> 6;
+    for (unsigned int w = 0; w < waves; ++w) total += share[w];
+    return total;
+}
+
+static __device__ __forceinline__ unsigned int aotx_which(const unsigned int *offset,
+                                                          unsigned int seqs, unsigned int row)
+{
+    unsigned int low = 0u, high = seqs;
+    while (low + 1u < high) {
+        unsigned int mid = (low + high) / 2u;
+        if (offset[mid] <= row) low = mid; else high = mid;
+    }
+    return low;
+}
+
+/* Cache position and slot of every token (cuda/model/gather.cu:29-40 with the bisection
+ * of cuda/model/forward.cuh:200-214); also the row each sequence's last token selects. */
+__global__ void aotx_rows_kernel(const aotx_step *step, aotx_state *state, unsigned int *pos,
+                                 unsigned int *tagent, unsigned int *last)
+{
+    const aotx_model_run *run = &step->run;
+    unsigned int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < run->seqs) {
+        last[t] = run->offset[t + 1u] - 1u;
+    }
+    if (t >= run->tokens) return;
+    unsigned int s = aotx_which(run->offset, run->seqs, t);
+    unsigned int agent = run->agent[s];
+    unsigned int base = agent < AOTX_SLOTS ? state->seen[agent] : 0u;
+    pos[t] = base + (t - run->offset[s]);
+    tagent[t] = agent;
+}
+
+/* Move every slot's cache position on by its tokens (cuda/model/gather.cu:42-51). */
+__global__ void aotx_shut_rows_kernel(const aotx_step *step, aotx_state *state)
+{
+    const aotx_model_run *run = &step->run;
+    unsigned int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= run->seqs) return;
+    unsigned int agent = run->agent[s];
+    if (agent < AOTX_SLOTS) state->seen[agent] += run->offset[s + 1u] - run->offset[s];
+}
+
+/* Ask the page cache for the pages of the next pass (cuda/model/gather.cu:8-26) and
+ * queue the request as cuda/kvcache/pages.cu:13-36 does: a full queue or a bad slot is
+ * refused and counted. One thread per sequence. */
+__global__ void aotx_request_kernel(const unsigned int *offset, const unsigned int *agent,
+                                    unsigned int seqs, aotx_kvl_shape shape, aotx_state *state)
+{
+    unsigned int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= seqs) return;
+    unsigned int a = agent[s];
+    aotx_kv_table *kv = &state->kv;
+    if (a >= AOTX_SLOTS) return;
+    unsigned int end = state->seen[a] + (offset[s + 1u] - offset[s]);
+    unsigned int need = aotx_kvl_pages(shape, end);
+    unsigned int held = kv->count[a];
+    if (need <= held) return;
+    unsigned int pages = need - held;
+    if (pages > AOTX_KV_PAGES_EACH) {
+        atomicAdd(&kv->refused, 1u);
+        return;
+    }
+    unsigned int at = atomicAdd(&kv->made, 0u);
+    for (;;) {
+        if (at - atomicAdd(&kv->served, 0u) >= AOTX_KV_QUEUE_MAX) {
+            atomicAdd(&kv->refused, 1u);
+            return;
+        }
+        unsigned int was = atomicCAS(&kv->made, at, at + 1u);
+        if (was == at) break;
+        at = was;
+    }
+    kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].agent = a;
+    kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].pages = pages;
+}
+
+/* Embedding rows into the residual stream (fp32(scale) * q: cuda/model/gather.cu:53-80 with
+ * the Q8_0 reader of cuda/model/blocks.cuh:99-105), then the first layer's norm into x. */
+__global__ __launch_bounds__(256) void aotx_gather_kernel(const aotx_step *step,
+                                                         const unsigned char *table,
+                                                         unsigned int embd_type,
+                                                         unsigned int hidden, unsigned int vocab,
+                                                         float *resid, unsigned short *x,
+                                                         const float *norm_w, float eps)
+{
+    __shared__ float share[4];
+    const aotx_model_run *run = &step->run;
+    unsigned int t = blockIdx.x;
+    if (t >= run->tokens) return;
+    int id = run->ids[t];
+    unsigned int row = (id < 0 || (unsigned int)id >= vocab) ? 0u : (unsigned int)id;
+    float *r = resid + (unsigned long long)t * hidden;
+    float sum = 0.0f;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
+        float v;
+        if (embd_type == AOTX_WEIGHT_Q8_0) {
+            const unsigned char *blk = table + ((unsigned long long)row * (hidden / 32u) + d / 32u) * 34ull;
+            float scale = aotx_h2f((unsigned short)(blk[0] | (blk[1] << 8)));
+            v = scale * (float)(int)(signed char)blk[2u + d % 32u];
+        } else if (embd_type == AOTX_WEIGHT_F16) {
+            v = aotx_h2f(((const unsigned short *)table)[(unsigned long long)row * hidden + d]);
+        } else {
+            v = ((const float *)table)[(unsigned long long)row * hidden + d];
+        }
+        r[d] = v;
+        sum += v * v;
+    }
+    sum = aotx_block_sum(sum, share);
+    float scale = rsqrtf(sum / (float)hidden + eps);
+    unsigned short *xr = x + (unsigned long long)t * hidden;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
+        xr[d] = aotx_f2h(scale * r[d] * norm_w[d]);
+    }
+}
+
+/* resid += (split partials | expert sum), then x = half(rms(resid) * w) (norm.cu:49-90).
+ * Partials: [groups][splits][64][mt] tiles of a deferred product (m0 = 0).
+ * Experts: y fp32 [tokens*used][hidden], prob [tokens][experts], ids [tokens][used]; the
+ * sum rounds each product before it adds, rank by rank (experts.cu:88-95).
+ * sel (may be null): the selected rows also go to sel[row] (the head input). */
+__global__ __launch_bounds__(256) void aotx_resid_norm_kernel(aotx_resid_norm_args a)
+{
+    __shared__ float share[4];
+    unsigned int tokens = *a.m_dev;
+    unsigned int t = blockIdx.x;
+    if (t >= tokens) return;
+    const unsigned int h = a.hidden;
+    float *r = a.resid + (unsigned long long)t * h;
+    float sum = 0.0f;
+    for (unsigned int d = threadIdx.x; d < h; d += blockDim.x) {
+        float v = r[d];
+        if (a.partial != nullptr) {
+            const unsigned int grp = d >> 6, row = d & 63u;
+            const float *p = a.partial + ((unsigned long long)grp * a.splits * 64u + row) * a.mt + t;
+            float add = 0.0f;
+            for (unsigned int sp = 0; sp < a.splits; ++sp) add += p[(unsigned long long)sp * 64u * a.mt];
+            v += add;
+        }
+        if (a.expert_y != nullptr) {
+            float acc = 0.0f;
+            for (unsigned int rk = 0; rk < a.used; ++rk) {
+                unsigned int e = a.expert_ids[t * a.used + rk];
+                float p = a.expert_prob[t * a.experts + e];
+                float one = __fmul_rn(a.expert_y[((unsigned long long)t * a.used + rk) * h + d], p);
+                acc = rk == 0u ? one : __fadd_rn(acc, one);
+            }
+            v += acc;
+        }
+        r[d] = v;
+        sum += v * v;
+    }
+    if (a.norm_w == nullptr) return;
+    sum = aotx_block_sum(sum, share);
+    float scale = rsqrtf(sum / (float)h + a.eps);
+    unsigned short *xr = a.x + (unsigned long long)t * h;
+    int selected = -1;
+    if (a.sel != nullptr && a.last != nullptr && a.step != nullptr) {
+        if (a.step->run.select == AOTX_MODEL_ROWS_ALL) {
+            selected = (int)t;
+        } else {
+            const unsigned int seqs = a.step->run.seqs;
+            for (unsigned int s = 0; s < seqs; ++s) if (a.last[s] == t) { selected = (int)s; break; }
+        }
+    }
+    for (unsigned int d = threadIdx.x; d < h; d += blockDim.x) {
+        unsigned short hv = aotx_f2h(scale * r[d] * a.norm_w[d]);
+        xr[d] = hv;
+        if (selected >= 0) a.sel[(unsigned long long)selected * h + d] = hv;
+    }
+}
+
+/* Head norm (optional), rotary turn and page write of one (token, head) from fp32 q/k/v
+ * rows (cuda/model/rope.cu:128-196, :200-234); the general path for the split pair rule
+ * and the head-norm layer kind. Block = d/2 threads (at least 32). */
+__global__ void aotx_rope_kernel(aotx_rope_args a)
+{
+    __shared__ float share[4];
+    unsigned int tokens = *a.m_dev;
+    unsigned int t = blockIdx.x;
+    unsigned int head = blockIdx.y;
+    if (t >= tokens || head >= a.heads + a.kv_heads) return;
+    const unsigned int d = a.head_dim;
+    const unsigned int half_dim = d / 2u;
+    const bool is_q = head < a.heads;
+    const unsigned int kh = is_q ? 0u : head - a.heads;
+    const float *src = is_q ? a.q + (unsigned long long)t * a.ld + (unsigned long long)head * d
+                            : a.k + (unsigned long long)t * a.ld + (unsigned long long)kh * d;
+    const float *nw = is_q ? a.q_norm : a.k_norm;
+    const unsigned int position = a.pos[t];
+    float scale = 1.0f;
+    if (nw != nullptr) {
+        float sum = 0.0f;
+        for (unsigned int i = threadIdx.x; i < d; i += blockDim.x) sum += src[i] * src[i];
+        sum = aotx_block_sum(sum, share);
+        scale = rsqrtf(sum / (float)d + a.eps);
+    }
+    unsigned short *dst;
+    if (is_q) {
+        dst = a.qh + ((unsigned long long)t * a.heads + head) * d;
+    } else {
+        unsigned char *blk = aotx_kvl_block(a.shape, &a.state->kv, a.agent[t], a.layer, position);
+        if (blk == nullptr) {
+            if (threadIdx.x == 0u) atomicAdd(&a.state->faults, 1u);
+            return;
+        }
+        unsigned short *vrow = (unsigned short *)blk
+            + (unsigned long long)((a.kv_heads + kh) * AOTX_KVL_BLOCK + position % AOTX_KVL_BLOCK) * d;
+        const float *vsrc = a.v + (unsigned long long)t * a.ld + (unsigned long long)kh * d;
+        for (unsigned int i = threadIdx.x; i < d; i += blockDim.x) vrow[i] = aotx_f2h(vsrc[i]);
+        dst = (unsigned short *)blk
+            + (unsigned long long)(kh * AOTX_KVL_BLOCK + position % AOTX_KVL_BLOCK) * d;
+    }
+    const float step = powf(a.theta, -2.0f / (float)d);
+    for (unsigned int i = threadIdx.x; i < half_dim; i += blockDim.x) {
+        unsigned int lo = a.pairs == AOTX_ROPE_PAIRS_ADJACENT ? 2u * i : i;
+        unsigned int hi = a.pairs == AOTX_ROPE_PAIRS_ADJACENT ? 2u * i + 1u : i + half_dim;
+        float x0 = src[lo], x1 = src[hi];
+        if (nw != nullptr) {
+            x0 = scale * x0 * nw[lo];
+            x1 = scale * x1 * nw[hi];
+        }
+        float angle = (float)position * powf(step, (float)i);
+        if (a.factor != nullptr) angle = angle / a.factor[i];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        dst[lo] = aotx_f2h(x0 * cs - x1 * sn);
+        dst[hi] = aotx_f2h(x0 * sn + x1 * cs);
+    }
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Host launchers
+ * ------------------------------------------------------------------------------------- */
+void aotx_launch_rows(const aotx_step *step, unsigned int max_tokens, unsigned int *pos,
+                      unsigned int *tagent, unsigned int *last, hipStream_t s)
+{
+    unsigned int n = max_tokens > AOTX_SLOTS ? max_tokens : AOTX_SLOTS;
+    hipLaunchKernelGGL(aotx_rows_kernel, dim3((n + 255u) / 256u), dim3(256), 0, s, step,
+                       aotx_state_device(), pos, tagent, last);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_shut_rows(const aotx_step *step, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_shut_rows_kernel, dim3(1), dim3(AOTX_SLOTS), 0, s, step,
+                       aotx_state_device());
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_request(const unsigned int *offset, const unsigned int *agent,
+                         unsigned int seqs, aotx_kvl_shape shape, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_request_kernel, dim3(1), dim3(AOTX_SLOTS), 0, s, offset, agent, seqs,
+                       shape, aotx_state_device());
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_gather(const aotx_step *step, unsigned int max_tokens,
+                        const unsigned char *table, unsigned int embd_type,
+                        unsigned int hidden, unsigned int vocab, float *resid,
+                        unsigned short *x, const float *norm_w, float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_gather_kernel, dim3(max_tokens), dim3(256), 0, s, step, table,
+                       embd_type, hidden, vocab, resid, x, norm_w, eps);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_resid_norm(const aotx_resid_norm_args &a, unsigned int max_tokens, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_resid_norm_kernel, dim3(max_tokens), dim3(256), 0, s, a);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_rope(const aotx_rope_args &a, unsigned int max_tokens, hipStream_t s)
+{
+    unsigned int threads = a.head_dim / 2u;
+    if (threads < 64u) threads = 64u;
+    hipLaunchKernelGGL(aotx_rope_kernel, dim3(max_tokens, a.heads + a.kv_heads), dim3(threads), 0,
+                       s, a);
+    AOTX_LAUNCH_CHECK();
+}

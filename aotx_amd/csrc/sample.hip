@@ -1,0 +1,363 @@
+/* Sampler and Philox stream.
+ *
+ * Reference: aotx_model_pick (cuda/model/sample.cu:456-765) and the Philox4x32-10 stream
+ * (cuda/rng/rng.cuh:29-94). One block of 256 threads takes one row of logits. The steps,
+ * their order and every float expression follow the reference so that the same logits
+ * give the same token: the largest logit (ties to the lowest thread = token mod 256, then
+ * the lowest token), a temperature of zero returns it; otherwise the row sum of
+ * exp(v - top), a two-pass 256-bucket search over the 42 below the top for a cut that
+ * keeps at most 256 candidates, the candidates sorted largest first, then top-k, min-p,
+ * top-p on the T = 1 probabilities, the temperature, and the inverse CDF at the Philox
+ * uniform of (seed, slot, lane 0, draw position). Every sum runs in the reference's
+ * order: thread t adds tokens t, t + 256, ..., then thread 0 adds the 256 partials in
+ * thread order. One deliberate difference: where the reference leaves a choice to timing
+ * (which candidates fill the 256 places when more pass the cut; the order of equal values
+ * after its bitonic network), this kernel takes the lowest token ids, so the result is a
+ * function of the logits alone.
+ *
+ * The penalties, voice bias and thinking masks of aotx_pick_value (sample.cu:277-319)
+ * read the decode runtime's sequence table, which is outside this path; with a null
+ * per-row `how` (the aotx_model_sample case) the reference leaves the logit unchanged
+ * and so does this kernel.
+ */
+#include "aotx_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#define PICK_THREADS 256u
+#define PICK_BUCKETS 256u
+#define PICK_PASSES 2u
+
+#pragma clang fp contract(off)
+
+struct aotx_u32x4 {
+    unsigned int x, y, z, w;
+};
+
+static __device__ __forceinline__ aotx_u32x4 aotx_philox_dev(unsigned int c0, unsigned int c1,
+                                                             unsigned int c2, unsigned int c3,
+                                                             unsigned int k0, unsigned int k1)
+{
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r != 0) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        unsigned int lo0 = 0xD2511F53u * c0;
+        unsigned int hi0 = __umulhi(0xD2511F53u, c0);
+        unsigned int lo1 = 0xCD9E8D57u * c2;
+        unsigned int hi1 = __umulhi(0xCD9E8D57u, c2);
+        unsigned int n0 = hi1 ^ c1 ^ k0;
+        unsigned int n2 = hi0 ^ c3 ^ k1;
+        c0 = n0;
+        c1 = lo1;
+        c2 = n2;
+        c3 = lo0;
+    }
+    aotx_u32x4 out = {c0, c1, c2, c3};
+    return out;
+}
+
+__global__ void aotx_philox_kernel(const unsigned int *ctr, const unsigned int *key,
+                                   unsigned int n, unsigned int *out)
+{
+    unsigned int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    aotx_u32x4 w = aotx_philox_dev(ctr[4 * i], ctr[4 * i + 1], ctr[4 * i + 2], ctr[4 * i + 3],
+                                   key[2 * i], key[2 * i + 1]);
+    out[4 * i] = w.x;
+    out[4 * i + 1] = w.y;
+    out[4 * i + 2] = w.z;
+    out[4 * i + 3] = w.w;
+}
+
+struct aotx_pick_args {
+    const float *logits;          /* [rows][ld] */
+    unsigned int ld;
+    unsigned int vocab;
+    const unsigned int *rows_dev; /* device row count, or null */
+    unsigned int rows;
+    const unsigned int *agent;    /* [rows] */
+    const aotx_model_how *how;    /* per-row settings, or null */
+    unsigned int top_k;
+    float top_p;
+    float temperature;
+    unsigned long long seed;
+    int *token;
+    unsigned int *draw;
+    aotx_state *state;
+    const aotx_model_run *run;    /* when set, every per-call value comes from here */
+};
+
+__global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args a)
+{
+    __shared__ float part[PICK_THREADS];
+    __shared__ unsigned int mark[PICK_THREADS];
+    __shared__ unsigned int bucket[PICK_BUCKETS];
+    __shared__ float value[AOTX_MODEL_PICK_MAX];
+    __shared__ unsigned int index[AOTX_MODEL_PICK_MAX];
+    __shared__ float s_top, s_sum, s_cut, s_lo, s_hi;
+    __shared__ unsigned int s_more, s_count, s_position;
+
+    const unsigned int tid = threadIdx.x;
+    const unsigned int r = blockIdx.x;
+    const aotx_model_run *run = a.run;
+    unsigned int rows = run ? run->rows : (a.rows_dev ? *a.rows_dev : a.rows);
+    int *token_out = run ? run->token : a.token;
+    unsigned int *draw_out = run ? run->draw : a.draw;
+    if (r >= rows || token_out == nullptr) return;
+    if (run && run->select != AOTX_MODEL_ROWS_LAST) return;
+    const float *row = a.logits + (unsigned long long)r * a.ld;
+    const unsigned int vocab = a.vocab;
+    unsigned int agent = run ? run->agent[r] : a.agent[r];
+    if (agent >= AOTX_SLOTS) agent = 0u;
+
+    const aotx_model_how *how = run ? run->how : a.how;
+    unsigned int want_k = run ? run->top_k : a.top_k;
+    float want_p = run ? run->top_p : a.top_p;
+    float warmth = run ? run->temperature : a.temperature;
+    unsigned long long stream = run ? run->seed : a.seed;
+    float min_p = 0.0f;
+    if (how != nullptr) {
+        want_k = how[r].top_k;
+        want_p = how[r].top_p;
+        warmth = how[r].temperature;
+        stream = how[r].seed;
+        min_p = how[r].min_p;
+    }
+
+    /* largest logit and its place */
+    float best = -INFINITY;
+    unsigned int at = 0u;
+    for (unsigned int i = tid; i < vocab; i += PICK_THREADS) {
+        float one = row[i];
+        if (one > best) {
+            best = one;
+            at = i;
+        }
+    }
+    part[tid] = best;
+    mark[tid] = at;
+    __syncthreads();
+    if (tid == 0u) {
+        for (unsigned int i = 1u; i < PICK_THREADS; ++i) {
+            if (part[i] > part[0]) {
+                part[0] = part[i];
+                mark[0] = mark[i];
+            }
+        }
+        s_top = part[0];
+        s_position = atomicAdd(&a.state->draw[agent], 1u);
+        if (draw_out != nullptr) draw_out[r] = s_position;
+    }
+    __syncthreads();
+    const float top = s_top;
+    const unsigned int position = s_position;
+    if (warmth <= 0.0f) {
+        if (tid == 0u) token_out[r] = (int)mark[0];
+        return;
+    }
+
+    /* bucket search for the cut */
+    float lo = -AOTX_MODEL_PICK_SPAN;
+    float hi = 0.0f;
+    for (unsigned int pass = 0u; pass < PICK_PASSES; ++pass) {
+        for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS) bucket[i] = 0u;
+        __syncthreads();
+        float band = hi - lo;
+        float row_total = 0.0f;
+        for (unsigned int i = tid; i < vocab; i += PICK_THREADS) {
+            float scaled = row[i] - top;
+            if (pass == 0u) row_total += expf(scaled);
+            if (scaled >= lo && scaled <= hi) {
+                unsigned int b = (unsigned int)((scaled - lo) * (float)PICK_BUCKETS / band);
+                if (b >= PICK_BUCKETS) b = PICK_BUCKETS - 1u;
+                atomicAdd(&bucket[b], 1u);
+            }
+        }
+        part[tid] = row_total;
+        __syncthreads();
+        if (tid == 0u) {
+            if (pass == 0u) {
+                float sum = 0.0f;
+                for (unsigned int i = 0u; i < PICK_THREADS; ++i) sum += part[i];
+                s_sum = sum;
+            }
+            unsigned int held = 0u;
+            s_more = 0u;
+            s_cut = lo;
+            for (unsigned int b = PICK_BUCKETS; b != 0u; --b) {
+                if (held + bucket[b - 1u] > AOTX_MODEL_PICK_MAX) {
+                    s_cut = lo + band * (float)b / (float)PICK_BUCKETS;
+                    if (held == 0u) {
+                        s_more = 1u;
+                        s_lo = lo + band * (float)(b - 1u) / (float)PICK_BUCKETS;
+                        s_hi = s_cut;
+                    }
+                    break;
+                }
+                held += bucket[b - 1u];
+            }
+        }
+        __syncthreads();
+        if (s_more == 0u) break;
+        lo = s_lo;
+        hi = s_hi;
+        __syncthreads();
+    }
+
+    /* candidates at or above the cut: each thread counts those of its contiguous run of
+     * tokens, and a prefix over the threads places them in token order. */
+    const float cut = s_cut;
+    const unsigned int per = (vocab + PICK_THREADS - 1u) / PICK_THREADS;
+    const unsigned int first = tid * per;
+    const unsigned int after = first + per < vocab ? first + per : vocab;
+    unsigned int mine = 0u;
+    for (unsigned int i = first; i < after; ++i) {
+        if (row[i] - top >= cut) mine += 1u;
+    }
+    mark[tid] = mine;
+    __syncthreads();
+    if (tid == 0u) {
+        unsigned int run = 0u;
+        for (unsigned int i = 0u; i < PICK_THREADS; ++i) {
+            unsigned int c = mark[i];
+            mark[i] = run;
+            run += c;
+        }
+        s_count = run;
+    }
+    __syncthreads();
+    /* Place the candidates in token order; when more than 256 pass the cut (logits equal
+     * to within the finest band, where the reference keeps whichever arrive first), the
+     * 256 lowest token ids are kept. The list is then sorted by value. */
+    unsigned int count = s_count;
+    {
+        unsigned int slot = mark[tid];
+        for (unsigned int i = first; i < after; ++i) {
+            float scaled = row[i] - top;
+            if (scaled >= cut) {
+                if (slot < AOTX_MODEL_PICK_MAX) {
+                    value[slot] = scaled;
+                    index[slot] = i;
+                }
+                slot += 1u;
+            }
+        }
+    }
+    if (count > AOTX_MODEL_PICK_MAX) count = AOTX_MODEL_PICK_MAX;
+    for (unsigned int i = tid; i < AOTX_MODEL_PICK_MAX; i += PICK_THREADS) {
+        if (i >= count) {
+            value[i] = -INFINITY;
+            index[i] = 0xFFFFFFFFu;
+        }
+    }
+    __syncthreads();
+
+    /* bitonic sort, largest first, ties to the lower id */
+    for (unsigned int span = 2u; span <= AOTX_MODEL_PICK_MAX; span <<= 1) {
+        for (unsigned int step = span >> 1; step != 0u; step >>= 1) {
+            unsigned int i = tid;
+            unsigned int other = i ^ step;
+            if (other > i && i < AOTX_MODEL_PICK_MAX) {
+                bool down = (i & span) == 0u;
+                float vi = value[i], vo = value[other];
+                unsigned int ii = index[i], io = index[other];
+                bool o_first = vo > vi || (vo == vi && io < ii);  /* other ranks ahead */
+                bool i_first = vi > vo || (vi == vo && ii < io);
+                bool swap = down ? o_first : i_first;
+                if (swap) {
+                    value[i] = vo;
+                    index[i] = io;
+                    value[other] = vi;
+                    index[other] = ii;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (tid != 0u) return;
+
+    unsigned int keep = (want_k == 0u || want_k > count) ? count : want_k;
+    if (min_p > 0.0f && min_p <= 1.0f) {
+        unsigned int min_keep = 1u;
+        for (unsigned int i = 1u; i < keep; ++i) {
+            if (expf(value[i] - value[0]) < min_p) break;
+            min_keep = i + 1u;
+        }
+        keep = min_keep;
+    }
+    float limit = (want_p <= 0.0f || want_p > 1.0f) ? 1.0f : want_p;
+    float mass = 0.0f;
+    unsigned int taken = 0u;
+    for (unsigned int i = 0u; i < keep; ++i) {
+        mass += expf(value[i]) / s_sum;
+        taken = i + 1u;
+        if (mass >= limit) break;
+    }
+    float heat = warmth;
+    float heat_total = 0.0f;
+    for (unsigned int i = 0u; i < taken; ++i) heat_total += expf((value[i] - value[0]) / heat);
+    aotx_u32x4 word = aotx_philox_dev(position, 0u, 0u, agent, (unsigned int)stream,
+                                      (unsigned int)(stream >> 32));
+    float pick = (float)(word.x >> 8) * (1.0f / 16777216.0f) * heat_total;
+    float walk = 0.0f;
+    unsigned int chosen = index[0];
+    for (unsigned int i = 0u; i < taken; ++i) {
+        walk += expf((value[i] - value[0]) / heat);
+        chosen = index[i];
+        if (walk >= pick) break;
+    }
+    token_out[r] = (int)chosen;
+}
+
+void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
+                      const unsigned int *rows_dev, unsigned int rows,
+                      const unsigned int *agent, const aotx_model_how *how,
+                      unsigned int top_k, float top_p, float temperature,
+                      unsigned long long seed, int *token, unsigned int *draw,
+                      const aotx_model_run *run, hipStream_t s)
+{
+    aotx_pick_args a;
+    a.logits = logits;
+    a.ld = ld;
+    a.vocab = vocab;
+    a.rows_dev = rows_dev;
+    a.rows = rows;
+    a.agent = agent;
+    a.how = how;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.temperature = temperature;
+    a.seed = seed;
+    a.token = token;
+    a.draw = draw;
+    a.state = aotx_state_device();
+    a.run = run;
+    hipLaunchKernelGGL(aotx_pick_kernel, dim3(rows), dim3(PICK_THREADS), 0, s, a);
+    AOTX_LAUNCH_CHECK();
+}
+
+extern "C" int aotx_pick(const float *logits, unsigned int rows, unsigned int vocab,
+                         const unsigned int *agent, const aotx_model_how *how,
+                         unsigned int top_k, float top_p, float temperature,
+                         unsigned long long seed, int *token, unsigned int *draw, void *stream)
+{
+    if (logits == nullptr || agent == nullptr || token == nullptr || rows == 0u || vocab == 0u)
+        return 1;
+    aotx_launch_pick(logits, vocab, vocab, nullptr, rows, agent, how, top_k, top_p,
+                     temperature, seed, token, draw, nullptr, aotx_stream(stream));
+    return 0;
+}
+
+extern "C" int aotx_philox(const unsigned int *ctr, const unsigned int *key, unsigned int n,
+                           unsigned int *out, void *stream)
+{
+    if (ctr == nullptr || key == nullptr || out == nullptr) return 1;
+    if (n == 0u) return 0;
+    hipLaunchKernelGGL(aotx_philox_kernel, dim3((n + 255u) / 256u), dim3(256), 0,
+                       aotx_stream(stream), ctr, key, n, out);
+    AOTX_LAUNCH_CHECK();
+    return 0;
+}

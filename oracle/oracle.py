@@ -1,0 +1,147 @@
+"""ctypes wrapper of the CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module,
+and only as the checker / the CPU baseline; the product never does.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u32, u64, f32, i32 = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64,
+                                  ctypes.c_float, ctypes.c_int)
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f32_to_f16.argtypes = [f32]
+        L.orc_f16_to_f32.restype = f32
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_q8_gemv_f64.argtypes = [vp, u32, u32, vp, u32, vp, i32]
+        L.orc_q8_gemv_f32.argtypes = [vp, u32, u32, vp, u32, vp, u32]
+        L.orc_philox.argtypes = [vp, vp, vp]
+        L.orc_rng_unit.restype = f32
+        L.orc_rng_unit.argtypes = [u64, u32, u32, u64]
+        L.orc_pick.restype = i32
+        L.orc_pick.argtypes = [vp, u32, u32, f32, f32, f32, u64, u32, u64, vp, vp, vp]
+        L.orc_route.argtypes = [vp, vp, u32, u32, u32, u32, vp, vp]
+        L.orc_attend_one.argtypes = [vp, vp, vp, u32, u32, u32, vp]
+        L.orc_model_new.restype = vp
+        L.orc_model_new.argtypes = [vp, vp, u32, u32, u32]
+        L.orc_model_free.argtypes = [vp]
+        L.orc_model_forget.argtypes = [vp]
+        L.orc_model_step.restype = i32
+        L.orc_model_step.argtypes = [vp, vp, vp, u32, vp, vp]
+        L.orc_model_last_xnorm.restype = ctypes.POINTER(f32)
+        L.orc_model_last_xnorm.argtypes = [vp]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def q8_gemv_f64(w, n, k, x16, swap=False):
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    m = x16.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    lib().orc_q8_gemv_f64(_p(w), n, k, _p(x16), m, _p(y), 1 if swap else 0)
+    return y
+
+
+def q8_gemv_f32(w, n, k, x16, threads=1):
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    m = x16.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    lib().orc_q8_gemv_f32(_p(w), n, k, _p(x16), m, _p(y), threads)
+    return y
+
+
+def philox(ctr, key):
+    c = np.ascontiguousarray(ctr, dtype=np.uint32)
+    k = np.ascontiguousarray(key, dtype=np.uint32)
+    out = np.empty(4, dtype=np.uint32)
+    lib().orc_philox(_p(c), _p(k), _p(out))
+    return out
+
+
+def pick(row, top_k=0, top_p=1.0, min_p=0.0, temperature=0.0, seed=0, agent=0, position=0):
+    row = np.ascontiguousarray(row, dtype=np.float32)
+    count = ctypes.c_uint32()
+    taken = ctypes.c_uint32()
+    allowed = np.zeros(256, dtype=np.uint32)
+    tok = lib().orc_pick(_p(row), row.size, top_k, top_p, min_p, temperature, seed, agent,
+                         position, ctypes.byref(count), ctypes.byref(taken), _p(allowed))
+    return tok, count.value, allowed[:taken.value].copy()
+
+
+def route(router, x16, experts, used):
+    router = np.ascontiguousarray(router, dtype=np.float32)
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    tokens, hidden = x16.shape
+    prob = np.empty((tokens, experts), dtype=np.float32)
+    ids = np.empty((tokens, used), dtype=np.uint32)
+    lib().orc_route(_p(router), _p(x16), tokens, hidden, experts, used, _p(prob), _p(ids))
+    return prob, ids
+
+
+def attend_one(q, keys, values, last):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    keys = np.ascontiguousarray(keys, dtype=np.float32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    d = q.size
+    out = np.empty(d, dtype=np.float32)
+    lib().orc_attend_one(_p(q), _p(keys), _p(values), keys.shape[1], last, d, _p(out))
+    return out
+
+
+class Model:
+    """The oracle's whole-model forward over the same descriptor and weight bytes."""
+
+    def __init__(self, desc, weights, slots, max_context, threads=1):
+        self.desc = desc
+        self.weights = np.ascontiguousarray(weights, dtype=np.uint8)
+        self.vocab = desc.vocab
+        self.hidden = desc.hidden
+        self.h = lib().orc_model_new(ctypes.byref(desc), _p(self.weights), slots,
+                                     max_context, threads)
+
+    def step(self, ids, offset, agent):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        offset = np.ascontiguousarray(offset, dtype=np.uint32)
+        agent = np.ascontiguousarray(agent, dtype=np.uint32)
+        seqs = agent.size
+        logits = np.empty((seqs, self.vocab), dtype=np.float32)
+        rc = lib().orc_model_step(self.h, _p(ids), _p(offset), seqs, _p(agent), _p(logits))
+        if rc != 0:
+            raise RuntimeError("oracle step refused (slot or context overflow)")
+        return logits
+
+    def last_xnorm(self, seqs):
+        p = lib().orc_model_last_xnorm(self.h)
+        return np.ctypeslib.as_array(p, shape=(seqs * self.hidden,)).reshape(seqs, self.hidden).copy()
+
+    def forget(self):
+        lib().orc_model_forget(self.h)
+
+    def __del__(self):
+        try:
+            lib().orc_model_free(self.h)
+        except Exception:
+            pass

@@ -1,0 +1,134 @@
+"""Paged decode attention on the GPU vs the oracle's online-softmax attention
+(cuda/model/attention.cu:22-154), over pages the pool hands out by the reference's policy,
+with ragged contexts, grouped-query heads and a missing page."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import aotx_amd
+from oracle.kvpolicy import KvPolicy, layout_pages
+from tests.gpu_util import dev, p
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+def _open_pool(lib, pages):
+    m = aotx_amd.KvMap()
+    m.limit = pages
+    assert lib.aotx_kv_open(ctypes.byref(m)) == 0
+    return m
+
+
+def _fill(torch, lib, slots, contexts, layers, layer, kvh, d, rng):
+    """K/V rows for every position of every slot (fp16), written through aotx_kv_write."""
+    keys, vals = {}, {}
+    for s, n in zip(slots, contexts):
+        k = rng.normal(0, 1, (n, kvh, d)).astype(np.float16)
+        v = rng.normal(0, 1, (n, kvh, d)).astype(np.float16)
+        keys[s], vals[s] = k, v
+        pos = np.arange(n, dtype=np.uint32)
+        ag = np.full(n, s, dtype=np.uint32)
+        assert lib.aotx_kv_write(p(dev(k, torch)), p(dev(v, torch)), p(dev(pos, torch)),
+                                 p(dev(ag, torch)), n, kvh, d, layer, layers, None) == 0
+    torch.cuda.synchronize()
+    return keys, vals
+
+
+@pytest.mark.parametrize("heads,kvh,d,layers,layer", [(32, 8, 128, 2, 1), (4, 4, 64, 4, 3),
+                                                      (8, 4, 128, 1, 0), (16, 2, 64, 3, 0)])
+def test_attend_vs_oracle(torch, lib, orc, heads, kvh, d, layers, layer):
+    rng = np.random.default_rng(heads * 7 + d)
+    slots = [3, 0, 17, 9]
+    contexts = [1, 17, 300, 1200]
+    pool = 256
+    m = _open_pool(lib, pool)
+    try:
+        policy = KvPolicy(pool)
+        for s, n in zip(slots, contexts):
+            need = layout_pages(n, layers, kvh, d)
+            assert lib.aotx_kv_request(s, need) == 1
+            policy.request(s, need)
+        assert lib.aotx_kv_serve(ctypes.byref(m), None) == len(slots)
+        policy.serve()
+        table = aotx_amd.KvTable()
+        lib.aotx_kv_table_read(ctypes.byref(table))
+        for s in slots:   # page-table decisions bit-exact vs the reference policy
+            got = [(table.page[s][i] - m.range) // aotx_amd.AOTX_KV_PAGE_BYTES for i in range(table.count[s])]
+            assert got == policy.page[s]
+        keys, vals = _fill(torch, lib, slots, contexts, layers, layer, kvh, d, rng)
+        # queries: the last position of each slot, plus a middle position of the longest
+        qs = [(s, n - 1) for s, n in zip(slots, contexts)] + [(9, 555)]
+        q = rng.normal(0, 1, (len(qs), heads, d)).astype(np.float16)
+        pos = np.array([x[1] for x in qs], dtype=np.uint32)
+        ag = np.array([x[0] for x in qs], dtype=np.uint32)
+        out = torch.zeros(len(qs) * heads * d, dtype=torch.float16, device="cuda")
+        assert lib.aotx_attend_paged(p(dev(q, torch)), p(dev(pos, torch)), p(dev(ag, torch)), len(qs),
+                                     heads, kvh, d, layer, layers, p(out), None) == 0
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(len(qs), heads, d).astype(np.float32)
+        g = heads // kvh
+        for i, (s, last) in enumerate(qs):
+            for hh in range(heads):
+                kk = keys[s][:, hh // g, :].astype(np.float32)
+                vv = vals[s][:, hh // g, :].astype(np.float32)
+                want = orc.attend_one(q[i, hh].astype(np.float32), kk, vv, last)
+                err = np.abs(got[i, hh] - want).max()
+                assert err < 4e-3, (i, hh, err)
+        assert lib.aotx_model_faulted() == 0
+    finally:
+        lib.aotx_kv_close(ctypes.byref(m))
+
+
+def test_attend_missing_page_counts_fault(torch, lib):
+    m = _open_pool(lib, 8)
+    try:
+        lib.aotx_model_forget()
+        q = np.zeros((1, 4, 64), dtype=np.float16)
+        pos = np.array([40], dtype=np.uint32)
+        ag = np.array([5], dtype=np.uint32)          # slot 5 holds no page
+        out = torch.zeros(4 * 64, dtype=torch.float16, device="cuda")
+        assert lib.aotx_attend_paged(p(dev(q, torch)), p(dev(pos, torch)), p(dev(ag, torch)), 1, 4, 4,
+                                     64, 0, 1, p(out), None) == 0
+        torch.cuda.synchronize()
+        assert lib.aotx_model_faulted() > 0
+        lib.aotx_model_forget()
+        assert lib.aotx_model_faulted() == 0
+    finally:
+        lib.aotx_kv_close(ctypes.byref(m))
+
+
+def test_kv_release_and_reuse(torch, lib):
+    """Release gives every page back; the next request takes them LIFO (kv_host.cu:60-74)."""
+    m = _open_pool(lib, 16)
+    try:
+        policy = KvPolicy(16)
+        for s, n in ((1, 3), (2, 2)):
+            lib.aotx_kv_request(s, n)
+            policy.request(s, n)
+        lib.aotx_kv_serve(ctypes.byref(m), None)
+        policy.serve()
+        lib.aotx_kv_release(1)
+        policy.release(1)
+        lib.aotx_kv_request(4, 4)
+        policy.request(4, 4)
+        lib.aotx_kv_serve(ctypes.byref(m), None)
+        policy.serve()
+        t = aotx_amd.KvTable()
+        lib.aotx_kv_table_read(ctypes.byref(t))
+        for s in (1, 2, 4):
+            got = [(t.page[s][i] - m.range) // aotx_amd.AOTX_KV_PAGE_BYTES for i in range(t.count[s])]
+            assert got == policy.page.get(s, [])
+        assert t.mapped_pages == 6
+        # every mapped page carries the fp16 header
+        hdr = torch.zeros(16, dtype=torch.uint8, device="cuda")
+        import ctypes as C
+        assert t.page[4][0] != 0
+    finally:
+        lib.aotx_kv_close(ctypes.byref(m))

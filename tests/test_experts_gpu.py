@@ -1,0 +1,71 @@
+"""Routed experts on the GPU vs the oracle: router probabilities (tolerance 2e-6, as
+tests/expert_test.cu:118-152) and ids bit-exact; the grouped expert FFN vs a per-token
+oracle product with the ordered weighted sum (cuda/model/experts.cu:77-98)."""
+import numpy as np
+import pytest
+
+from aotx_amd.model import quantize_q8, normal
+from tests.gpu_util import dev, p, rel_rms
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+@pytest.mark.parametrize("experts,used,tokens", [(8, 2, 64), (1, 1, 3), (3, 1, 7), (7, 7, 5), (64, 8, 33)])
+def test_route_vs_oracle(torch, lib, orc, experts, used, tokens):
+    rng = np.random.default_rng(experts * 13 + tokens)
+    hidden = 512
+    router = rng.normal(0, 0.05, (experts, hidden)).astype(np.float32)
+    x = rng.normal(0, 1, (tokens, hidden)).astype(np.float16)
+    prob = torch.zeros(tokens * experts, dtype=torch.float32, device="cuda")
+    ids = torch.zeros(tokens * used, dtype=torch.int32, device="cuda")
+    assert lib.aotx_expert_route(p(dev(router, torch)), p(dev(x, torch)), tokens, hidden, experts,
+                                 used, p(prob), p(ids), None) == 0
+    torch.cuda.synchronize()
+    want_p, want_ids = orc.route(router, x.view(np.uint16), experts, used)
+    got_p = prob.cpu().numpy().reshape(tokens, experts)
+    assert np.abs(got_p - want_p).max() < 2e-6
+    assert np.array_equal(ids.cpu().numpy().reshape(tokens, used).astype(np.uint32), want_ids)
+
+
+def _ffn_oracle(orc, gate, up, down, E, H, F, x, prob, ids):
+    tokens, used = ids.shape
+    out = np.zeros((tokens, H), dtype=np.float32)
+    gs = F * (H // 32) * 34
+    ds = H * (F // 32) * 34
+    for t in range(tokens):
+        acc = None
+        for r in range(used):
+            e = int(ids[t, r])
+            g = orc.q8_gemv_f64(gate[e * gs:(e + 1) * gs], F, H, x[t:t + 1].view(np.uint16))[0]
+            u = orc.q8_gemv_f64(up[e * gs:(e + 1) * gs], F, H, x[t:t + 1].view(np.uint16))[0]
+            act = (g / (1 + np.exp(-g)) * u).astype(np.float16)
+            y = orc.q8_gemv_f64(down[e * ds:(e + 1) * ds], H, F, act[None].view(np.uint16))[0]
+            one = np.float32(y) * np.float32(prob[t, e])
+            acc = one if acc is None else np.float32(acc + one)
+        out[t] = acc
+    return out
+
+
+@pytest.mark.parametrize("E,used,tokens", [(8, 2, 64), (4, 2, 5), (8, 2, 1)])
+def test_expert_ffn_vs_oracle(torch, lib, orc, E, used, tokens):
+    rng = np.random.default_rng(E + tokens)
+    H, F = 256, 512
+    gate = quantize_q8(normal(1, 0, E * F * H).reshape(E * F, H) * np.float32(0.02)).reshape(-1)
+    up = quantize_q8(normal(2, 0, E * F * H).reshape(E * F, H) * np.float32(0.02)).reshape(-1)
+    down = quantize_q8(normal(3, 0, E * H * F).reshape(E * H, F) * np.float32(0.02)).reshape(-1)
+    router = rng.normal(0, 0.1, (E, H)).astype(np.float32)
+    x = rng.normal(0, 1, (tokens, H)).astype(np.float16)
+    prob, ids = orc.route(router, x.view(np.uint16), E, used)
+    out = torch.zeros(tokens * H, dtype=torch.float32, device="cuda")
+    assert lib.aotx_expert_ffn(p(dev(gate, torch)), p(dev(up, torch)), p(dev(down, torch)), E, used, H, F,
+                               p(dev(x, torch)), tokens, p(dev(prob, torch)), p(dev(ids, torch)), p(out),
+                               None) == 0
+    torch.cuda.synchronize()
+    want = _ffn_oracle(orc, gate, up, down, E, H, F, x, prob, ids)
+    assert rel_rms(out.cpu().numpy().reshape(tokens, H), want) < 1e-2

@@ -1,0 +1,227 @@
+"""The model-step operator surface on the GPU vs the oracle's whole-model forward.
+
+BASELINE config 1 (tiny Llama: 4 layers, d_model 256, 4 heads x 64, FFN 688 zero-padded to
+704, vocab 4096, eps 1e-5, theta 1e4, Q8 N(0, 0.02)): a 16-token prompt of uniform ids,
+then 32 greedy steps through aotx_model_sample. Logits within 1e-2 of max(|want|, rms),
+greedy ids equal wherever the oracle's top-2 gap exceeds twice the logit error bound
+(docs/17-accuracy.md:41), page-table decisions equal to the reference policy."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import aotx_amd
+from aotx_amd.model import TINY, Shape, Runtime, build_host
+from oracle.kvpolicy import KvPolicy, layout_pages
+from tests.gpu_util import rel_rms
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+@pytest.fixture(scope="module")
+def tiny(torch):
+    region, lay = build_host(TINY, seed=1)
+    return region, lay
+
+
+def _runtime(torch, region, lay, max_tokens=32, pages=64):
+    dev_region = torch.from_numpy(region).cuda()
+    return Runtime(dev_region, lay.desc, max_tokens=max_tokens, pool_pages=pages)
+
+
+def _gap_ok(want_row, err):
+    s = np.sort(want_row)
+    return s[-1] - s[-2] > 2 * err
+
+
+def test_tiny_prompt_then_greedy(torch, orc, tiny):
+    region, lay = tiny
+    rt = _runtime(torch, region, lay)
+    try:
+        ref = orc.Model(lay.desc, region, slots=64, max_context=64)
+        rng = np.random.default_rng(1)
+        prompt = rng.integers(0, TINY.vocab, 16).tolist()
+        tok, draw, logits = rt.step(prompt, [0, 16], [0])
+        want = ref.step(prompt, [0, 16], [0])
+        assert rel_rms(logits, want) < 1e-2
+        flips = 0
+        cur = int(tok[0])
+        assert cur == int(np.argmax(want[0])) or not _gap_ok(want[0], np.abs(logits - want).max())
+        for step in range(32):
+            tok, draw, logits = rt.step([cur], [0, 1], [0])
+            want = ref.step([cur], [0, 1], [0])
+            err = np.abs(logits - want).max()
+            assert rel_rms(logits, want) < 1e-2, step
+            if int(tok[0]) != int(np.argmax(want[0])):
+                assert not _gap_ok(want[0], err), (step, tok[0], np.argmax(want[0]))
+                flips += 1
+            assert draw[0] == step + 1
+            cur = int(np.argmax(want[0]))  # follow the oracle so a flip cannot cascade
+        assert flips <= 1
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
+def test_tiny_sample_surface_and_pages(torch, orc, tiny):
+    """aotx_model_sample (the drop-in operator) on ragged slots; page decisions vs policy."""
+    region, lay = tiny
+    rt = _runtime(torch, region, lay, pages=32)
+    try:
+        ref = orc.Model(lay.desc, region, slots=64, max_context=256)
+        policy = KvPolicy(32)
+        seen = {}
+        rng = np.random.default_rng(5)
+        slots = [7, 2, 40]
+        lens = [20, 3, 9]
+        ids = rng.integers(0, TINY.vocab, sum(lens)).tolist()
+        offset = np.concatenate([[0], np.cumsum(lens)]).tolist()
+        for s, n in zip(slots, lens):
+            need = layout_pages(n, TINY.layers, TINY.kv_heads, TINY.head_dim)
+            if need:
+                policy.request(s, need)
+            seen[s] = n
+        policy.serve()
+        tok, draw = rt.sample(ids, offset, slots)
+        want = ref.step(ids, offset, slots)
+        for i in range(3):
+            assert tok[i] == np.argmax(want[i]) or not _gap_ok(want[i], 1e-2 * np.abs(want[i]).max())
+        t = aotx_amd.KvTable()
+        rt.L.aotx_kv_table_read(ctypes.byref(t))
+        for s in slots:
+            got = [(t.page[s][i] - rt.map.range) // aotx_amd.AOTX_KV_PAGE_BYTES for i in range(t.count[s])]
+            assert got == policy.page.get(s, [])
+        # decode one step for every slot; a slot that crosses into a new page gets it
+        nxt = [int(x) for x in tok]
+        tok2, draw2 = rt.sample(nxt, [0, 1, 2, 3], slots)
+        want2 = ref.step(nxt, [0, 1, 2, 3], slots)
+        for i in range(3):
+            assert tok2[i] == np.argmax(want2[i]) or not _gap_ok(want2[i], 1e-2 * np.abs(want2[i]).max())
+        assert list(draw2) == [1, 1, 1]
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
+def test_tiny_sampling_seeded(torch, tiny):
+    """Temperature 0 equals argmax; top-k 1 equals greedy; the same seed and draw position
+    give the same token; restream replays (tests/model_test.cu:406-518)."""
+    region, lay = tiny
+    rt = _runtime(torch, region, lay)
+    try:
+        prompt = list(range(100, 116))
+        g, _, lg = rt.step(prompt, [0, 16], [0])
+        assert g[0] == np.argmax(lg[0])
+        rt.L.aotx_model_forget()
+        rt.L.aotx_model_restream()
+        k1, _, _ = rt.step(prompt, [0, 16], [0], how=aotx_amd.neutral_how(temperature=0.8, top_k=1, seed=3))
+        assert k1[0] == g[0]
+        outs = []
+        for rep in range(2):
+            rt.L.aotx_model_forget()
+            rt.L.aotx_model_restream()
+            how = aotx_amd.neutral_how(temperature=0.8, top_k=40, top_p=0.9, seed=0x5EED)
+            seq = []
+            cur = prompt
+            for step in range(6):
+                t, d, _ = rt.step(cur, [0, len(cur)], [0], how=how)
+                seq.append(int(t[0]))
+                cur = [int(t[0])]
+            outs.append(seq)
+        assert outs[0] == outs[1]
+    finally:
+        rt.close()
+
+
+def test_graph_replay_equals_eager(torch, tiny, monkeypatch):
+    """The captured graph of a bucket gives the same logits on every replay as the eager
+    launch of the same kernels, with other work and synchronisation between replays."""
+    import subprocess, sys, os, json
+    region, lay = tiny
+    code = r'''
+import sys, json, numpy as np, torch
+sys.path.insert(0, %r)
+from aotx_amd.model import TINY, Runtime, build_host
+region, lay = build_host(TINY, seed=1)
+rt = Runtime(torch.from_numpy(region).cuda(), lay.desc, max_tokens=32, pool_pages=16)
+rows = []
+for rep in range(4):
+    rt.L.aotx_model_forget()
+    t, d, lg = rt.step(list(range(50, 60)), [0, 10], [3])
+    x = torch.randn(1000, 1000, device="cuda") @ torch.randn(1000, 1000, device="cuda")
+    torch.cuda.synchronize()
+    rows.append(lg[0].tolist())
+print(json.dumps(rows))
+''' % os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    outs = []
+    for graphs in ("1", "0"):
+        env = dict(os.environ, AOTX_GRAPHS=graphs)
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        outs.append(np.array(json.loads(r.stdout.strip().splitlines()[-1])))
+    graph, eager = outs
+    for i in range(4):
+        assert np.array_equal(graph[i], eager[0])
+        assert np.array_equal(eager[i], eager[0])
+
+
+def test_qknorm_split_layer_kind(torch, orc):
+    """The head-norm layer kind with split rotary pairs (the reference's Qwen3 kind) runs
+    the general turn kernel; logits vs the oracle."""
+    shape = Shape(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1024,
+                  qk_norm=True, pairs=0)
+    region, lay = build_host(shape, seed=3)
+    rt = _runtime(torch, region, lay)
+    try:
+        ref = orc.Model(lay.desc, region, slots=8, max_context=64)
+        ids = list(range(10, 30))
+        _, _, lg = rt.step(ids, [0, 12, 20], [1, 4])
+        want = ref.step(ids, [0, 12, 20], [1, 4])
+        assert rel_rms(lg, want) < 1e-2
+        _, _, lg = rt.step([3, 4], [0, 1, 2], [1, 4])
+        want = ref.step([3, 4], [0, 1, 2], [1, 4])
+        assert rel_rms(lg, want) < 1e-2
+    finally:
+        rt.close()
+
+
+def test_moe_model_vs_oracle(torch, orc):
+    """A small routed-expert model (8 experts, top-2, reference routing rule) end to end."""
+    shape = Shape(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1024,
+                  experts=8, used=2)
+    region, lay = build_host(shape, seed=4)
+    rt = _runtime(torch, region, lay, max_tokens=64)
+    try:
+        ref = orc.Model(lay.desc, region, slots=8, max_context=64)
+        ids = list(range(200, 240))
+        _, _, lg = rt.step(ids, [0, 25, 40], [0, 6])
+        want = ref.step(ids, [0, 25, 40], [0, 6])
+        assert rel_rms(lg, want) < 1e-2
+        _, _, lg = rt.step([9, 8], [0, 1, 2], [0, 6])
+        want = ref.step([9, 8], [0, 1, 2], [0, 6])
+        assert rel_rms(lg, want) < 1e-2
+    finally:
+        rt.close()
+
+
+def test_prefill_all_rows(torch, orc, tiny):
+    """aotx_model_prefill with a logits buffer gives every token's row."""
+    region, lay = tiny
+    rt = _runtime(torch, region, lay)
+    try:
+        ids = list(range(7, 27))
+        lg = rt.prefill_logits(ids, [0, 20], [0])
+        ref = orc.Model(lay.desc, region, slots=2, max_context=64)
+        for n in (1, 7, 20):
+            r2 = orc.Model(lay.desc, region, slots=2, max_context=64)
+            want = r2.step(ids[:n], [0, n], [0])
+            assert rel_rms(lg[n - 1:n], want) < 1e-2
+    finally:
+        rt.close()
