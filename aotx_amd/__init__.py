@@ -139,6 +139,7 @@ PROTOTYPES = {
     "aotx_model_prefill": (i32, [u32, vp, vp, u32, vp, vp, vp]),
     "aotx_model_probe": (i32, [u32, vp, vp, u32, vp, vp, vp, u32, vp, vp, u32]),
     "aotx_model_buffer": (u64, [u32, u32]),
+    "aotx_model_seat": (i32, [u32, u32]),
     "aotx_kv_open": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_reserve": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_serve": (i32, [ctypes.POINTER(KvMap), vp]),

@@ -510,6 +510,15 @@ extern "C" void aotx_model_restream(void)
     AOTX_CHECK(hipDeviceSynchronize());
 }
 
+extern "C" int aotx_model_seat(unsigned int agent, unsigned int position)
+{
+    if (agent >= AOTX_SLOTS || position > AOTX_SEQ_MAX_TOKENS) return 1;
+    aotx_state *st = aotx_state_device();
+    AOTX_CHECK(hipDeviceSynchronize());
+    AOTX_CHECK(hipMemcpy(&st->seen[agent], &position, sizeof position, hipMemcpyHostToDevice));
+    return 0;
+}
+
 extern "C" unsigned int aotx_model_faulted(void)
 {
     unsigned int count = 0u;

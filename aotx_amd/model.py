@@ -114,6 +114,17 @@ MIXTRAL = Shape(layers=32, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_di
                 vocab=32000, experts=8, used=2, theta=1e6)
 
 
+def layout_pages(context, layers, kv_heads, head_dim, page_bytes=2 * 1024 * 1024, header=256,
+                 block=16):
+    """Pages one slot needs for `context` positions (cuda/model/kv_layout.cuh:94-103)."""
+    block_bytes = 2 * kv_heads * block * head_dim * 2
+    per_page = (page_bytes - header) // block_bytes
+    if per_page == 0:
+        return 0
+    blocks = ((context + block - 1) // block) * layers
+    return (blocks + per_page - 1) // per_page
+
+
 def _align(n):
     return (n + ALIGN - 1) // ALIGN * ALIGN
 

@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token loop (BASELINE.json metric: decode tokens/s at batch 1
+and 32 on the 8B-shape Q8 decoder; Q8 GEMV achieved HBM GB/s).
+
+Workload: 32 layers, d_model 4096, 32/8 heads x 128, FFN 14336
+SwiGLU, vocab 128256, untied head, every linear Q8_0 from N(0, 0.02) (synthetic weights
+generated on the GPU). 32 agent slots each seated on a 2048-token paged KV cache (the
+pages are requested through the pool, written with random fp16 keys/values, and the
+slots' cache positions set), then greedy decode steps through the drop-in operator
+surface: aotx_model_pages -> aotx_kv_serve -> aotx_model_sample, one step = one token for
+every slot. `value` is the batch-32 whole-step throughput in tokens/s; the batch-1 rate,
+the sampled (top-k 40 / top-p 0.9 / T 0.8) rate and the Q8 GEMV table ride along.
+
+`roofline` is measured on the dominant kernel, the Q8_0 product at the FFN shape
+(N=14336, K=4096) with the batch-32 activations, timed with HIP events on the stream it is
+launched on. `cpu_baseline` times the repository's C oracle (oracle/) on the host cores
+over a bounded sample of the same decode step.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_table(torch, L, shapes, ms, iters=20, warm=3):
+    """Per-launch time and achieved GB/s of the Q8_0 product (fp16 out, config 2)."""
+    import aotx_amd as A
+    out = []
+    for n, k in shapes:
+        w = torch.empty(n * (k // 32) * 34, dtype=torch.uint8, device="cuda")
+        A.check(L.aotx_synth_q8(A.ptr(w), n, k, 0.02, 7, None), "synth")
+        for m in ms:
+            x = torch.randn(m, k, device="cuda").half()
+            y = torch.empty(m, n, device="cuda", dtype=torch.float16)
+            s = A.stream_of()
+            for _ in range(warm):
+                L.aotx_q8_gemv_f16(A.ptr(w), n, k, A.ptr(x), m, A.ptr(y), s)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(iters):
+                L.aotx_q8_gemv_f16(A.ptr(w), n, k, A.ptr(x), m, A.ptr(y), s)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / iters
+            algo = n * k * 34 // 32 + m * k * 2 + m * n * 2
+            out.append({"n": n, "k": k, "m": m, "us": round(us, 2),
+                        "gbs": round(algo / us / 1e3, 1), "bytes": algo})
+        del w
+    return out
+
+
+def seat_context(torch, rt, slots, context, reserve, layers, kvh, hd):
+    """Request pages for `context + reserve` positions per slot, write random fp16 K/V for
+    positions [0, context) of every layer, and seat each slot at `context`."""
+    import aotx_amd as A
+    from aotx_amd.model import layout_pages
+    L = rt.L
+    for s in slots:
+        need = layout_pages(context + reserve, layers, kvh, hd)
+        if L.aotx_kv_request(s, need) != 1:
+            raise RuntimeError("page request refused")
+    L.aotx_kv_serve(ctypes.byref(rt.map), None)
+    n = len(slots) * context
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    k = torch.randn(n, kvh * hd, device="cuda", generator=g).half()
+    v = torch.randn(n, kvh * hd, device="cuda", generator=g).half()
+    pos = torch.arange(context, device="cuda", dtype=torch.int32).repeat(len(slots))
+    ag = torch.tensor(slots, device="cuda", dtype=torch.int32).repeat_interleave(context)
+    for layer in range(layers):
+        A.check(L.aotx_kv_write(A.ptr(k), A.ptr(v), A.ptr(pos), A.ptr(ag), n, kvh, hd, layer,
+                                layers, None), "aotx_kv_write")
+    torch.cuda.synchronize()
+    for s in slots:
+        A.check(L.aotx_model_seat(s, context), "aotx_model_seat")
+    del k, v
+
+
+def decode(torch, rt, slots, steps, warmup, how):
+    """Timed decode steps through the operator surface; returns (tokens/s, ms/step)."""
+    import aotx_amd as A
+    L = rt.L
+    B = len(slots)
+    off = torch.arange(B + 1, device="cuda", dtype=torch.int32)
+    ag = torch.tensor(slots, device="cuda", dtype=torch.int32)
+    ids = torch.randint(0, rt.desc.vocab, (B,), device="cuda", dtype=torch.int32)
+    tok = torch.zeros(B, device="cuda", dtype=torch.int32)
+    draw = torch.zeros(B, device="cuda", dtype=torch.int32)
+    seed = ctypes.c_uint64()
+
+    def one():
+        nonlocal ids, tok
+        A.check(L.aotx_model_pages(rt.role, A.ptr(off), B, A.ptr(ag)), "pages")
+        L.aotx_kv_serve(ctypes.byref(rt.map), None)
+        A.check(L.aotx_model_sample(rt.role, A.ptr(ids), A.ptr(off), B, A.ptr(ag),
+                                    ctypes.byref(how), A.ptr(tok), A.ptr(draw),
+                                    ctypes.byref(seed)), "aotx_model_sample")
+        ids, tok = tok, ids
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    if L.aotx_model_faulted() != 0:
+        raise RuntimeError("page faults during the timed decode")
+    return B * steps / dt, dt * 1000.0 / steps
+
+
+def cpu_baseline(region_dev, lay, torch, batch, context, threads):
+    """The C oracle's decode step on the host cores (a bounded sample: one step of the
+    batch on a seated context)."""
+    from oracle import oracle as orc
+    host = region_dev.cpu().numpy()
+    m = orc.Model(lay.desc, host, slots=batch, max_context=context + 2, threads=threads)
+    m.seat(list(range(batch)), context, seed=7)
+    ids = np.random.default_rng(0).integers(0, lay.desc.vocab, batch).astype(np.int32)
+    offset = np.arange(batch + 1, dtype=np.uint32)
+    agent = np.arange(batch, dtype=np.uint32)
+    t0 = time.perf_counter()
+    m.step(ids, offset, agent)
+    dt = time.perf_counter() - t0
+    return batch / dt, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--context", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the token loop's slots are independent; see the sharding note in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import aotx_amd as A
+    from aotx_amd.model import LLAMA_8B, Runtime, build_device
+    L = A.lib()
+    torch.cuda.init()
+    log("bench: device", torch.cuda.get_device_name(0))
+
+    # Q8 GEMV table (config 2) and the roofline of the dominant kernel.
+    shapes = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+    table = gemv_table(torch, L, shapes, [1, 4, 8, 32])
+    for row in table:
+        log(f"gemv n={row['n']} k={row['k']} m={row['m']}: {row['us']} us {row['gbs']} GB/s")
+    dom = next(r for r in table if r["n"] == 14336 and r["k"] == 4096 and r["m"] == args.batch) \
+        if args.batch in (1, 4, 8, 32) else None
+
+    # 8B-shape decoder, synthetic weights on the GPU.
+    shape = LLAMA_8B
+    t0 = time.perf_counter()
+    region, lay = build_device(shape, seed=0x5EED)
+    log(f"bench: weights {region.numel() / 1e9:.2f} GB built in {time.perf_counter() - t0:.1f}s")
+    reserve = args.warmup * 3 + args.steps * 3 + 8
+    from aotx_amd.model import layout_pages
+    per_slot = layout_pages(args.context + reserve, shape.layers, shape.kv_heads, shape.head_dim)
+    batch_slots = list(range(args.batch))
+    one_slot = [63]
+    rt = Runtime(region, lay.desc, max_tokens=max(32, args.batch),
+                 pool_pages=per_slot * (len(batch_slots) + 1) + 8)
+    seat_context(torch, rt, batch_slots + one_slot, args.context, reserve, shape.layers,
+                 shape.kv_heads, shape.head_dim)
+    greedy = A.neutral_how()
+    tps, ms = decode(torch, rt, batch_slots, args.steps, args.warmup, greedy)
+    log(f"bench: batch {args.batch} greedy: {tps:.1f} tokens/s, {ms:.3f} ms/step")
+    tps1, ms1 = decode(torch, rt, one_slot, args.steps, args.warmup, greedy)
+    log(f"bench: batch 1 greedy: {tps1:.1f} tokens/s, {ms1:.3f} ms/step")
+    sampled = A.neutral_how(temperature=0.8, top_k=40, top_p=0.9, seed=0x5EED)
+    tpss, mss = decode(torch, rt, batch_slots, max(4, args.steps // 2), 1, sampled)
+    log(f"bench: batch {args.batch} top-k 40/top-p 0.9/T 0.8: {tpss:.1f} tokens/s")
+
+    # algorithmic bytes of one decode step: weights + KV read/write + logits
+    wbytes = region.numel()
+    ctx_mid = args.context + args.warmup + args.steps // 2
+    kv_tok = 2 * shape.kv_heads * shape.head_dim * 2 * shape.layers
+    step_bytes = wbytes + args.batch * (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
+    step_bytes1 = wbytes + (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
+
+    result = {
+        "metric": "decode tokens/s at batch 1 & 32 (8B-shape Q8); Q8 GEMV achieved HBM GB/s",
+        "value": round(tps, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 weights (int8 x fp16 scale), fp16 activations, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) Q8_0 weights; random fp16 KV; greedy ids)",
+        "config": {"workload": "8B-shape Q8 decoder decode step, 32 slots x 2048-token paged KV",
+                   "layers": 32, "d_model": 4096, "heads": "32/8x128", "ffn": 14336,
+                   "vocab": 128256, "batch": args.batch, "context": args.context,
+                   "parallelism": "single GPU"},
+        "batch1_tokens_per_s": round(tps1, 2),
+        "batch1_ms_per_step": round(ms1, 4),
+        "sampled_tokens_per_s": round(tpss, 2),
+        "step_roofline_frac": round(step_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "step_roofline_frac_batch1": round(step_bytes1 / (ms1 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "gemv": table,
+    }
+    if dom is not None:
+        result["roofline"] = {
+            "bound": "hbm", "kernel": f"aotx_gemv_q8 n={dom['n']} k={dom['k']} m={dom['m']}",
+            "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
+    rt.close()
+
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+        cbatch = args.batch
+        cps, cdt = cpu_baseline(region, lay, torch, cbatch, args.context, threads)
+        result["cpu_baseline"] = {
+            "value": round(cps, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one oracle decode step, batch {cbatch}, context {args.context} "
+                      f"({cdt:.1f} s on {threads} threads)"}
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

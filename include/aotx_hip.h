@@ -279,6 +279,11 @@ int aotx_model_probe(unsigned int role, const int *ids, const unsigned int *offs
                      unsigned int seqs, const unsigned int *agent,
                      const aotx_model_how *how, float *logits, unsigned int select,
                      float *capture, const unsigned int *layers, unsigned int layer_count);
+/* Set one slot's cache position. No counterpart in the reference, which restores a slot
+ * by prefilling its tokens again (cuda/model/decode.cu:230-305); this is for callers that
+ * write a slot's KV pages out of band (restore from a copy, benchmarks that seat a
+ * prefilled context) and then continue decoding at `position`. Returns 1 for a bad slot. */
+int aotx_model_seat(unsigned int agent, unsigned int position);
 /* Address of a role's hidden-state rows after the last norm (half [max_tokens][hidden]),
  * for checks. */
 unsigned long long aotx_model_buffer(unsigned int role, unsigned int which);

@@ -42,6 +42,16 @@ float orc_f16_to_f32(uint16_t h)
 
 float orc_round_half(float f) { return orc_f16_to_f32(orc_f32_to_f16(f)); }
 
+static float orc_lut[65536];
+static int orc_lut_ready = 0;
+
+static void orc_lut_init(void)
+{
+    if (orc_lut_ready) return;
+    for (unsigned int i = 0; i < 65536u; ++i) orc_lut[i] = orc_f16_to_f32((uint16_t)i);
+    orc_lut_ready = 1;
+}
+
 /* ------------------------------------------------------------------------------------
  * Q8_0 (cuda/model/matrix.cuh:6-9: fp16 scale + 32 int8 in 34 bytes)
  * ---------------------------------------------------------------------------------- */
@@ -357,6 +367,31 @@ void orc_attend_one(const float *q, const float *keys, const float *values,
     for (unsigned int i = 0; i < d; ++i) out[i] = orc_round_half(sum[i] * back);
 }
 
+/* The same attention over fp16 rows as the pages hold them. */
+static void orc_attend_half(const float *q, const uint16_t *keys, const uint16_t *values,
+                            unsigned int stride, unsigned int last, unsigned int d, float *out)
+{
+    float scale = 1.0f / sqrtf((float)d);
+    float top = -INFINITY, mass = 0.0f;
+    float sum[512];
+    for (unsigned int i = 0; i < d; ++i) sum[i] = 0.0f;
+    for (unsigned int j = 0; j <= last; ++j) {
+        const uint16_t *key = keys + (size_t)j * stride;
+        float dot = 0.0f;
+        for (unsigned int i = 0; i < d; ++i) dot += q[i] * orc_lut[key[i]];
+        dot = dot * scale;
+        float raised = fmaxf(top, dot);
+        float shift = expf(top - raised);
+        float weight = expf(dot - raised);
+        const uint16_t *value = values + (size_t)j * stride;
+        for (unsigned int i = 0; i < d; ++i) sum[i] = sum[i] * shift + weight * orc_lut[value[i]];
+        mass = mass * shift + weight;
+        top = raised;
+    }
+    float back = mass > 0.0f ? 1.0f / mass : 0.0f;
+    for (unsigned int i = 0; i < d; ++i) out[i] = orc_round_half(sum[i] * back);
+}
+
 /* ------------------------------------------------------------------------------------
  * Whole model (tests/model_ref.h:301-427, generalised to the layer kinds of the path)
  * ---------------------------------------------------------------------------------- */
@@ -365,10 +400,12 @@ struct orc_model {
     const uint8_t *w;
     unsigned int slots, max_context, threads;
     unsigned int *seen;
-    float *keys;     /* [slots][layers][max_context][kv_heads*d] */
-    float *values;
+    uint16_t *keys;  /* [slots][layers][max_context][kv_heads*d], fp16 as the pages hold */
+    uint16_t *values;
     float *last_xnorm;
 };
+
+
 
 static const void *orc_tensor(const orc_model *m, unsigned long long off)
 {
@@ -387,8 +424,9 @@ orc_model *orc_model_new(const aotx_model_desc *desc, const uint8_t *weights,
     m->seen = (unsigned int *)calloc(slots, sizeof(unsigned int));
     size_t narrow = (size_t)desc->kv_heads * desc->head_dim;
     size_t cells = (size_t)slots * desc->layers * max_context * narrow;
-    m->keys = (float *)calloc(cells, sizeof(float));
-    m->values = (float *)calloc(cells, sizeof(float));
+    orc_lut_init();
+    m->keys = (uint16_t *)calloc(cells, sizeof(uint16_t));
+    m->values = (uint16_t *)calloc(cells, sizeof(uint16_t));
     m->last_xnorm = (float *)calloc((size_t)slots * desc->hidden, sizeof(float));
     return m;
 }
@@ -442,6 +480,94 @@ static void orc_rope(float *head, unsigned int dim, unsigned int position, float
         head[lo] = orc_round_half(a * c - b * s);
         head[hi] = orc_round_half(a * s + b * c);
     }
+}
+
+struct orc_attn_job {
+    const orc_model *m;
+    unsigned int l, tokens;
+    const float *q;
+    float *att;
+    const unsigned int *pos, *slot;
+    size_t slot_stride, narrow, wide;
+    unsigned int lo, hi;   /* (token, head) items of one worker */
+};
+
+static void *orc_attn_worker(void *arg)
+{
+    struct orc_attn_job *j = (struct orc_attn_job *)arg;
+    const aotx_model_desc *d = &j->m->d;
+    unsigned int hd = d->head_dim;
+    for (unsigned int it = j->lo; it < j->hi; ++it) {
+        unsigned int t = it / d->heads, hh = it % d->heads;
+        unsigned int kvh = hh / (d->heads / d->kv_heads);
+        const uint16_t *kb = j->m->keys + j->slot[t] * j->slot_stride + (size_t)j->l * j->m->max_context * j->narrow;
+        const uint16_t *vb = j->m->values + j->slot[t] * j->slot_stride + (size_t)j->l * j->m->max_context * j->narrow;
+        orc_attend_half(j->q + (size_t)t * j->wide + (size_t)hh * hd, kb + kvh * hd, vb + kvh * hd,
+                        (unsigned int)j->narrow, j->pos[t], hd, j->att + (size_t)t * j->wide + (size_t)hh * hd);
+    }
+    return NULL;
+}
+
+/* Attention of every (token, head) of one layer, over the model's threads. */
+static void orc_attn_run(struct orc_attn_job *base)
+{
+    unsigned int items = base->tokens * base->m->d.heads;
+    unsigned int threads = base->m->threads;
+    if (threads > items) threads = items;
+    if (threads <= 1u) {
+        base->lo = 0;
+        base->hi = items;
+        orc_attn_worker(base);
+        return;
+    }
+    pthread_t th[256];
+    struct orc_attn_job jobs[256];
+    if (threads > 256u) threads = 256u;
+    unsigned int per = (items + threads - 1u) / threads;
+    for (unsigned int t = 0; t < threads; ++t) {
+        jobs[t] = *base;
+        jobs[t].lo = per * t;
+        jobs[t].hi = per * (t + 1u) < items ? per * (t + 1u) : items;
+        pthread_create(&th[t], NULL, orc_attn_worker, &jobs[t]);
+    }
+    for (unsigned int t = 0; t < threads; ++t) pthread_join(th[t], NULL);
+}
+
+struct orc_seat_job { orc_model *m; unsigned int slot, position, layer; uint64_t seed; };
+
+static void *orc_seat_worker(void *arg)
+{
+    struct orc_seat_job *j = (struct orc_seat_job *)arg;
+    orc_model *m = j->m;
+    size_t narrow = (size_t)m->d.kv_heads * m->d.head_dim;
+    size_t slot_stride = (size_t)m->d.layers * m->max_context * narrow;
+    uint16_t *kb = m->keys + j->slot * slot_stride + (size_t)j->layer * m->max_context * narrow;
+    uint16_t *vb = m->values + j->slot * slot_stride + (size_t)j->layer * m->max_context * narrow;
+    uint64_t x = j->seed * 0x9E3779B97F4A7C15ull + (uint64_t)j->slot * 1000003ull + j->layer + 1ull;
+    for (size_t i = 0; i < (size_t)j->position * narrow; ++i) {
+        x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+        float u = (float)(x >> 40) * (1.0f / 16777216.0f) * 4.0f - 2.0f;
+        kb[i] = orc_f32_to_f16(u);
+        x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+        u = (float)(x >> 40) * (1.0f / 16777216.0f) * 4.0f - 2.0f;
+        vb[i] = orc_f32_to_f16(u);
+    }
+    return NULL;
+}
+
+int orc_model_seat(orc_model *m, unsigned int slot, unsigned int position, uint64_t seed)
+{
+    if (slot >= m->slots || position > m->max_context) return 1;
+    unsigned int layers = m->d.layers;
+    pthread_t th[AOTX_MODEL_MAX_LAYERS];
+    struct orc_seat_job jobs[AOTX_MODEL_MAX_LAYERS];
+    for (unsigned int l = 0; l < layers; ++l) {
+        jobs[l] = (struct orc_seat_job){ m, slot, position, l, seed };
+        pthread_create(&th[l], NULL, orc_seat_worker, &jobs[l]);
+    }
+    for (unsigned int l = 0; l < layers; ++l) pthread_join(th[l], NULL);
+    m->seen[slot] = position;
+    return 0;
 }
 
 int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
@@ -516,8 +642,8 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
                 }
                 orc_rope(head, hd, pos[t], d->rope_theta, d->rope_pairs, factor);
             }
-            float *kc = m->keys + slot[t] * slot_stride + ((size_t)l * m->max_context + pos[t]) * narrow;
-            float *vc = m->values + slot[t] * slot_stride + ((size_t)l * m->max_context + pos[t]) * narrow;
+            uint16_t *kc = m->keys + slot[t] * slot_stride + ((size_t)l * m->max_context + pos[t]) * narrow;
+            uint16_t *vc = m->values + slot[t] * slot_stride + ((size_t)l * m->max_context + pos[t]) * narrow;
             for (unsigned int hh = 0; hh < d->kv_heads; ++hh) {
                 float *head = k + (size_t)t * narrow + (size_t)hh * hd;
                 if (kn) {
@@ -530,19 +656,14 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
                 }
                 orc_rope(head, hd, pos[t], d->rope_theta, d->rope_pairs, factor);
                 for (unsigned int i = 0; i < hd; ++i) {
-                    kc[hh * hd + i] = head[i];
-                    vc[hh * hd + i] = orc_round_half(v[(size_t)t * narrow + hh * hd + i]);
+                    kc[hh * hd + i] = orc_f32_to_f16(head[i]);
+                    vc[hh * hd + i] = orc_f32_to_f16(v[(size_t)t * narrow + hh * hd + i]);
                 }
             }
         }
-        for (unsigned int t = 0; t < tokens; ++t) {
-            const float *kb = m->keys + slot[t] * slot_stride + (size_t)l * m->max_context * narrow;
-            const float *vb = m->values + slot[t] * slot_stride + (size_t)l * m->max_context * narrow;
-            for (unsigned int hh = 0; hh < d->heads; ++hh) {
-                unsigned int kvh = hh / (d->heads / d->kv_heads);
-                orc_attend_one(q + (size_t)t * wide + (size_t)hh * hd, kb + kvh * hd, vb + kvh * hd,
-                               narrow, pos[t], hd, att + (size_t)t * wide + (size_t)hh * hd);
-            }
+        {
+            struct orc_attn_job job = { m, l, tokens, q, att, pos, slot, slot_stride, narrow, wide, 0, 0 };
+            orc_attn_run(&job);
         }
         orc_matmul(m, (const uint8_t *)orc_tensor(m, L->offset[AOTX_SLOT_ATTN_O]), h, wide, att, tokens, proj);
         for (size_t i = 0; i < (size_t)tokens * h; ++i) resid[i] += proj[i];

@@ -86,6 +86,9 @@ void orc_model_forget(orc_model *m);
  * per sequence (its last token) [seqs][vocab]. Returns 0, or 1 when a slot overflows. */
 int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
                    unsigned int seqs, const unsigned int *agent, float *logits);
+/* Seat a slot at `position` with random fp16 keys/values in every layer (the CPU
+ * baseline's stand-in for a prefilled context; not a parity function). */
+int orc_model_seat(orc_model *m, unsigned int slot, unsigned int position, uint64_t seed);
 /* The xnorm (half values as float) of the last row of each sequence of the last step. */
 const float *orc_model_last_xnorm(const orc_model *m);
 

@@ -47,6 +47,8 @@ def lib():
         L.orc_model_forget.argtypes = [vp]
         L.orc_model_step.restype = i32
         L.orc_model_step.argtypes = [vp, vp, vp, u32, vp, vp]
+        L.orc_model_seat.restype = i32
+        L.orc_model_seat.argtypes = [vp, u32, u32, u64]
         L.orc_model_last_xnorm.restype = ctypes.POINTER(f32)
         L.orc_model_last_xnorm.argtypes = [vp]
         _lib = L
@@ -136,6 +138,11 @@ class Model:
     def last_xnorm(self, seqs):
         p = lib().orc_model_last_xnorm(self.h)
         return np.ctypeslib.as_array(p, shape=(seqs * self.hidden,)).reshape(seqs, self.hidden).copy()
+
+    def seat(self, slots, position, seed=7):
+        for s in slots:
+            if lib().orc_model_seat(self.h, s, position, seed) != 0:
+                raise RuntimeError("oracle seat refused")
 
     def forget(self):
         lib().orc_model_forget(self.h)
