@@ -35,28 +35,38 @@ struct aotx_attn_args {
     unsigned int kv_heads;
     unsigned int layer;
     unsigned int splits;          /* chunks per (token, KV head) at most */
-    unsigned int chunk_max;       /* LDS capacity in positions */
+    unsigned int chunk_max;       /* the largest context planned for */
     aotx_kvl_shape shape;
     aotx_state *state;
     float *partial;               /* [tokens*kv_heads][splits][G*(d+2)] */
 };
 
-#define ATTN_UNROLL 4
-#define ATTN_MIN_CHUNK 64u
+#define ATTN_UNROLL 4          /* positions per lane group per block: 32 per wave */
+#define ATTN_CHUNK_ALIGN 128u  /* a chunk is a whole number of 4-wave blocks */
+#define ATTN_MAX_SPLITS 64u
 
 static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 {
     return aotx_h2f((unsigned short)(hi ? (word >> 16) : (word & 0xFFFFu)));
 }
 
+/* One workgroup = 4 waves = one (token, KV head, context chunk). Each wave takes a
+ * quarter of the chunk in blocks of 32 positions (8 lane groups x 4), loads the key and
+ * value rows of a block together, and keeps a running maximum and mass (online softmax,
+ * as cuda/model/attention.cu:90-104, per block instead of per position). The 4 waves'
+ * (max, mass, sum) are merged in wave order through LDS; a chunk that is not the whole
+ * context leaves its merged triple for the merge kernel. */
 template <int D, int G>
-__global__ __launch_bounds__(64) void aotx_attend_kernel(aotx_attn_args a)
+__global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
 {
     constexpr int NP = D / 64;          /* 16-byte pieces per lane per row */
     constexpr int E = 8 * NP;           /* elements per lane */
-    extern __shared__ float sc[];       /* [chunk][G] scores, then exponentials */
+    constexpr int U = ATTN_UNROLL;      /* positions per lane group per block */
+    __shared__ float wm[4][G], wl[4][G];
+    __shared__ float wo[4][G][D];
 
-    const unsigned int lane = threadIdx.x;
+    const unsigned int lane = threadIdx.x & 63u;
+    const unsigned int wave = threadIdx.x >> 6;
     const unsigned int grp = lane >> 3;
     const unsigned int sub = lane & 7u;
     unsigned int tokens = a.m_dev ? *a.m_dev : a.tokens;
@@ -69,22 +79,21 @@ __global__ __launch_bounds__(64) void aotx_attend_kernel(aotx_attn_args a)
     if (t >= tokens) return;
     const unsigned int n = a.pos[t] + 1u;
     unsigned int chunk = (n + S - 1u) / S;
-    chunk = (chunk + 15u) & ~15u;
-    if (chunk < ATTN_MIN_CHUNK) chunk = ATTN_MIN_CHUNK;
-    if (chunk > a.chunk_max) {               /* a position past the planned context */
-        if (threadIdx.x == 0u && blockIdx.x % S == 0u) atomicAdd(&a.state->faults, 1u);
-        return;
-    }
+    chunk = (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
     const unsigned int st = (n + chunk - 1u) / chunk;   /* chunks of this token */
     if (c >= st) return;
     const unsigned int p0 = c * chunk;
     const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
-    const unsigned int cnt = p1 - p0;
+    /* this wave's quarter, in whole blocks of 8 * U positions */
+    const unsigned int blk = 8u * U;
+    const unsigned int nblk = (p1 - p0 + blk - 1u) / blk;
+    const unsigned int per = (nblk + 3u) / 4u;
+    const unsigned int w0 = p0 + wave * per * blk;
+    const unsigned int w1 = (w0 + per * blk < p1) ? w0 + per * blk : p1;
     const unsigned int agent = a.agent[t];
     const aotx_kv_table *kv = &a.state->kv;
     const float scale = 1.0f / sqrtf((float)D);
 
-    /* the G query heads of this KV head, as fp32 */
     float qv[G][E];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
@@ -99,39 +108,52 @@ __global__ __launch_bounds__(64) void aotx_attend_kernel(aotx_attn_args a)
             }
         }
     }
-
+    float o[G][E];
+    float mrun[G], lrun[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        mrun[j] = -INFINITY;
+        lrun[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[j][e] = 0.0f;
+    }
     int missing = 0;
     const unsigned int kbase = kh * AOTX_KVL_BLOCK;
     const unsigned int vbase = (a.kv_heads + kh) * AOTX_KVL_BLOCK;
 
-    /* pass 1: scores */
-    for (unsigned int base = p0; base < p1; base += 8u * ATTN_UNROLL) {
-        aotx_u4a kr[ATTN_UNROLL][NP];
-        bool valid[ATTN_UNROLL];
+    for (unsigned int base = w0; base < w1; base += blk) {
+        aotx_u4a kr[U][NP], vr[U][NP];
+        bool valid[U];
 #pragma unroll
-        for (int u = 0; u < ATTN_UNROLL; ++u) {
+        for (int u = 0; u < U; ++u) {
             unsigned int p = base + 8u * u + grp;
-            valid[u] = p < p1;
-            unsigned int pp = valid[u] ? p : p0;
-            const unsigned char *blk = aotx_kvl_block(a.shape, kv, agent, a.layer, pp);
-            if (blk == nullptr) {
+            valid[u] = p < w1;
+            unsigned int pp = valid[u] ? p : w0;
+            const unsigned char *bk = aotx_kvl_block(a.shape, kv, agent, a.layer, pp);
+            const bool absent = bk == nullptr;
+            if (absent) {
                 missing = 1;
-                blk = (const unsigned char *)a.q;   /* any readable address */
                 valid[u] = false;
+                bk = (const unsigned char *)a.q;    /* readable; replaced by zeros below */
             }
-            const unsigned short *row = (const unsigned short *)blk
-                + (unsigned long long)(kbase + pp % AOTX_KVL_BLOCK) * D;
+            const unsigned short *krow = (const unsigned short *)bk
+                + (absent ? 0ull : (unsigned long long)(kbase + pp % AOTX_KVL_BLOCK) * D);
+            const unsigned short *vrow = (const unsigned short *)bk
+                + (absent ? 0ull : (unsigned long long)(vbase + pp % AOTX_KVL_BLOCK) * D);
+            const aotx_u4a zero = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int pc = 0; pc < NP; ++pc) {
-                kr[u][pc] = blk == (const unsigned char *)a.q ? (aotx_u4a){0u, 0u, 0u, 0u}
-                                                              : *(const aotx_u4a *)(row + 64 * pc + 8 * sub);
+                aotx_u4a kk = *(const aotx_u4a *)(krow + (absent ? 0 : 64 * pc + 8 * sub));
+                aotx_u4a vv = *(const aotx_u4a *)(vrow + (absent ? 0 : 64 * pc + 8 * sub));
+                kr[u][pc] = absent ? zero : kk;
+                vr[u][pc] = absent ? zero : vv;
             }
         }
+        float sc[U][G];
 #pragma unroll
-        for (int u = 0; u < ATTN_UNROLL; ++u) {
-            float dot[G];
+        for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int j = 0; j < G; ++j) dot[j] = 0.0f;
+            for (int j = 0; j < G; ++j) sc[u][j] = 0.0f;
 #pragma unroll
             for (int pc = 0; pc < NP; ++pc) {
 #pragma unroll
@@ -140,102 +162,69 @@ __global__ __launch_bounds__(64) void aotx_attend_kernel(aotx_attn_args a)
                     float k1 = aotx_attn_h(kr[u][pc][e], 1);
 #pragma unroll
                     for (int j = 0; j < G; ++j) {
-                        dot[j] += qv[j][8 * pc + 2 * e] * k0;
-                        dot[j] += qv[j][8 * pc + 2 * e + 1] * k1;
+                        sc[u][j] += qv[j][8 * pc + 2 * e] * k0;
+                        sc[u][j] += qv[j][8 * pc + 2 * e + 1] * k1;
                     }
                 }
             }
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-                dot[j] += __shfl_xor(dot[j], 1, 64);
-                dot[j] += __shfl_xor(dot[j], 2, 64);
-                dot[j] += __shfl_xor(dot[j], 4, 64);
-            }
-            unsigned int p = base + 8u * u + grp;
-            if (valid[u] && sub == 0u) {
-#pragma unroll
-                for (int j = 0; j < G; ++j) sc[(p - p0) * G + j] = dot[j] * scale;
+                float v = sc[u][j];
+                v += __shfl_xor(v, 1, 64);
+                v += __shfl_xor(v, 2, 64);
+                v += __shfl_xor(v, 4, 64);
+                sc[u][j] = valid[u] ? v * scale : -INFINITY;
             }
         }
-    }
-    missing = __any(missing);
-    if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
-    __syncthreads();
-
-    /* chunk maximum and mass of each query head */
-    float mx[G], mass[G];
+        /* block maximum over the wave's 8 * U positions */
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        float m = -INFINITY;
-        for (unsigned int p = lane; p < cnt; p += 64u) m = fmaxf(m, sc[p * G + j]);
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        mx[j] = missing ? -INFINITY : m;
-    }
-    __syncthreads();
-    float part = 0.0f;
-    {
-        const unsigned int jj = lane % G;
-        float mj = mx[0];
+        for (int j = 0; j < G; ++j) {
+            float mb = sc[0][j];
 #pragma unroll
-        for (int j = 1; j < G; ++j) if ((unsigned int)j == jj) mj = mx[j];
-        for (unsigned int idx = lane; idx < cnt * G; idx += 64u) {
-            float e = missing ? 0.0f : expf(sc[idx] - mj);
-            sc[idx] = e;
-            part += e;
+            for (int u = 1; u < U; ++u) mb = fmaxf(mb, sc[u][j]);
+            mb = fmaxf(mb, __shfl_xor(mb, 8, 64));
+            mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+            float mnew = fmaxf(mrun[j], mb);
+            float shift = (mrun[j] == -INFINITY) ? 0.0f : expf(mrun[j] - mnew);
+            if (mnew == -INFINITY) shift = 1.0f;
+            lrun[j] *= shift;
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[j][e] *= shift;
+            mrun[j] = mnew;
         }
-    }
-    /* lanes with the same lane % G hold one head's partial sums */
-    for (int off = 32; off >= G; off >>= 1) part += __shfl_xor(part, off, 64);
 #pragma unroll
-    for (int j = 0; j < G; ++j) mass[j] = __shfl(part, j, 64);
-    __syncthreads();
-
-    /* pass 2: values */
-    float o[G][E];
+        for (int u = 0; u < U; ++u) {
+            float pw[G];
 #pragma unroll
-    for (int j = 0; j < G; ++j)
-#pragma unroll
-        for (int e = 0; e < E; ++e) o[j][e] = 0.0f;
-    if (!missing) {
-        for (unsigned int base = p0; base < p1; base += 8u * ATTN_UNROLL) {
-            aotx_u4a vr[ATTN_UNROLL][NP];
-            bool valid[ATTN_UNROLL];
-#pragma unroll
-            for (int u = 0; u < ATTN_UNROLL; ++u) {
-                unsigned int p = base + 8u * u + grp;
-                valid[u] = p < p1;
-                unsigned int pp = valid[u] ? p : p0;
-                const unsigned char *blk = aotx_kvl_block(a.shape, kv, agent, a.layer, pp);
-                const unsigned short *row = (const unsigned short *)blk
-                    + (unsigned long long)(vbase + pp % AOTX_KVL_BLOCK) * D;
-#pragma unroll
-                for (int pc = 0; pc < NP; ++pc) vr[u][pc] = *(const aotx_u4a *)(row + 64 * pc + 8 * sub);
+            for (int j = 0; j < G; ++j) {
+                pw[j] = (sc[u][j] == -INFINITY) ? 0.0f : expf(sc[u][j] - mrun[j]);
+                lrun[j] += pw[j];
             }
 #pragma unroll
-            for (int u = 0; u < ATTN_UNROLL; ++u) {
-                unsigned int p = base + 8u * u + grp;
-                float w[G];
+            for (int pc = 0; pc < NP; ++pc) {
 #pragma unroll
-                for (int j = 0; j < G; ++j) w[j] = valid[u] ? sc[(p - p0) * G + j] : 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    float v0 = aotx_attn_h(vr[u][pc][e], 0);
+                    float v1 = aotx_attn_h(vr[u][pc][e], 1);
 #pragma unroll
-                for (int pc = 0; pc < NP; ++pc) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float v0 = aotx_attn_h(vr[u][pc][e], 0);
-                        float v1 = aotx_attn_h(vr[u][pc][e], 1);
-#pragma unroll
-                        for (int j = 0; j < G; ++j) {
-                            o[j][8 * pc + 2 * e] += w[j] * v0;
-                            o[j][8 * pc + 2 * e + 1] += w[j] * v1;
-                        }
+                    for (int j = 0; j < G; ++j) {
+                        o[j][8 * pc + 2 * e] += pw[j] * v0;
+                        o[j][8 * pc + 2 * e + 1] += pw[j] * v1;
                     }
                 }
             }
         }
     }
-    /* sum the 8 position groups: lanes with the same sub */
+    /* the lane groups' sums of one wave (mass counted once per group: lanes of a group
+     * hold the same weights) */
 #pragma unroll
-    for (int j = 0; j < G; ++j)
+    for (int j = 0; j < G; ++j) {
+        float l = lrun[j];
+        l += __shfl_xor(l, 8, 64);
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        lrun[j] = l;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             float v = o[j][e];
@@ -244,49 +233,60 @@ __global__ __launch_bounds__(64) void aotx_attend_kernel(aotx_attn_args a)
             v += __shfl_xor(v, 32, 64);
             o[j][e] = v;
         }
-
-    if (st == 1u) {
-        if (grp == 0u) {
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-                float back = mass[j] > 0.0f ? 1.0f / mass[j] : 0.0f;
-                unsigned short *orow = a.out + ((unsigned long long)t * a.heads + kh * G + j) * D;
-#pragma unroll
-                for (int pc = 0; pc < NP; ++pc)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        orow[64 * pc + 8 * sub + e] = aotx_f2h(o[j][8 * pc + e] * back);
-            }
-        }
-        return;
     }
-
-    /* split context: leave this chunk's (max, mass, sum) for the merge kernel */
-    const unsigned int unit = t * a.kv_heads + kh;
-    const unsigned int stride = G * (D + 2);
-    float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
+    missing = __any(missing);
+    if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
+    if (lane == 0u) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            wm[wave][j] = missing ? -INFINITY : mrun[j];
+            wl[wave][j] = missing ? 0.0f : lrun[j];
+        }
+    }
     if (grp == 0u) {
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
             for (int pc = 0; pc < NP; ++pc)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) mine[j * (D + 2) + 2 + 64 * pc + 8 * sub + e] = o[j][8 * pc + e];
+                for (int e = 0; e < 8; ++e) wo[wave][j][64 * pc + 8 * sub + e] = missing ? 0.0f : o[j][8 * pc + e];
     }
-    if (lane == 0u) {
+    __syncthreads();
+    /* merge the 4 waves in wave order */
+    const unsigned int unit = t * a.kv_heads + kh;
+    const unsigned int stride = G * (D + 2);
+    float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += 256u) {
+        unsigned int j = idx / D, e = idx - j * D;
+        float top = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+        float msum = 0.0f, osum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            mine[j * (D + 2)] = mx[j];
-            mine[j * (D + 2) + 1] = mass[j];
+        for (int w = 0; w < 4; ++w) {
+            float f = (wm[w][j] == -INFINITY) ? 0.0f : expf(wm[w][j] - top);
+            msum += wl[w][j] * f;
+            osum += wo[w][j][e] * f;
+        }
+        if (st == 1u) {
+            float back = msum > 0.0f ? 1.0f / msum : 0.0f;
+            a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
+        } else {
+            mine[j * (D + 2) + 2 + e] = osum;
+            if (e == 0u) {
+                mine[j * (D + 2)] = top;
+                mine[j * (D + 2) + 1] = msum;
+            }
         }
     }
 }
 
 /* Merge the chunks of every (token, KV head) that was split, in chunk order:
- * M = max m_c, out = half(sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M)). */
+ * M = max m_c, out = half(sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M)). The chunk
+ * weights are computed once into LDS; every load of the sums is independent. */
 template <int D, int G>
 __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
 {
+    __shared__ float fw[ATTN_MAX_SPLITS][G];
+    __shared__ float inv[G];
     unsigned int tokens = a.m_dev ? *a.m_dev : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
     const unsigned int unit = blockIdx.x;
@@ -296,28 +296,32 @@ __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
     const unsigned int S = a.splits;
     const unsigned int n = a.pos[t] + 1u;
     unsigned int chunk = (n + S - 1u) / S;
-    chunk = (chunk + 15u) & ~15u;
-    if (chunk < ATTN_MIN_CHUNK) chunk = ATTN_MIN_CHUNK;
-    if (chunk > a.chunk_max) return;
+    chunk = (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
     const unsigned int st = (n + chunk - 1u) / chunk;
     if (st <= 1u) return;
     const unsigned int stride = G * (D + 2);
     const float *all = a.partial + (unsigned long long)unit * S * stride;
+    if (threadIdx.x < (unsigned int)G) {
+        const unsigned int j = threadIdx.x;
+        float top = -INFINITY;
+        for (unsigned int cc = 0; cc < st; ++cc) top = fmaxf(top, all[cc * stride + j * (D + 2)]);
+        float msum = 0.0f;
+        for (unsigned int cc = 0; cc < st; ++cc) {
+            float mc = all[cc * stride + j * (D + 2)];
+            float f = (mc == -INFINITY) ? 0.0f : expf(mc - top);
+            fw[cc][j] = f;
+            msum += all[cc * stride + j * (D + 2) + 1] * f;
+        }
+        inv[j] = msum > 0.0f ? 1.0f / msum : 0.0f;
+    }
+    __syncthreads();
     for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += blockDim.x) {
         unsigned int j = idx / D;
         unsigned int e = idx - j * D;
-        float top = -INFINITY;
-        for (unsigned int cc = 0; cc < st; ++cc) top = fmaxf(top, all[cc * stride + j * (D + 2)]);
-        float msum = 0.0f, osum = 0.0f;
-        for (unsigned int cc = 0; cc < st; ++cc) {
-            const float *pc = all + cc * stride + j * (D + 2);
-            float mc = pc[0];
-            float f = (mc == -INFINITY) ? 0.0f : expf(mc - top);
-            msum += pc[1] * f;
-            osum += pc[2 + e] * f;
-        }
-        float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-        a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
+        float osum = 0.0f;
+#pragma unroll 8
+        for (unsigned int cc = 0; cc < st; ++cc) osum += all[cc * stride + j * (D + 2) + 2 + e] * fw[cc][j];
+        a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * inv[j]);
     }
 }
 
@@ -333,11 +337,12 @@ struct aotx_attn_plan {
 unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
                               unsigned int max_context)
 {
+    /* about 1024 workgroups over the launch, chunks of at least 128 positions */
     unsigned int units = tokens * kv_heads;
-    unsigned int s = (2048u + units - 1u) / units;
-    unsigned int need = (max_context + 1023u) / 1024u;  /* chunk <= 1024 positions */
-    if (s < need) s = need;
-    if (s > 256u) s = 256u;
+    unsigned int s = (1024u + units - 1u) / units;
+    unsigned int cap = (max_context + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN;
+    if (s > cap) s = cap;
+    if (s > ATTN_MAX_SPLITS) s = ATTN_MAX_SPLITS;
     if (s < 1u) s = 1u;
     return s;
 }
@@ -371,21 +376,17 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
     a.kv_heads = kv_heads;
     a.layer = layer;
     a.splits = aotx_attn_splits(tokens, kv_heads, max_context);
-    unsigned int chunk = (max_context + a.splits - 1u) / a.splits;
-    chunk = (chunk + 15u) & ~15u;
-    if (chunk < ATTN_MIN_CHUNK) chunk = ATTN_MIN_CHUNK;
-    a.chunk_max = chunk;
+    a.chunk_max = max_context;
     a.shape = aotx_kvl_make(layers, kv_heads, head_dim);
     a.state = aotx_state_device();
     a.partial = partial != nullptr
         ? partial
         : (float *)aotx_scratch(AOTX_SCRATCH_ATTN_PARTIAL,
                                 aotx_attn_scratch(tokens, kv_heads, a.splits, g, head_dim));
-    size_t lds = (size_t)chunk * g * sizeof(float);
     dim3 grid(tokens * kv_heads * a.splits);
 #define AOTX_ATTN_GO(DD, GG)                                                               \
     do {                                                                                   \
-        hipLaunchKernelGGL((aotx_attend_kernel<DD, GG>), grid, dim3(64), lds, stream, a);  \
+        hipLaunchKernelGGL((aotx_attend_kernel<DD, GG>), grid, dim3(256), 0, stream, a);   \
         AOTX_LAUNCH_CHECK();                                                               \
         if (a.splits > 1u) {                                                               \
             hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads),       \

@@ -18,6 +18,11 @@ void aotx_launch_route(const float *router, const unsigned short *x, const unsig
                        unsigned int tokens, unsigned int hidden, unsigned int experts,
                        unsigned int used, float *prob, unsigned int *ids, hipStream_t s);
 
+/* Slots (token * used + rank) of each expert in slot order: list[e * cap + i], count[e]. */
+void aotx_launch_group(const unsigned int *ids, const unsigned int *m_dev, unsigned int tokens,
+                       unsigned int used, unsigned int experts, unsigned int *list,
+                       unsigned int *count, unsigned int cap, hipStream_t s);
+
 /* Group the routed slots, then gate/up (+SwiGLU) into act [slots][ffn] and down into
  * y [slots][hidden] fp32. tokens = the capacity of the batch (passes of 32 rows). */
 int aotx_launch_expert_ffn(const aotx_expert_plan &p, const unsigned short *x,

@@ -109,6 +109,15 @@ __global__ void aotx_expert_sum_kernel(const float *y, const float *prob, const 
     }
 }
 
+void aotx_launch_group(const unsigned int *ids, const unsigned int *m_dev, unsigned int tokens,
+                       unsigned int used, unsigned int experts, unsigned int *list,
+                       unsigned int *count, unsigned int cap, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_group_kernel, dim3((experts + 255u) / 256u), dim3(256), 0, s, ids, m_dev,
+                       tokens, used, experts, list, count, cap);
+    AOTX_LAUNCH_CHECK();
+}
+
 void aotx_launch_route(const float *router, const unsigned short *x, const unsigned int *m_dev,
                        unsigned int tokens, unsigned int hidden, unsigned int experts,
                        unsigned int used, float *prob, unsigned int *ids, hipStream_t s)

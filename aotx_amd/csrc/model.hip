@@ -26,6 +26,7 @@
 #include "experts.h"
 #include "gemv.h"
 #include "norm.h"
+#include "rgemv.h"
 #include "sample.h"
 
 #include <stdlib.h>
@@ -34,6 +35,11 @@
 unsigned long long aotx_mem_weights_bytes(void);
 
 #define AOTX_BUCKETS 10u   /* 1, 2, 4, ..., 512 */
+
+/* Repacked (Q8R) copies of one layer's matrices; the library owns them. */
+struct aotx_rlayer {
+    const unsigned char *q, *k, *v, *o, *gate, *up, *down;
+};
 
 struct aotx_hold {
     int ready;
@@ -45,8 +51,13 @@ struct aotx_hold {
     hipStream_t stream;
     aotx_step *pinned;
     aotx_step *step;              /* device copy */
+    /* repacked weights */
+    unsigned char *rw;
+    aotx_rlayer rl[AOTX_MODEL_MAX_LAYERS];
+    const unsigned char *rhead;
     /* buffers */
     float *resid;
+    float *sumsq;                 /* [tokens][hidden/16] */
     unsigned short *x;
     unsigned short *qh;
     unsigned short *att;
@@ -56,16 +67,17 @@ struct aotx_hold {
     float *logits;                /* [max_rows][vocab] */
     unsigned int *pos, *tagent, *last;
     float *gemv_partial;
+    size_t gemv_partial_bytes;
     float *attn_partial;
     float *prob;
     unsigned int *ids;
     float *ey;
     unsigned short *eact;
     unsigned int *elist, *ecount;
-    void *piece[32];
+    void *piece[40];
     unsigned int pieces;
-    /* graphs per token bucket and head-row bucket */
-    hipGraphExec_t exec[AOTX_BUCKETS][AOTX_BUCKETS];
+    /* graphs per row selection, token bucket and head-row bucket */
+    hipGraphExec_t exec[2][AOTX_BUCKETS][AOTX_BUCKETS];
     unsigned int nodes;
 };
 
@@ -96,7 +108,7 @@ static void *aotx_take(aotx_hold *h, size_t bytes)
     if (bytes == 0u) bytes = 256u;
     AOTX_CHECK(hipMalloc(&p, bytes));
     AOTX_CHECK(hipMemset(p, 0, bytes));
-    if (h->pieces >= 32u) {
+    if (h->pieces >= 40u) {
         fprintf(stderr, "aotx: too many buffers\n");
         exit(1);
     }
@@ -174,39 +186,55 @@ extern "C" int aotx_model_set_desc(unsigned int role, const aotx_model_desc *des
 
 /* ---- planning helpers -------------------------------------------------------------- */
 
-static aotx_gemv_args aotx_plan_or_die(const void *const *w, const unsigned int *rows,
-                                       unsigned int nseg, unsigned int k, int epi)
+/* One product of a step over repacked weights, in passes of at most 32 batch rows; a
+ * batch of at most 16 rows may stage x from the residual stream (norm fused). */
+static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int *rows,
+                          unsigned int nseg, unsigned int k, int epi, unsigned int cap,
+                          const unsigned int *m_dev, const aotx_rgemv_args &tmpl)
 {
-    aotx_gemv_args a;
-    if (aotx_gemv_plan(&a, w, rows, nseg, k, epi) != 0) {
-        fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);
-        exit(1);
-    }
-    return a;
-}
-
-/* One product of a step: row passes of 32 over the bucket; with one pass and a split k,
- * the partials may be left for the next kernel (defer). */
-static void aotx_product(aotx_hold *h, aotx_gemv_args a, unsigned int bucket_rows,
-                         const unsigned int *m_dev, int allow_defer, int *deferred)
-{
-    a.partial = h->gemv_partial;
-    a.m_dev = m_dev;
-    unsigned int passes = (bucket_rows + 31u) / 32u;
-    *deferred = 0;
-    for (unsigned int i = 0; i < passes; ++i) {
-        aotx_gemv_args p = a;
-        p.m0 = 32u * i;
-        p.m = bucket_rows <= 16u ? 16u : 32u;
-        p.defer = (allow_defer && passes == 1u && a.splits > 1u) ? 1 : 0;
-        if (p.defer) *deferred = 1;
-        aotx_gemv_launch(p, h->stream);
+    for (unsigned int m0 = 0; m0 < cap; m0 += 32u) {
+        unsigned int mt = cap - m0 < 32u ? cap - m0 : 32u;
+        aotx_rgemv_args a;
+        if (aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt) != 0) {
+            fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);
+            exit(1);
+        }
+        /* the call's operands over the plan */
+        a.xmode = tmpl.xmode;
+        a.x = tmpl.x;
+        a.ldx = tmpl.ldx;
+        a.resid = tmpl.resid;
+        a.norm_w = tmpl.norm_w;
+        a.sumsq = tmpl.sumsq;
+        a.eps = tmpl.eps;
+        a.xrow = tmpl.xrow;
+        a.m_dev = m_dev;
+        a.m0 = m0;
+        a.y = tmpl.y;
+        a.ldy = tmpl.ldy;
+        a.sumsq_out = tmpl.sumsq_out;
+        a.qkv = tmpl.qkv;
+        a.expert_stride = tmpl.expert_stride;
+        a.list = tmpl.list;
+        a.list_count = tmpl.list_count;
+        a.list_cap = tmpl.list_cap;
+        a.xrow_div = tmpl.xrow_div;
+        a.experts = tmpl.experts;
+        if (a.splits > 1u) {
+            size_t need = aotx_rgemv_partial_bytes(a);
+            if (need > h->gemv_partial_bytes) {
+                fprintf(stderr, "aotx: split partials exceed the planned buffer\n");
+                exit(1);
+            }
+            a.partial = h->gemv_partial;
+        }
+        aotx_rgemv_launch(a, h->stream);
     }
 }
 
 /* ---- the step ---------------------------------------------------------------------- */
 
-static void aotx_record_step(aotx_hold *h, unsigned int bt, unsigned int br)
+static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br)
 {
     const aotx_model_desc *d = &h->desc;
     hipStream_t s = h->stream;
@@ -216,46 +244,68 @@ static void aotx_record_step(aotx_hold *h, unsigned int bt, unsigned int br)
     const unsigned int *m_rows = &h->step->run.rows;
     const unsigned int hd = d->head_dim;
     const unsigned int wide = d->heads * hd, narrow = d->kv_heads * hd;
-    const unsigned int mt = T <= 16u ? 16u : 32u;
     const aotx_kvl_shape shape = aotx_kvl_make(d->layers, d->kv_heads, hd);
     const unsigned int max_context = AOTX_SEQ_MAX_TOKENS;
+    const bool fused_norm = T <= 16u;                /* x staged from the residual stream */
+    const bool experts = d->expert_count != 0u;
 
     AOTX_CHECK(hipMemcpyAsync(h->step, h->pinned, sizeof(aotx_step), hipMemcpyHostToDevice, s));
     aotx_launch_rows(h->step, T, h->pos, h->tagent, h->last, s);
     aotx_launch_gather(h->step, T, aotx_tensor(d->token_embd), d->embd_type, d->hidden, d->vocab,
-                       h->resid, h->x, (const float *)aotx_tensor(d->layer[0].offset[AOTX_SLOT_ATTN_NORM]),
-                       d->rms_eps, s);
+                       h->resid, h->sumsq, s);
+
+    aotx_norm_args nrm;
+    memset(&nrm, 0, sizeof nrm);
+    nrm.m_dev = m_tokens;
+    nrm.resid = h->resid;
+    nrm.sumsq = h->sumsq;
+    nrm.eps = d->rms_eps;
+    nrm.hidden = d->hidden;
+    nrm.x = h->x;
+
     for (unsigned int l = 0; l < d->layers; ++l) {
         const aotx_model_layer *L = &d->layer[l];
-        int deferred = 0;
-        /* attention half */
-        const void *qkv_w[3] = {aotx_tensor(L->offset[AOTX_SLOT_ATTN_Q]),
-                                aotx_tensor(L->offset[AOTX_SLOT_ATTN_K]),
-                                aotx_tensor(L->offset[AOTX_SLOT_ATTN_V])};
+        const aotx_rlayer *RL = &h->rl[l];
+        const float *attn_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_ATTN_NORM]);
+        const float *ffn_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_FFN_NORM]);
+
+        /* ---- attention half ---- */
+        aotx_rgemv_args x_in;
+        memset(&x_in, 0, sizeof x_in);
+        if (fused_norm) {
+            x_in.xmode = AOTX_X_NORM;
+            x_in.resid = h->resid;
+            x_in.norm_w = attn_w;
+            x_in.sumsq = h->sumsq;
+            x_in.eps = d->rms_eps;
+        } else {
+            nrm.norm_w = attn_w;
+            aotx_launch_norm(nrm, T, s);
+            x_in.xmode = AOTX_X_F16;
+            x_in.x = h->x;
+            x_in.ldx = d->hidden;
+        }
+        const void *qkv_w[3] = {RL->q, RL->k, RL->v};
         unsigned int qkv_rows[3] = {wide, narrow, narrow};
         if (aotx_fused_qkv(d, l)) {
-            aotx_gemv_args a = aotx_plan_or_die(qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_QKV);
-            a.x = h->x;
-            a.ldx = d->hidden;
-            a.qkv.qh = h->qh;
-            a.qkv.pos = h->pos;
-            a.qkv.agent = h->tagent;
-            a.qkv.state = aotx_state_device();
-            a.qkv.shape = shape;
-            a.qkv.layer = l;
-            a.qkv.heads = d->heads;
-            a.qkv.kv_heads = d->kv_heads;
-            a.qkv.head_dim = hd;
-            a.qkv.theta = d->rope_theta;
-            a.qkv.factor = (const float *)aotx_tensor(d->rope_freqs);
-            aotx_product(h, a, T, m_tokens, 0, &deferred);
+            aotx_rgemv_args t = x_in;
+            t.qkv.qh = h->qh;
+            t.qkv.pos = h->pos;
+            t.qkv.agent = h->tagent;
+            t.qkv.state = aotx_state_device();
+            t.qkv.shape = shape;
+            t.qkv.layer = l;
+            t.qkv.heads = d->heads;
+            t.qkv.kv_heads = d->kv_heads;
+            t.qkv.head_dim = hd;
+            t.qkv.theta = d->rope_theta;
+            t.qkv.factor = (const float *)aotx_tensor(d->rope_freqs);
+            aotx_rproduct(h, qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_QKV, T, m_tokens, t);
         } else {
-            aotx_gemv_args a = aotx_plan_or_die(qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_F32);
-            a.x = h->x;
-            a.ldx = d->hidden;
-            a.y = h->qkv;
-            a.ldy = wide + 2u * narrow;
-            aotx_product(h, a, T, m_tokens, 0, &deferred);
+            aotx_rgemv_args t = x_in;
+            t.y = h->qkv;
+            t.ldy = wide + 2u * narrow;
+            aotx_rproduct(h, qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_F32, T, m_tokens, t);
             aotx_rope_args r;
             memset(&r, 0, sizeof r);
             r.m_dev = m_tokens;
@@ -287,105 +337,131 @@ static void aotx_record_step(aotx_hold *h, unsigned int bt, unsigned int br)
             fprintf(stderr, "aotx: attention refused the shape\n");
             exit(1);
         }
-        const void *o_w[1] = {aotx_tensor(L->offset[AOTX_SLOT_ATTN_O])};
-        unsigned int o_rows[1] = {d->hidden};
-        aotx_gemv_args o = aotx_plan_or_die(o_w, o_rows, 1u, wide, AOTX_EPI_RESID);
-        o.x = h->att;
-        o.ldx = wide;
-        o.y = h->resid;
-        o.ldy = d->hidden;
-        aotx_product(h, o, T, m_tokens, 1, &deferred);
-        aotx_resid_norm_args rn;
-        memset(&rn, 0, sizeof rn);
-        rn.m_dev = m_tokens;
-        rn.resid = h->resid;
-        rn.x = h->x;
-        rn.norm_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_FFN_NORM]);
-        rn.eps = d->rms_eps;
-        rn.hidden = d->hidden;
-        if (deferred) {
-            rn.partial = h->gemv_partial;
-            rn.splits = o.splits;
-            rn.mt = mt;
+        {
+            aotx_rgemv_args t;
+            memset(&t, 0, sizeof t);
+            t.xmode = AOTX_X_F16;
+            t.x = h->att;
+            t.ldx = wide;
+            t.y = h->resid;
+            t.ldy = d->hidden;
+            t.sumsq_out = h->sumsq;
+            const void *o_w[1] = {RL->o};
+            unsigned int o_rows[1] = {d->hidden};
+            aotx_rproduct(h, o_w, o_rows, 1u, wide, AOTX_EPI_RESID, T, m_tokens, t);
         }
-        aotx_launch_resid_norm(rn, T, s);
 
-        /* feed-forward half */
-        aotx_resid_norm_args nx;
-        memset(&nx, 0, sizeof nx);
-        nx.m_dev = m_tokens;
-        nx.resid = h->resid;
-        nx.x = h->x;
-        nx.eps = d->rms_eps;
-        nx.hidden = d->hidden;
-        if (d->kind[l] == AOTX_LAYER_KIND_FFN_EXPERTS) {
+        /* ---- feed-forward half ---- */
+        if (experts) {
+            nrm.norm_w = ffn_w;
+            aotx_launch_norm(nrm, T, s);
             aotx_launch_route((const float *)aotx_tensor(L->offset[AOTX_EXPERT_ROUTER]), h->x, m_tokens,
                               T, d->hidden, d->expert_count, d->expert_used_count, h->prob, h->ids, s);
-            aotx_expert_plan p;
-            p.gate = aotx_tensor(L->offset[AOTX_SLOT_FFN_GATE]);
-            p.up = aotx_tensor(L->offset[AOTX_SLOT_FFN_UP]);
-            p.down = aotx_tensor(L->offset[AOTX_SLOT_FFN_DOWN]);
-            p.experts = d->expert_count;
-            p.used = d->expert_used_count;
-            p.hidden = d->hidden;
-            p.ffn = d->ffn;
-            p.list = h->elist;
-            p.count = h->ecount;
-            p.cap = h->max_tokens * d->expert_used_count;
-            if (aotx_launch_expert_ffn(p, h->x, m_tokens, T, h->ids, h->eact, h->ey, s) != 0) {
-                fprintf(stderr, "aotx: the expert products were refused\n");
-                exit(1);
-            }
-            nx.expert_y = h->ey;
-            nx.expert_prob = h->prob;
-            nx.expert_ids = h->ids;
-            nx.experts = d->expert_count;
-            nx.used = d->expert_used_count;
-        } else {
-            const void *gu_w[2] = {aotx_tensor(L->offset[AOTX_SLOT_FFN_GATE]),
-                                   aotx_tensor(L->offset[AOTX_SLOT_FFN_UP])};
+            const unsigned int used = d->expert_used_count;
+            const unsigned int cap = h->max_tokens * used;
+            aotx_launch_group(h->ids, m_tokens, T, used, d->expert_count, h->elist, h->ecount, cap, s);
+            aotx_rgemv_args t;
+            memset(&t, 0, sizeof t);
+            t.xmode = AOTX_X_F16;
+            t.x = h->x;
+            t.ldx = d->hidden;
+            t.y = h->eact;
+            t.ldy = d->ffn;
+            t.expert_stride = aotx_q8r_bytes(d->ffn, d->hidden);
+            t.list = h->elist;
+            t.list_count = h->ecount;
+            t.list_cap = cap;
+            t.xrow_div = used;
+            t.experts = d->expert_count;
+            const void *gu_w[2] = {RL->gate, RL->up};
             unsigned int gu_rows[2] = {d->ffn, d->ffn};
-            aotx_gemv_args gu = aotx_plan_or_die(gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU);
-            gu.x = h->x;
-            gu.ldx = d->hidden;
-            gu.y = h->act;
-            gu.ldy = d->ffn;
-            aotx_product(h, gu, T, m_tokens, 0, &deferred);
-            const void *dn_w[1] = {aotx_tensor(L->offset[AOTX_SLOT_FFN_DOWN])};
+            /* an expert takes at most every token once */
+            aotx_rproduct(h, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, nullptr, t);
+            aotx_rgemv_args u = t;
+            u.x = h->eact;
+            u.ldx = d->ffn;
+            u.y = h->ey;
+            u.ldy = d->hidden;
+            u.expert_stride = aotx_q8r_bytes(d->hidden, d->ffn);
+            u.xrow_div = 1u;
+            const void *dn_w[1] = {RL->down};
             unsigned int dn_rows[1] = {d->hidden};
-            aotx_gemv_args dn = aotx_plan_or_die(dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_RESID);
-            dn.x = h->act;
-            dn.ldx = d->ffn;
-            dn.y = h->resid;
-            dn.ldy = d->hidden;
-            aotx_product(h, dn, T, m_tokens, 1, &deferred);
-            if (deferred) {
-                nx.partial = h->gemv_partial;
-                nx.splits = dn.splits;
-                nx.mt = mt;
-            }
-        }
-        if (l + 1u < d->layers) {
-            nx.norm_w = (const float *)aotx_tensor(d->layer[l + 1u].offset[AOTX_SLOT_ATTN_NORM]);
+            aotx_rproduct(h, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_F32, T, nullptr, u);
+            aotx_expert_resid_args er;
+            er.m_dev = m_tokens;
+            er.resid = h->resid;
+            er.sumsq = h->sumsq;
+            er.y = h->ey;
+            er.prob = h->prob;
+            er.ids = h->ids;
+            er.experts = d->expert_count;
+            er.used = used;
+            er.hidden = d->hidden;
+            aotx_launch_expert_resid(er, T, s);
         } else {
-            nx.norm_w = (const float *)aotx_tensor(d->output_norm);
-            nx.sel = h->sel;
-            nx.last = h->last;
-            nx.step = h->step;
+            aotx_rgemv_args t;
+            memset(&t, 0, sizeof t);
+            if (fused_norm) {
+                t.xmode = AOTX_X_NORM;
+                t.resid = h->resid;
+                t.norm_w = ffn_w;
+                t.sumsq = h->sumsq;
+                t.eps = d->rms_eps;
+            } else {
+                nrm.norm_w = ffn_w;
+                aotx_launch_norm(nrm, T, s);
+                t.xmode = AOTX_X_F16;
+                t.x = h->x;
+                t.ldx = d->hidden;
+            }
+            t.y = h->act;
+            t.ldy = d->ffn;
+            const void *gu_w[2] = {RL->gate, RL->up};
+            unsigned int gu_rows[2] = {d->ffn, d->ffn};
+            aotx_rproduct(h, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, m_tokens, t);
+            aotx_rgemv_args u;
+            memset(&u, 0, sizeof u);
+            u.xmode = AOTX_X_F16;
+            u.x = h->act;
+            u.ldx = d->ffn;
+            u.y = h->resid;
+            u.ldy = d->hidden;
+            u.sumsq_out = h->sumsq;
+            const void *dn_w[1] = {RL->down};
+            unsigned int dn_rows[1] = {d->hidden};
+            aotx_rproduct(h, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_RESID, T, m_tokens, u);
         }
-        aotx_launch_resid_norm(nx, T, s);
     }
-    /* output head on the selected rows, then the sampler */
-    const unsigned long long head_off = d->tied_output ? d->token_embd : d->output;
-    const void *hw[1] = {aotx_tensor(head_off)};
-    unsigned int hrows[1] = {d->vocab};
-    aotx_gemv_args hp = aotx_plan_or_die(hw, hrows, 1u, d->hidden, AOTX_EPI_F32);
-    hp.x = h->sel;
-    hp.ldx = d->hidden;
-    hp.y = h->logits;
-    hp.ldy = d->vocab;
-    int deferred = 0;
-    aotx_product(h, hp, R, m_rows, 0, &deferred);
+    /* output head on the selected rows (each sequence's last token, or every token) */
+    {
+        aotx_rgemv_args t;
+        memset(&t, 0, sizeof t);
+        const float *out_w = (const float *)aotx_tensor(d->output_norm);
+        if (R <= 16u) {
+            t.xmode = AOTX_X_NORM;
+            t.resid = h->resid;
+            t.norm_w = out_w;
+            t.sumsq = h->sumsq;
+            t.eps = d->rms_eps;
+            t.xrow = sel_all ? nullptr : h->last;
+        } else {
+            aotx_norm_args on = nrm;
+            on.norm_w = out_w;
+            on.x = nullptr;
+            on.sel = h->sel;
+            on.last = h->last;
+            on.step = h->step;
+            aotx_launch_norm(on, T, s);
+            t.xmode = AOTX_X_F16;
+            t.x = h->sel;
+            t.ldx = d->hidden;
+        }
+        t.y = h->logits;
+        t.ldy = d->vocab;
+        const void *hw[1] = {h->rhead};
+        unsigned int hrows[1] = {d->vocab};
+        aotx_rproduct(h, hw, hrows, 1u, d->hidden, AOTX_EPI_F32, R, m_rows, t);
+    }
     aotx_launch_pick(h->logits, d->vocab, d->vocab, m_rows, R, nullptr, nullptr, 0u, 1.0f, 0.0f,
                      0ull, nullptr, nullptr, &h->step->run, s);
     aotx_launch_shut_rows(h->step, s);
@@ -421,7 +497,8 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     const unsigned int hd = d->head_dim;
     const size_t wide = (size_t)d->heads * hd, narrow = (size_t)d->kv_heads * hd;
     h->resid = (float *)aotx_take(h, T * d->hidden * 4u);
-    h->x = (unsigned short *)aotx_take(h, T * (d->hidden > d->ffn ? d->hidden : d->ffn) * 2u);
+    h->sumsq = (float *)aotx_take(h, T * ((d->hidden + 15u) / 16u) * 4u);
+    h->x = (unsigned short *)aotx_take(h, T * d->hidden * 2u);
     h->qh = (unsigned short *)aotx_take(h, T * wide * 2u);
     h->att = (unsigned short *)aotx_take(h, T * wide * 2u);
     h->act = (unsigned short *)aotx_take(h, T * d->ffn * 2u);
@@ -431,24 +508,81 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     h->pos = (unsigned int *)aotx_take(h, T * 4u);
     h->tagent = (unsigned int *)aotx_take(h, T * 4u);
     h->last = (unsigned int *)aotx_take(h, AOTX_SLOTS * 4u);
-    /* split partials: the largest product plan over every bucket */
+
+    /* repacked copies of every matrix (the same bytes per weight, MFMA operand order) */
+    const unsigned int E = d->expert_count != 0u ? d->expert_count : 1u;
+    const unsigned long long bq = aotx_q8r_bytes((unsigned int)wide, d->hidden);
+    const unsigned long long bk = aotx_q8r_bytes((unsigned int)narrow, d->hidden);
+    const unsigned long long bo = aotx_q8r_bytes(d->hidden, (unsigned int)wide);
+    const unsigned long long bg = aotx_q8r_bytes(d->ffn, d->hidden);
+    const unsigned long long bd = aotx_q8r_bytes(d->hidden, d->ffn);
+    const unsigned long long per_layer = bq + 2ull * bk + bo + E * (2ull * bg + bd);
+    const unsigned long long bh = aotx_q8r_bytes(d->vocab, d->hidden);
+    const unsigned long long total = per_layer * d->layers + bh;
+    h->rw = (unsigned char *)aotx_take(h, (size_t)total);
+    {
+        unsigned char *at = h->rw;
+        const unsigned long long src_g = (unsigned long long)d->ffn * (d->hidden / 32u) * 34ull;
+        const unsigned long long src_d = (unsigned long long)d->hidden * (d->ffn / 32u) * 34ull;
+        for (unsigned int l = 0; l < d->layers; ++l) {
+            const aotx_model_layer *L = &d->layer[l];
+            aotx_rlayer *RL = &h->rl[l];
+            aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_ATTN_Q]), (unsigned int)wide, d->hidden, at, nullptr);
+            RL->q = at; at += bq;
+            aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_ATTN_K]), (unsigned int)narrow, d->hidden, at, nullptr);
+            RL->k = at; at += bk;
+            aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_ATTN_V]), (unsigned int)narrow, d->hidden, at, nullptr);
+            RL->v = at; at += bk;
+            aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_ATTN_O]), d->hidden, (unsigned int)wide, at, nullptr);
+            RL->o = at; at += bo;
+            RL->gate = at;
+            for (unsigned int e = 0; e < E; ++e, at += bg)
+                aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_FFN_GATE]) + e * src_g, d->ffn, d->hidden, at, nullptr);
+            RL->up = at;
+            for (unsigned int e = 0; e < E; ++e, at += bg)
+                aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_FFN_UP]) + e * src_g, d->ffn, d->hidden, at, nullptr);
+            RL->down = at;
+            for (unsigned int e = 0; e < E; ++e, at += bd)
+                aotx_q8r_repack(aotx_tensor(L->offset[AOTX_SLOT_FFN_DOWN]) + e * src_d, d->hidden, d->ffn, at, nullptr);
+        }
+        const unsigned long long head_off = d->tied_output ? d->token_embd : d->output;
+        aotx_q8r_repack(aotx_tensor(head_off), d->vocab, d->hidden, at, nullptr);
+        h->rhead = at;
+        AOTX_CHECK(hipDeviceSynchronize());
+    }
+
+    /* split partials: the largest plan over every product and batch capacity */
     size_t gp = 0u;
     {
-        const unsigned int ks[3] = {d->hidden, (unsigned int)wide, d->ffn};
-        const unsigned int ns[4] = {(unsigned int)(wide + 2u * narrow), d->hidden, 2u * d->ffn, d->vocab};
-        for (unsigned int i = 0; i < 3u; ++i) {
-            for (unsigned int j = 0; j < 4u; ++j) {
-                aotx_gemv_args a;
-                const void *w[1] = {(const void *)1};
-                unsigned int rows[1] = {ns[j]};
-                if (aotx_gemv_plan(&a, w, rows, 1u, ks[i], AOTX_EPI_F32) == 0) {
-                    size_t need = aotx_gemv_scratch_partial(a);
-                    if (need > gp) gp = need;
-                }
+        const void *w1[1] = {(const void *)1};
+        const void *w2[2] = {(const void *)1, (const void *)1};
+        const void *w3[3] = {(const void *)1, (const void *)1, (const void *)1};
+        for (unsigned int mt = 1u; mt <= 32u; ++mt) {
+            aotx_rgemv_args a;
+            unsigned int r3[3] = {(unsigned int)wide, (unsigned int)narrow, (unsigned int)narrow};
+            if (aotx_rgemv_plan(&a, w3, r3, 3u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            unsigned int r1[1] = {d->hidden};
+            if (aotx_rgemv_plan(&a, w1, r1, 1u, (unsigned int)wide, AOTX_EPI_RESID, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt) == 0) {
+                a.expert_stride = d->expert_count != 0u ? 1ull : 0ull;
+                a.experts = E;
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
             }
+            unsigned int r2[2] = {d->ffn, d->ffn};
+            if (aotx_rgemv_plan(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt) == 0) {
+                a.expert_stride = d->expert_count != 0u ? 1ull : 0ull;
+                a.experts = E;
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            }
+            unsigned int rv[1] = {d->vocab};
+            if (aotx_rgemv_plan(&a, w1, rv, 1u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
         }
     }
-    h->gemv_partial = (float *)aotx_take(h, gp + 4096u);
+    h->gemv_partial_bytes = gp + 4096u;
+    h->gemv_partial = (float *)aotx_take(h, h->gemv_partial_bytes);
     size_t ap = 0u;
     for (unsigned int t = 1u; t <= cap; t <<= 1) {
         unsigned int sp = aotx_attn_splits(t, d->kv_heads, AOTX_SEQ_MAX_TOKENS);
@@ -480,9 +614,10 @@ extern "C" void aotx_model_shut(unsigned int role)
     aotx_hold *h = &aotx_holds[role];
     if (!h->ready) return;
     AOTX_CHECK(hipStreamSynchronize(h->stream));
-    for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
-        for (unsigned int j = 0; j < AOTX_BUCKETS; ++j)
-            if (h->exec[i][j] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->exec[i][j]));
+    for (unsigned int a = 0; a < 2u; ++a)
+        for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
+            for (unsigned int j = 0; j < AOTX_BUCKETS; ++j)
+                if (h->exec[a][i][j] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->exec[a][i][j]));
     AOTX_CHECK(hipStreamDestroy(h->stream));
     AOTX_CHECK(hipHostFree(h->pinned));
     for (unsigned int i = 0; i < h->pieces; ++i) AOTX_CHECK(hipFree(h->piece[i]));
@@ -561,12 +696,13 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
     h->pinned->run = *set;
     unsigned int bt = aotx_bucket_of(set->tokens);
     unsigned int br = aotx_bucket_of(set->rows);
+    unsigned int all = set->select == AOTX_MODEL_ROWS_ALL ? 1u : 0u;
     if (aotx_use_graphs()) {
-        hipGraphExec_t &exec = h->exec[bt][br];
+        hipGraphExec_t &exec = h->exec[all][bt][br];
         if (exec == nullptr) {
             hipGraph_t graph = nullptr;
             AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
-            aotx_record_step(h, bt, br);
+            aotx_record_step(h, all, bt, br);
             AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
             size_t count = 0;
             AOTX_CHECK(hipGraphGetNodes(graph, nullptr, &count));
@@ -576,7 +712,7 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
         }
         AOTX_CHECK(hipGraphLaunch(exec, h->stream));
     } else {
-        aotx_record_step(h, bt, br);
+        aotx_record_step(h, all, bt, br);
     }
     if (set->logits != nullptr) {
         AOTX_CHECK(hipMemcpyAsync(set->logits, h->logits,

@@ -11,24 +11,27 @@ struct aotx_step {
     aotx_model_run run;
 };
 
-struct aotx_resid_norm_args {
+struct aotx_norm_args {
     const unsigned int *m_dev;    /* token count */
-    float *resid;                 /* [tokens][hidden] */
-    unsigned short *x;            /* out: [tokens][hidden] fp16 */
-    const float *norm_w;          /* null: add only */
+    const float *resid;           /* [tokens][hidden] */
+    const float *sumsq;           /* [tokens][hidden/16] */
+    const float *norm_w;
     float eps;
     unsigned int hidden;
-    const float *partial;         /* deferred split partials or null */
-    unsigned int splits;
-    unsigned int mt;
-    const float *expert_y;        /* [tokens*used][hidden] or null */
-    const float *expert_prob;
-    const unsigned int *expert_ids;
-    unsigned int experts;
-    unsigned int used;
+    unsigned short *x;            /* out [tokens][hidden], or null */
     unsigned short *sel;          /* head rows, or null */
     const unsigned int *last;     /* last token row of each sequence */
-    const aotx_step *step;        /* seqs and row selection of the call (with sel) */
+    const aotx_step *step;        /* seqs and row selection of the call */
+};
+
+struct aotx_expert_resid_args {
+    const unsigned int *m_dev;
+    float *resid;
+    float *sumsq;
+    const float *y;               /* [tokens*used][hidden] */
+    const float *prob;            /* [tokens][experts] */
+    const unsigned int *ids;      /* [tokens][used] */
+    unsigned int experts, used, hidden;
 };
 
 struct aotx_rope_args {
@@ -52,10 +55,11 @@ void aotx_launch_request(const unsigned int *offset, const unsigned int *agent,
                          unsigned int seqs, aotx_kvl_shape shape, hipStream_t s);
 void aotx_launch_gather(const aotx_step *step, unsigned int max_tokens,
                         const unsigned char *table, unsigned int embd_type,
-                        unsigned int hidden, unsigned int vocab, float *resid,
-                        unsigned short *x, const float *norm_w, float eps, hipStream_t s);
-void aotx_launch_resid_norm(const aotx_resid_norm_args &a, unsigned int max_tokens,
-                            hipStream_t s);
+                        unsigned int hidden, unsigned int vocab, float *resid, float *sumsq,
+                        hipStream_t s);
+void aotx_launch_norm(const aotx_norm_args &a, unsigned int max_tokens, hipStream_t s);
+void aotx_launch_expert_resid(const aotx_expert_resid_args &a, unsigned int max_tokens,
+                              hipStream_t s);
 void aotx_launch_rope(const aotx_rope_args &a, unsigned int max_tokens, hipStream_t s);
 
 #endif

@@ -3,10 +3,10 @@
  *
  * Reference: cuda/model/gather.cu:8-105 (request, open/shut rows, gather, select),
  * cuda/model/norm.cu:49-105 (norm, residual, SwiGLU), cuda/model/rope.cu:128-234 (turn +
- * page write), cuda/model/experts.cu:77-98 (ordered weighted sum). The residual add that
- * follows a projection, the expert sum and the norm that reads the residual are one
- * kernel here: the split partial tiles of the projection are added in split order, then
- * the residual row is normed, so the residual makes one trip through HBM per layer half.
+ * page write), cuda/model/experts.cu:77-98 (ordered weighted sum). Every kernel that writes
+ * the residual stream also leaves the sum of squares of each 16 columns, so a norm needs
+ * no pass of its own over the row: the next product stages x = half(scale * resid * w)
+ * itself (small batches), or the norm kernel here writes x (larger batches).
  */
 #include "aotx_internal.h"
 #include "norm.h"
@@ -99,84 +99,60 @@ __global__ void aotx_request_kernel(const unsigned int *offset, const unsigned i
 }
 
 /* Embedding rows into the residual stream (fp32(scale) * q: cuda/model/gather.cu:53-80 with
- * the Q8_0 reader of cuda/model/blocks.cuh:99-105), then the first layer's norm into x. */
+ * the Q8_0 reader of cuda/model/blocks.cuh:99-105), and the sum of squares of every 16
+ * columns for the first layer's norm. One thread per 16 columns. */
 __global__ __launch_bounds__(256) void aotx_gather_kernel(const aotx_step *step,
                                                          const unsigned char *table,
                                                          unsigned int embd_type,
                                                          unsigned int hidden, unsigned int vocab,
-                                                         float *resid, unsigned short *x,
-                                                         const float *norm_w, float eps)
+                                                         float *resid, float *sumsq)
 {
-    __shared__ float share[4];
     const aotx_model_run *run = &step->run;
     unsigned int t = blockIdx.x;
     if (t >= run->tokens) return;
     int id = run->ids[t];
     unsigned int row = (id < 0 || (unsigned int)id >= vocab) ? 0u : (unsigned int)id;
     float *r = resid + (unsigned long long)t * hidden;
-    float sum = 0.0f;
-    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
-        float v;
-        if (embd_type == AOTX_WEIGHT_Q8_0) {
-            const unsigned char *blk = table + ((unsigned long long)row * (hidden / 32u) + d / 32u) * 34ull;
-            float scale = aotx_h2f((unsigned short)(blk[0] | (blk[1] << 8)));
-            v = scale * (float)(int)(signed char)blk[2u + d % 32u];
-        } else if (embd_type == AOTX_WEIGHT_F16) {
-            v = aotx_h2f(((const unsigned short *)table)[(unsigned long long)row * hidden + d]);
-        } else {
-            v = ((const float *)table)[(unsigned long long)row * hidden + d];
+    const unsigned int tiles = (hidden + 15u) / 16u;
+    for (unsigned int tile = threadIdx.x; tile < tiles; tile += blockDim.x) {
+        float sum = 0.0f;
+        for (unsigned int d = tile * 16u; d < tile * 16u + 16u && d < hidden; ++d) {
+            float v;
+            if (embd_type == AOTX_WEIGHT_Q8_0) {
+                const unsigned char *blk = table + ((unsigned long long)row * (hidden / 32u) + d / 32u) * 34ull;
+                float scale = aotx_h2f((unsigned short)(blk[0] | (blk[1] << 8)));
+                v = scale * (float)(int)(signed char)blk[2u + d % 32u];
+            } else if (embd_type == AOTX_WEIGHT_F16) {
+                v = aotx_h2f(((const unsigned short *)table)[(unsigned long long)row * hidden + d]);
+            } else {
+                v = ((const float *)table)[(unsigned long long)row * hidden + d];
+            }
+            r[d] = v;
+            sum += v * v;
         }
-        r[d] = v;
-        sum += v * v;
-    }
-    sum = aotx_block_sum(sum, share);
-    float scale = rsqrtf(sum / (float)hidden + eps);
-    unsigned short *xr = x + (unsigned long long)t * hidden;
-    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
-        xr[d] = aotx_f2h(scale * r[d] * norm_w[d]);
+        sumsq[(unsigned long long)t * tiles + tile] = sum;
     }
 }
 
-/* resid += (split partials | expert sum), then x = half(rms(resid) * w) (norm.cu:49-90).
- * Partials: [groups][splits][64][mt] tiles of a deferred product (m0 = 0).
- * Experts: y fp32 [tokens*used][hidden], prob [tokens][experts], ids [tokens][used]; the
- * sum rounds each product before it adds, rank by rank (experts.cu:88-95).
- * sel (may be null): the selected rows also go to sel[row] (the head input). */
-__global__ __launch_bounds__(256) void aotx_resid_norm_kernel(aotx_resid_norm_args a)
+/* x = half(rsqrt(sum/h + eps) * resid * w) (cuda/model/norm.cu:49-77), with the row sum
+ * taken from the 16-column partial sums left by the kernel that last wrote the residual.
+ * Grid (tokens, column blocks of 1024). The selected head rows also go to sel. */
+__global__ __launch_bounds__(256) void aotx_norm_kernel(aotx_norm_args a)
 {
     __shared__ float share[4];
     unsigned int tokens = *a.m_dev;
     unsigned int t = blockIdx.x;
     if (t >= tokens) return;
     const unsigned int h = a.hidden;
-    float *r = a.resid + (unsigned long long)t * h;
+    const unsigned int tiles = (h + 15u) / 16u;
+    const float *ss = a.sumsq + (unsigned long long)t * tiles;
     float sum = 0.0f;
-    for (unsigned int d = threadIdx.x; d < h; d += blockDim.x) {
-        float v = r[d];
-        if (a.partial != nullptr) {
-            const unsigned int grp = d >> 6, row = d & 63u;
-            const float *p = a.partial + ((unsigned long long)grp * a.splits * 64u + row) * a.mt + t;
-            float add = 0.0f;
-            for (unsigned int sp = 0; sp < a.splits; ++sp) add += p[(unsigned long long)sp * 64u * a.mt];
-            v += add;
-        }
-        if (a.expert_y != nullptr) {
-            float acc = 0.0f;
-            for (unsigned int rk = 0; rk < a.used; ++rk) {
-                unsigned int e = a.expert_ids[t * a.used + rk];
-                float p = a.expert_prob[t * a.experts + e];
-                float one = __fmul_rn(a.expert_y[((unsigned long long)t * a.used + rk) * h + d], p);
-                acc = rk == 0u ? one : __fadd_rn(acc, one);
-            }
-            v += acc;
-        }
-        r[d] = v;
-        sum += v * v;
-    }
-    if (a.norm_w == nullptr) return;
-    sum = aotx_block_sum(sum, share);
-    float scale = rsqrtf(sum / (float)h + a.eps);
-    unsigned short *xr = a.x + (unsigned long long)t * h;
+    for (unsigned int i = threadIdx.x; i < tiles; i += blockDim.x) sum += ss[i];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if ((threadIdx.x & 63u) == 0u) share[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    sum = share[0] + share[1] + share[2] + share[3];
+    const float scale = rsqrtf(sum / (float)h + a.eps);
     int selected = -1;
     if (a.sel != nullptr && a.last != nullptr && a.step != nullptr) {
         if (a.step->run.select == AOTX_MODEL_ROWS_ALL) {
@@ -186,11 +162,44 @@ __global__ __launch_bounds__(256) void aotx_resid_norm_kernel(aotx_resid_norm_ar
             for (unsigned int s = 0; s < seqs; ++s) if (a.last[s] == t) { selected = (int)s; break; }
         }
     }
-    for (unsigned int d = threadIdx.x; d < h; d += blockDim.x) {
+    const float *r = a.resid + (unsigned long long)t * h;
+    const unsigned int d0 = blockIdx.y * 1024u;
+    for (unsigned int d = d0 + threadIdx.x; d < h && d < d0 + 1024u; d += blockDim.x) {
         unsigned short hv = aotx_f2h(scale * r[d] * a.norm_w[d]);
-        xr[d] = hv;
+        if (a.x != nullptr) a.x[(unsigned long long)t * h + d] = hv;
         if (selected >= 0) a.sel[(unsigned long long)selected * h + d] = hv;
     }
+}
+
+/* resid += the routed experts' weighted sum, rank by rank with each product rounded before
+ * it adds (cuda/model/experts.cu:77-98), then the 16-column sums of squares. Grid (tokens,
+ * column blocks of 256); 16 consecutive threads own one 16-column tile. */
+__global__ __launch_bounds__(256) void aotx_expert_resid_kernel(aotx_expert_resid_args a)
+{
+    unsigned int tokens = *a.m_dev;
+    unsigned int t = blockIdx.x;
+    if (t >= tokens) return;
+    const unsigned int h = a.hidden;
+    const unsigned int d = blockIdx.y * 256u + threadIdx.x;
+    float v2 = 0.0f;
+    if (d < h) {
+        float acc = 0.0f;
+        for (unsigned int rk = 0; rk < a.used; ++rk) {
+            unsigned int e = a.ids[t * a.used + rk];
+            float p = a.prob[t * a.experts + e];
+            float one = __fmul_rn(a.y[((unsigned long long)t * a.used + rk) * h + d], p);
+            acc = rk == 0u ? one : __fadd_rn(acc, one);
+        }
+        float v = a.resid[(unsigned long long)t * h + d] + acc;
+        a.resid[(unsigned long long)t * h + d] = v;
+        v2 = v * v;
+    }
+    /* 16 lanes in order: a fixed butterfly */
+    v2 += __shfl_xor(v2, 1, 64);
+    v2 += __shfl_xor(v2, 2, 64);
+    v2 += __shfl_xor(v2, 4, 64);
+    v2 += __shfl_xor(v2, 8, 64);
+    if ((threadIdx.x & 15u) == 0u && d < h) a.sumsq[(unsigned long long)t * ((h + 15u) / 16u) + d / 16u] = v2;
 }
 
 /* Head norm (optional), rotary turn and page write of one (token, head) from fp32 q/k/v
@@ -281,17 +290,26 @@ void aotx_launch_request(const unsigned int *offset, const unsigned int *agent,
 
 void aotx_launch_gather(const aotx_step *step, unsigned int max_tokens,
                         const unsigned char *table, unsigned int embd_type,
-                        unsigned int hidden, unsigned int vocab, float *resid,
-                        unsigned short *x, const float *norm_w, float eps, hipStream_t s)
+                        unsigned int hidden, unsigned int vocab, float *resid, float *sumsq,
+                        hipStream_t s)
 {
     hipLaunchKernelGGL(aotx_gather_kernel, dim3(max_tokens), dim3(256), 0, s, step, table,
-                       embd_type, hidden, vocab, resid, x, norm_w, eps);
+                       embd_type, hidden, vocab, resid, sumsq);
     AOTX_LAUNCH_CHECK();
 }
 
-void aotx_launch_resid_norm(const aotx_resid_norm_args &a, unsigned int max_tokens, hipStream_t s)
+void aotx_launch_norm(const aotx_norm_args &a, unsigned int max_tokens, hipStream_t s)
 {
-    hipLaunchKernelGGL(aotx_resid_norm_kernel, dim3(max_tokens), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(aotx_norm_kernel, dim3(max_tokens, (a.hidden + 1023u) / 1024u), dim3(256), 0,
+                       s, a);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_expert_resid(const aotx_expert_resid_args &a, unsigned int max_tokens,
+                              hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_expert_resid_kernel, dim3(max_tokens, (a.hidden + 255u) / 256u),
+                       dim3(256), 0, s, a);
     AOTX_LAUNCH_CHECK();
 }
 

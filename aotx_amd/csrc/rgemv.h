@@ -1,0 +1,85 @@
+/* The streaming Q8 product over repacked weights (rgemv.hip).
+ *
+ * Repacked layout ("Q8R") of a Q8_0 tensor [n][k]: the same bytes per weight (one int8
+ * per weight, one fp16 scale per 32), reordered at model open so that one wave reads its
+ * MFMA operands with fully coalesced 16-byte loads and no LDS:
+ *   tiles  T  = ceil(n / 16)         (16 weight rows; rows past n are zero)
+ *   quads  Qn = ceil(k / 128)        (4 blocks of 32; blocks past k are zero)
+ *   quants: [T][Qn][64 lanes][32 B]  lane l = r + 16 g holds row 16t + r, block 4Q + g
+ *   scales: [T][Qn][64 lanes] fp16   the scale of that block
+ * A tensor is 34/32 bytes per weight plus the zero padding of the last tile and quad.
+ */
+#ifndef AOTX_RGEMV_H
+#define AOTX_RGEMV_H
+
+#include "aotx_internal.h"
+#include "gemv.h"
+
+static inline __host__ __device__ unsigned long long aotx_q8r_quads(unsigned int k) { return (k + 127u) / 128u; }
+static inline __host__ __device__ unsigned long long aotx_q8r_tiles(unsigned int n) { return (n + 15u) / 16u; }
+static inline unsigned long long aotx_q8r_quant_bytes(unsigned int n, unsigned int k)
+{
+    return aotx_q8r_tiles(n) * aotx_q8r_quads(k) * 64ull * 32ull;
+}
+static inline unsigned long long aotx_q8r_bytes(unsigned int n, unsigned int k)
+{
+    return aotx_q8r_tiles(n) * aotx_q8r_quads(k) * 64ull * 34ull;
+}
+
+/* Repack a Q8_0 tensor (row-major [rows][k/32] blocks) into Q8R on the stream. */
+void aotx_q8r_repack(const void *src, unsigned int n, unsigned int k, void *dst, hipStream_t s);
+
+/* How the batch rows of x reach the product. */
+enum {
+    AOTX_X_F16 = 0,       /* x fp16 [rows][ldx] in device memory */
+    AOTX_X_NORM = 1       /* x = half(rsqrt(ss/h + eps) * resid * w) computed per workgroup */
+};
+
+struct aotx_rgemv_args {
+    const unsigned char *w[3];    /* Q8R tensors stacked along n */
+    unsigned int seg_end[3];      /* cumulative row ends (multiples of 16 except the last) */
+    unsigned int nseg;
+    unsigned int n;               /* rows (SWIGLU: rows of one of the pair) */
+    unsigned int k;
+    unsigned int qn;              /* quads of k */
+    unsigned int rt;              /* 16-row tiles per workgroup */
+    unsigned int groups;          /* workgroups along n */
+    unsigned int splits;          /* workgroups along k */
+    unsigned int qps;             /* quads per split */
+    /* batch rows */
+    int xmode;
+    const unsigned short *x;      /* AOTX_X_F16 */
+    unsigned int ldx;
+    const float *resid;           /* AOTX_X_NORM: [rows][k] */
+    const float *norm_w;          /* [k] */
+    const float *sumsq;           /* [rows][k/64] partial sums of squares */
+    float eps;
+    const unsigned int *xrow;     /* optional: batch row i reads row xrow[i] */
+    unsigned int m;               /* rows when m_dev is null (also the pass capacity) */
+    const unsigned int *m_dev;
+    unsigned int m0;
+    /* result */
+    int epi;
+    void *y;
+    unsigned int ldy;
+    float *partial;               /* splits > 1: [groups][splits][rt*16][MT] */
+    float *sumsq_out;             /* AOTX_EPI_RESID: [rows][n/64] sums of squares */
+    aotx_qkv_epi qkv;
+    /* routed experts (grid.y): as aotx_gemv_args */
+    unsigned long long expert_stride;
+    const unsigned int *list;
+    const unsigned int *list_count;
+    unsigned int list_cap;
+    unsigned int xrow_div;
+    unsigned int experts;
+};
+
+/* Plan a product over Q8R tensors; rows per segment; returns 1 when refused. */
+int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                    unsigned int nseg, unsigned int k, int epi, unsigned int mt);
+/* Launch one pass (<= 32 rows) and, with splits > 1, the kernel that adds the partials
+ * and applies the epilogue. */
+void aotx_rgemv_launch(const aotx_rgemv_args &a, hipStream_t stream);
+size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a);
+
+#endif

@@ -1,0 +1,653 @@
+/* Streaming Q8 product over repacked (Q8R) weights, for the decode step.
+ *
+ * Same product and operand values as gemv.hip (A = half(q * scale), B = fp16 activations,
+ * fp32 accumulation in v_mfma_f32_16x16x32_f16; reference: cuda/model/gemv.cuh:33-195,
+ * cuda/model/gemm.cuh:55-189), arranged so that the weight stream never touches LDS and no
+ * wave waits on another inside the k loop:
+ *   - a workgroup owns rt 16-row tiles and a k range; its 4 waves take contiguous quarters
+ *     of the k range, each for all rt tiles, and stream their weights with two 16-byte
+ *     loads per lane per tile per 128 k (the repacked layout puts a lane's 32 quants of one
+ *     block next to each other), `pd` quads ahead of the MFMAs;
+ *   - the batch rows of x for the workgroup's k range sit in LDS, staged once at the start
+ *     (from fp16 x, or computed there from the residual stream: x = half(rsqrt(ss/h + eps)
+ *     * resid * w), the reference's RMSNorm rounding of cuda/model/norm.cu:49-77, so the
+ *     norm costs no kernel of its own);
+ *   - the 4 waves' accumulators are added in wave order through LDS at the end; with k
+ *     split over workgroups the partial tiles go to memory and a second kernel adds them in
+ *     split order. Results do not depend on timing.
+ *   - epilogues as gemv.hip, plus the residual add that also leaves the sums of squares of
+ *     every 16 rows for the next norm.
+ */
+#include "rgemv.h"
+
+#include <string.h>
+
+typedef _Float16 rg_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 rg_h2 __attribute__((ext_vector_type(2)));
+typedef float rg_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int rg_u4 __attribute__((ext_vector_type(4)));
+
+#define RG_THREADS 256
+
+/* ---- repack ------------------------------------------------------------------------- */
+
+__global__ void aotx_q8r_repack_kernel(const unsigned char *src, unsigned int n, unsigned int k,
+                                       unsigned char *dst)
+{
+    const unsigned long long qn = aotx_q8r_quads(k);
+    const unsigned long long tiles = aotx_q8r_tiles(n);
+    const unsigned long long items = tiles * qn * 64ull;
+    const unsigned long long quant_bytes = items * 32ull;
+    const unsigned int blocks = k / 32u;
+    const unsigned long long row_bytes = (unsigned long long)blocks * 34ull;
+    for (unsigned long long it = blockIdx.x * (unsigned long long)blockDim.x + threadIdx.x;
+         it < items; it += (unsigned long long)gridDim.x * blockDim.x) {
+        unsigned int lane = (unsigned int)(it % 64ull);
+        unsigned long long tq = it / 64ull;
+        unsigned long long q = tq % qn;
+        unsigned long long t = tq / qn;
+        unsigned int r = lane & 15u, g = lane >> 4;
+        unsigned long long row = t * 16ull + r;
+        unsigned long long blk = q * 4ull + g;
+        unsigned char *qd = dst + it * 32ull;
+        unsigned short *sd = (unsigned short *)(dst + quant_bytes) + it;
+        if (row < n && blk < blocks) {
+            const unsigned char *b = src + row * row_bytes + blk * 34ull;
+            *sd = (unsigned short)(b[0] | (b[1] << 8));
+            for (int j = 0; j < 32; ++j) qd[j] = b[2 + j];
+        } else {
+            *sd = 0u;
+            for (int j = 0; j < 32; ++j) qd[j] = 0u;
+        }
+    }
+}
+
+void aotx_q8r_repack(const void *src, unsigned int n, unsigned int k, void *dst, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_q8r_repack_kernel, dim3(8192), dim3(256), 0, s,
+                       (const unsigned char *)src, n, k, (unsigned char *)dst);
+    AOTX_LAUNCH_CHECK();
+}
+
+/* ---- product ------------------------------------------------------------------------ */
+
+static __device__ __forceinline__ void rg_dequant4(unsigned int w, rg_h2 s2, unsigned int &lo,
+                                                   unsigned int &hi)
+{
+    unsigned int u = w ^ 0x80808080u;
+    unsigned int a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    unsigned int b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const rg_h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(unsigned int, (__builtin_bit_cast(rg_h2, a) - bias) * s2);
+    hi = __builtin_bit_cast(unsigned int, (__builtin_bit_cast(rg_h2, b) - bias) * s2);
+}
+
+/* Weight tile j of a workgroup: Q8R base of its 16 rows, and whether it exists. */
+static __device__ __forceinline__ const unsigned char *rg_tile(const aotx_rgemv_args &a,
+                                                               unsigned int group, unsigned int j,
+                                                               unsigned int rt, unsigned int expert,
+                                                               unsigned int &quant_off_unused)
+{
+    (void)quant_off_unused;
+    unsigned int seg, tile;  /* tile index inside its segment's tensor */
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        seg = j < half ? 0u : 1u;
+        tile = group * half + (j < half ? j : j - half);
+    } else {
+        unsigned int v0 = (group * rt + j) * 16u;
+        unsigned int begin = 0u;
+        seg = 0u;
+        while (seg + 1u < a.nseg && v0 >= a.seg_end[seg]) {
+            begin = a.seg_end[seg];
+            seg += 1u;
+        }
+        tile = (v0 - begin) / 16u;
+        unsigned int seg_tiles = (a.seg_end[seg] - begin + 15u) / 16u;
+        if (tile >= seg_tiles) tile = seg_tiles - 1u;   /* past the last row: discarded */
+    }
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int seg_tiles = (a.n + 15u) / 16u;
+        if (tile >= seg_tiles) tile = seg_tiles - 1u;
+    }
+    return a.w[seg] + (unsigned long long)expert * a.expert_stride
+         + (unsigned long long)tile * a.qn * 2048ull;
+}
+
+/* Scale plane of the same tile: the quant plane of the whole tensor comes first. */
+static __device__ __forceinline__ const unsigned short *rg_scales(const aotx_rgemv_args &a,
+                                                                  unsigned int group, unsigned int j,
+                                                                  unsigned int rt, unsigned int expert)
+{
+    unsigned int seg, tile, seg_rows;
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        seg = j < half ? 0u : 1u;
+        tile = group * half + (j < half ? j : j - half);
+        seg_rows = a.n;
+    } else {
+        unsigned int v0 = (group * rt + j) * 16u;
+        unsigned int begin = 0u;
+        seg = 0u;
+        while (seg + 1u < a.nseg && v0 >= a.seg_end[seg]) {
+            begin = a.seg_end[seg];
+            seg += 1u;
+        }
+        tile = (v0 - begin) / 16u;
+        seg_rows = a.seg_end[seg] - begin;
+    }
+    unsigned long long tiles = (seg_rows + 15u) / 16u;
+    if (tile >= tiles) tile = (unsigned int)tiles - 1u;
+    const unsigned char *base = a.w[seg] + (unsigned long long)expert * a.expert_stride;
+    return (const unsigned short *)(base + tiles * a.qn * 2048ull)
+         + (unsigned long long)tile * a.qn * 64ull;
+}
+
+/* The virtual output row of row rr of tile j (SWIGLU: the gate/up row index). */
+static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a, unsigned int group,
+                                                       unsigned int j, unsigned int rr, unsigned int rt)
+{
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        return (group * half + (j < half ? j : j - half)) * 16u + rr;
+    }
+    return (group * rt + j) * 16u + rr;
+}
+
+/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. */
+template <int MT>
+static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
+                                                   unsigned int group, unsigned int rt,
+                                                   unsigned int mrows, const unsigned int *list)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned int gr = rt * 16u;
+#define RG_YROW(mm) (list != nullptr ? list[(mm)] : a.m0 + (mm))
+    if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr) {
+        /* one thread per (tile, row of x): add the 16 results of the tile into the residual
+         * stream and leave the tile's sum of squares for the next norm */
+        for (unsigned int idx = tid; idx < rt * MT; idx += RG_THREADS) {
+            unsigned int j = idx % rt, mm = idx / rt;
+            unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
+            if (mm >= mrows || v0 >= a.n) continue;
+            float *row = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0;
+            float s = 0.0f;
+            for (unsigned int rr = 0; rr < 16u && v0 + rr < a.n; ++rr) {
+                float v = row[rr] + out[(j * 16u + rr) * MT + mm];
+                row[rr] = v;
+                s += v * v;
+            }
+            a.sumsq_out[(unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u] = s;
+        }
+    } else if (a.epi == AOTX_EPI_F32 || a.epi == AOTX_EPI_F16 || a.epi == AOTX_EPI_RESID) {
+        for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) {
+            unsigned int row = idx % gr, mm = idx / gr;
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            float val = out[row * MT + mm];
+            unsigned long long at = (unsigned long long)RG_YROW(mm) * a.ldy + v;
+            if (a.epi == AOTX_EPI_F32) ((float *)a.y)[at] = val;
+            else if (a.epi == AOTX_EPI_F16) ((unsigned short *)a.y)[at] = aotx_f2h(val);
+            else ((float *)a.y)[at] += val;
+        }
+    } else if (a.epi == AOTX_EPI_SWIGLU) {
+        const unsigned int half = rt / 2u;
+        for (unsigned int idx = tid; idx < half * 16u * MT; idx += RG_THREADS) {
+            unsigned int row = idx % (half * 16u), mm = idx / (half * 16u);
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            float gate = out[row * MT + mm];
+            float up = out[(row + half * 16u) * MT + mm];
+            float unit = gate / (1.0f + expf(-gate));
+            ((unsigned short *)a.y)[(unsigned long long)RG_YROW(mm) * a.ldy + v] = aotx_f2h(unit * up);
+        }
+    } else if (a.epi == AOTX_EPI_QKV) {
+        const aotx_qkv_epi &e = a.qkv;
+        const unsigned int d = e.head_dim;
+        const float step = powf(e.theta, -2.0f / (float)d);
+        for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += RG_THREADS) {
+            unsigned int pr = idx % (gr / 2u), mm = idx / (gr / 2u);
+            unsigned int row = 2u * pr;
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            unsigned int sg = 0u, begin = 0u;
+            while (sg + 1u < a.nseg && v >= a.seg_end[sg]) {
+                begin = a.seg_end[sg];
+                sg += 1u;
+            }
+            unsigned int local = v - begin;
+            unsigned int t = a.m0 + mm;
+            float a0 = out[row * MT + mm];
+            float a1 = out[(row + 1u) * MT + mm];
+            unsigned int head = local / d;
+            unsigned int dim = local - head * d;
+            unsigned int position = e.pos[t];
+            if (sg == 0u) {
+                float angle = (float)position * powf(step, (float)(dim >> 1));
+                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                unsigned short *dst = e.qh + (unsigned long long)t * e.heads * d + local;
+                dst[0] = aotx_f2h(a0 * cs - a1 * sn);
+                dst[1] = aotx_f2h(a0 * sn + a1 * cs);
+                continue;
+            }
+            unsigned char *blk = aotx_kvl_block(e.shape, &e.state->kv, e.agent[t], e.layer, position);
+            if (blk == nullptr) {
+                if (dim == 0u && sg == 1u) atomicAdd(&e.state->faults, 1u);
+                continue;
+            }
+            unsigned int krow = (sg == 1u ? head : e.kv_heads + head) * AOTX_KVL_BLOCK
+                              + position % AOTX_KVL_BLOCK;
+            unsigned short *dst = (unsigned short *)blk + (unsigned long long)krow * d + dim;
+            if (sg == 1u) {
+                float angle = (float)position * powf(step, (float)(dim >> 1));
+                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                dst[0] = aotx_f2h(a0 * cs - a1 * sn);
+                dst[1] = aotx_f2h(a0 * sn + a1 * cs);
+            } else {
+                dst[0] = aotx_f2h(a0);
+                dst[1] = aotx_f2h(a1);
+            }
+        }
+    }
+#undef RG_YROW
+}
+
+/* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
+ * loaded ahead per wave. */
+template <int MT, int RT, int PD>
+__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
+{
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
+    const unsigned int expert = blockIdx.y;
+    const unsigned int *list = nullptr;
+    unsigned int mrows = a.m;
+    if (a.expert_stride != 0ull) {
+        unsigned int total = a.list_count[expert];
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+        list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
+    } else if (a.m_dev != nullptr) {
+        unsigned int total = *a.m_dev;
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+    if (mrows == 0u) return;
+
+    const unsigned int group = blockIdx.x / a.splits;
+    const unsigned int split = blockIdx.x % a.splits;
+    const unsigned int q0 = split * a.qps;
+    const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
+    const unsigned int kr = a.qps * 128u;          /* LDS k capacity */
+    const unsigned int xs = kr + 8u;               /* LDS x row stride (halves) */
+    unsigned short *xl = (unsigned short *)lds;
+
+    /* ---- stage the batch rows of x for [q0, q1) ---- */
+    {
+        const unsigned int kbeg = q0 * 128u;
+        const unsigned int kend = q1 * 128u;
+        const unsigned int width = kend - kbeg;          /* multiple of 128 */
+        const unsigned int pieces = width / 8u;          /* 16-byte pieces per row */
+        if (a.xmode == AOTX_X_NORM) {
+            __shared__ float share[4];
+            const unsigned int nss = (a.k + 15u) / 16u;
+            for (unsigned int mm = 0; mm < mrows; ++mm) {
+                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
+                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+                const float *ss = a.sumsq + (unsigned long long)src * nss;
+                float sum = 0.0f;
+                for (unsigned int i = tid; i < nss; i += RG_THREADS) sum += ss[i];
+                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                if (lane == 0u) share[wave] = sum;
+                __syncthreads();
+                sum = share[0] + share[1] + share[2] + share[3];
+                __syncthreads();
+                const float scale = rsqrtf(sum / (float)a.k + a.eps);
+                const float *r = a.resid + (unsigned long long)src * a.k;
+                for (unsigned int p = tid; p < pieces; p += RG_THREADS) {
+                    unsigned int kk = kbeg + p * 8u;
+                    unsigned int h[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        unsigned int kc = kk + (unsigned int)e;
+                        h[e] = kc < a.k ? aotx_f2h(scale * r[kc] * a.norm_w[kc]) : 0u;
+                    }
+                    rg_u4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                               h[6] | (h[7] << 16)};
+                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+                }
+            }
+        } else {
+            for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
+                unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
+                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+                unsigned int kk = kbeg + p * 8u;
+                rg_u4 v = {0u, 0u, 0u, 0u};
+                if (kk + 8u <= a.k) {
+                    v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
+                } else if (kk < a.k) {
+                    unsigned int h[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
+                    v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                h[6] | (h[7] << 16)};
+                }
+                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+            }
+        }
+        __syncthreads();
+    }
+
+    /* ---- per-wave k quarter ---- */
+    const unsigned int nq = q1 - q0;
+    const unsigned int per = (nq + 3u) / 4u;
+    const unsigned int wq0 = q0 + wave * per < q1 ? q0 + wave * per : q1;
+    const unsigned int wq1 = wq0 + per < q1 ? wq0 + per : q1;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+
+    const unsigned char *qb[RT];
+    const unsigned short *sb[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        unsigned int dummy = 0u;
+        qb[j] = rg_tile(a, group, (unsigned int)j, RT, expert, dummy) + lane * 32u;
+        sb[j] = rg_scales(a, group, (unsigned int)j, RT, expert) + lane;
+    }
+
+    rg_f4 acc[RT][MT / 16];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    rg_u4 wa[2][PD][RT][2];
+    unsigned short ws[2][PD][RT];
+
+#define RG_LOAD(BUF, QS)                                                                 \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = (QS) + (unsigned int)qi;                                   \
+            if (qq >= wq1) qq = wq1 - 1u;                                                \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
+                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 1);                \
+                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+#define RG_COMPUTE(BUF, QS)                                                              \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = (QS) + (unsigned int)qi;                                   \
+            if (qq < wq1) {                                                              \
+                const unsigned short *xq = xl + (qq - q0) * 128u + 32u * g;             \
+                rg_h8 B[MT / 16][4];                                                     \
+                _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                    \
+                    unsigned int mm = (unsigned int)t * 16u + r;                         \
+                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
+                        B[t][s] = mm < mrows ? *(const rg_h8 *)(xq + mm * xs + 8u * s)   \
+                                             : (rg_h8){0, 0, 0, 0, 0, 0, 0, 0};          \
+                    }                                                                    \
+                }                                                                        \
+                _Pragma("unroll") for (int j = 0; j < RT; ++j) {                         \
+                    unsigned int sbits = ws[BUF][qi][j];                                 \
+                    rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));         \
+                    const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];        \
+                    unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                \
+                                          q1v[0], q1v[1], q1v[2], q1v[3]};               \
+                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
+                        unsigned int d0, d1, d2, d3;                                     \
+                        rg_dequant4(qd[2 * s], s2, d0, d1);                              \
+                        rg_dequant4(qd[2 * s + 1], s2, d2, d3);                          \
+                        rg_u4 av = {d0, d1, d2, d3};                                     \
+                        rg_h8 A = __builtin_bit_cast(rg_h8, av);                         \
+                        _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {            \
+                            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(           \
+                                A, B[t][s], acc[j][t], 0, 0, 0);                         \
+                        }                                                                \
+                    }                                                                    \
+                }                                                                        \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+    if (wq0 < wq1) {
+        unsigned int q = wq0;
+        RG_LOAD(0, q);
+        for (;;) {
+            unsigned int qn1 = q + PD;
+            if (qn1 < wq1) RG_LOAD(1, qn1);
+            RG_COMPUTE(0, q);
+            q = qn1;
+            if (q >= wq1) break;
+            unsigned int qn2 = q + PD;
+            if (qn2 < wq1) RG_LOAD(0, qn2);
+            RG_COMPUTE(1, q);
+            q = qn2;
+            if (q >= wq1) break;
+        }
+    }
+#undef RG_LOAD
+#undef RG_COMPUTE
+
+    /* ---- add the 4 waves' accumulators in wave order ---- */
+    __syncthreads();
+    float *part = (float *)lds;                      /* [4][RT*16][MT] */
+    const unsigned int gr = RT * 16u;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                unsigned int row = (unsigned int)j * 16u + 4u * g + (unsigned int)i;
+                part[(wave * gr + row) * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
+            }
+    __syncthreads();
+    float *out = part + 4u * gr * MT;
+    for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) {
+        out[idx] = part[idx] + part[gr * MT + idx] + part[2u * gr * MT + idx] + part[3u * gr * MT + idx];
+    }
+    __syncthreads();
+    if (a.splits > 1u) {
+        float *mine = a.partial
+            + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
+        for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) mine[idx] = out[idx];
+        return;
+    }
+    rg_epilogue<MT>(a, out, group, RT, mrows, list);
+}
+
+/* Add the split partials of one workgroup's rows in split order, then the epilogue. */
+template <int MT>
+__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args a)
+{
+    __shared__ float out[64 * MT];
+    const unsigned int expert = blockIdx.y;
+    const unsigned int *list = nullptr;
+    unsigned int mrows = a.m;
+    if (a.expert_stride != 0ull) {
+        unsigned int total = a.list_count[expert];
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+        list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
+    } else if (a.m_dev != nullptr) {
+        unsigned int total = *a.m_dev;
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+    if (mrows == 0u) return;
+    const unsigned int group = blockIdx.x;
+    const unsigned int gr = a.rt * 16u;
+    const float *all = a.partial
+        + ((unsigned long long)expert * a.groups + group) * a.splits * gr * MT;
+    for (unsigned int idx = threadIdx.x; idx < gr * MT; idx += RG_THREADS) {
+        float sum = 0.0f;
+        for (unsigned int sp = 0; sp < a.splits; ++sp) sum += all[(unsigned long long)sp * gr * MT + idx];
+        out[idx] = sum;
+    }
+    __syncthreads();
+    rg_epilogue<MT>(a, out, group, a.rt, mrows, list);
+}
+
+/* ---- host ---------------------------------------------------------------------------- */
+
+static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
+{
+    size_t x = (size_t)a.m * (a.qps * 128u + 8u) * 2u;
+    size_t red = (size_t)5u * a.rt * 16u * mt * 4u;
+    return x > red ? x : red;
+}
+
+int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                    unsigned int nseg, unsigned int k, int epi, unsigned int mt)
+{
+    memset(a, 0, sizeof *a);
+    if (k == 0u || k % 32u != 0u || nseg == 0u || nseg > 3u || mt == 0u || mt > 32u) return 1;
+    a->m = mt;
+    a->k = k;
+    a->qn = (unsigned int)aotx_q8r_quads(k);
+    a->nseg = nseg;
+    a->epi = epi;
+    unsigned int total = 0u;
+    for (unsigned int s = 0; s < nseg; ++s) {
+        if (rows[s] == 0u || w[s] == nullptr) return 1;
+        a->w[s] = (const unsigned char *)w[s];
+        total += rows[s];
+        a->seg_end[s] = total;
+        if (s + 1u < nseg && rows[s] % 16u != 0u) return 1;
+    }
+    unsigned int tiles;
+    if (epi == AOTX_EPI_SWIGLU) {
+        if (nseg != 2u || rows[0] != rows[1]) return 1;
+        a->n = rows[0];
+        tiles = 2u * (unsigned int)aotx_q8r_tiles(rows[0]);
+    } else {
+        a->n = total;
+        tiles = (total + 15u) / 16u;
+    }
+    /* rows per workgroup: gate/up pairs need an even tile count. Wide batches take 4 tiles
+     * (each workgroup stages its x range once for 64 rows); narrow ones take fewer tiles
+     * while that leaves fewer than ~1024 workgroups. */
+    unsigned int rt;
+    if (mt > 8u) rt = 4u;
+    else if (tiles >= 4u * 1024u) rt = 4u;
+    else if (tiles >= 2u * 1024u) rt = 2u;
+    else rt = 1u;
+    if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
+    a->rt = rt;
+    if (epi == AOTX_EPI_SWIGLU) {
+        unsigned int half_tiles = (unsigned int)aotx_q8r_tiles(rows[0]);
+        a->groups = (half_tiles + rt / 2u - 1u) / (rt / 2u);
+    } else {
+        a->groups = (tiles + rt - 1u) / rt;
+    }
+    /* k split: the staged x rows of a workgroup's k range fit 96 KB of LDS; split further
+     * while there are fewer than 256 workgroups and a split keeps >= 8 quads */
+    unsigned int kmax = 98304u / (mt * 256u);
+    if (kmax < 1u) kmax = 1u;
+    unsigned int s = (a->qn + kmax - 1u) / kmax;
+    while (a->groups * s < 256u && (a->qn + s) / (s + 1u) >= 8u) s += 1u;
+    a->qps = (a->qn + s - 1u) / s;
+    a->splits = (a->qn + a->qps - 1u) / a->qps;
+    return 0;
+}
+
+size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
+{
+    size_t e = a.expert_stride != 0ull ? a.experts : 1u;
+    return a.splits > 1u ? e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float) : 0u;
+}
+
+template <int MT, int RT>
+static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
+{
+    constexpr int PD = RT == 1 ? 4 : (RT == 2 ? 2 : 1);
+    unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
+    size_t lds = aotx_rgemv_lds(a, MT);
+    hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD>), dim3(a.groups * a.splits, ey), dim3(RG_THREADS),
+                       lds, s, a);
+    AOTX_LAUNCH_CHECK();
+    if (a.splits > 1u) {
+        hipLaunchKernelGGL((aotx_rgemv_reduce<MT>), dim3(a.groups, ey), dim3(RG_THREADS), 0, s, a);
+        AOTX_LAUNCH_CHECK();
+    }
+}
+
+void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
+{
+    aotx_rgemv_args a = a0;
+    if (a.splits > 1u && a.partial == nullptr) {
+        a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
+    }
+    const unsigned int mt = a.m <= 16u ? 16u : 32u;
+    if (mt == 16u) {
+        if (a.rt == 1u) aotx_rgemv_go<16, 1>(a, s);
+        else if (a.rt == 2u) aotx_rgemv_go<16, 2>(a, s);
+        else aotx_rgemv_go<16, 4>(a, s);
+    } else {
+        if (a.rt == 1u) aotx_rgemv_go<32, 1>(a, s);
+        else if (a.rt == 2u) aotx_rgemv_go<32, 2>(a, s);
+        else aotx_rgemv_go<32, 4>(a, s);
+    }
+}
+
+/* ---- kernel-level C ABI ---------------------------------------------------------------- */
+
+extern "C" unsigned long long aotx_q8r_size(unsigned int n, unsigned int k)
+{
+    if (n == 0u || k == 0u || k % 32u != 0u) return 0ull;
+    return aotx_q8r_bytes(n, k);
+}
+
+extern "C" int aotx_q8_repack(const void *w, unsigned int n, unsigned int k, void *dst,
+                              void *stream)
+{
+    if (w == nullptr || dst == nullptr || n == 0u || k == 0u || k % 32u != 0u) return 1;
+    aotx_q8r_repack(w, n, k, dst, aotx_stream(stream));
+    return 0;
+}
+
+static int aotx_q8r_gemv_any(const void *wr, unsigned int n, unsigned int k, const void *x,
+                             unsigned int m, void *y, int epi, void *stream)
+{
+    if (wr == nullptr || x == nullptr || y == nullptr || n == 0u || m == 0u) return 1;
+    if (k == 0u || k % 32u != 0u || k % 8u != 0u) return 1;
+    const void *ws[1] = {wr};
+    unsigned int rows[1] = {n};
+    for (unsigned int m0 = 0; m0 < m; m0 += 32u) {
+        unsigned int mt = m - m0 < 32u ? m - m0 : 32u;
+        aotx_rgemv_args a;
+        if (aotx_rgemv_plan(&a, ws, rows, 1u, k, epi, mt) != 0) return 1;
+        a.xmode = AOTX_X_F16;
+        a.x = (const unsigned short *)x;
+        a.ldx = k;
+        a.m0 = m0;
+        a.y = y;
+        a.ldy = n;
+        aotx_rgemv_launch(a, aotx_stream(stream));
+    }
+    return 0;
+}
+
+extern "C" int aotx_q8r_gemv(const void *wr, unsigned int n, unsigned int k, const void *x,
+                             unsigned int m, float *y, void *stream)
+{
+    return aotx_q8r_gemv_any(wr, n, k, x, m, y, AOTX_EPI_F32, stream);
+}
+
+extern "C" int aotx_q8r_gemv_f16(const void *wr, unsigned int n, unsigned int k, const void *x,
+                                 unsigned int m, void *y, void *stream)
+{
+    return aotx_q8r_gemv_any(wr, n, k, x, m, y, AOTX_EPI_F16, stream);
+}

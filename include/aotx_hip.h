@@ -321,6 +321,20 @@ int aotx_q8_gemv(const void *w, unsigned int n, unsigned int k, const void *x,
 int aotx_q8_gemv_f16(const void *w, unsigned int n, unsigned int k, const void *x,
                      unsigned int m, void *y, void *stream);
 
+/* The repacked form the model path streams (no counterpart in the reference, whose weights
+ * stay in the file's layout). Same bytes per weight (int8 + one fp16 scale per 32),
+ * reordered so one wave reads its matrix-core operands with coalesced 16-byte loads:
+ * [n/16 tiles][k/128 quads][64 lanes][32 quants] then [tiles][quads][64 lanes] scales
+ * (lane = row % 16 + 16 * block-in-quad; the last tile and quad are zero padded).
+ * aotx_q8r_size gives the bytes; aotx_q8_repack converts; aotx_q8r_gemv(_f16) is the
+ * product over the repacked tensor with the arguments of aotx_q8_gemv. */
+unsigned long long aotx_q8r_size(unsigned int n, unsigned int k);
+int aotx_q8_repack(const void *w, unsigned int n, unsigned int k, void *dst, void *stream);
+int aotx_q8r_gemv(const void *wr, unsigned int n, unsigned int k, const void *x,
+                  unsigned int m, float *y, void *stream);
+int aotx_q8r_gemv_f16(const void *wr, unsigned int n, unsigned int k, const void *x,
+                      unsigned int m, void *y, void *stream);
+
 /* Dequantize rows of a Q8_0 tensor to fp16 (cuda/model/dequant.cu:9-70). */
 int aotx_q8_dequant(const void *w, unsigned int k, unsigned int first_row,
                     unsigned int rows, void *out, void *stream);

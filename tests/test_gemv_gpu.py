@@ -97,3 +97,71 @@ def test_device_synth_equals_host(torch, lib):
     host = np.empty(n * (k // 32) * 34, dtype=np.uint8)
     lib.aotx_synth_q8_host(host.ctypes.data_as(ctypes.c_void_p), n, k, 0.02, 0xABCDEF, 4)
     assert np.array_equal(w.cpu().numpy(), host)
+
+
+def repack(torch, lib, w, n, k):
+    size = lib.aotx_q8r_size(n, k)
+    assert size > 0
+    wr = torch.empty(size, dtype=torch.uint8, device="cuda")
+    assert lib.aotx_q8_repack(p(w), n, k, p(wr), None) == 0
+    return wr
+
+
+@pytest.mark.parametrize("n,k", [(64, 256), (128, 704), (80, 128), (1000, 4096), (256, 14336),
+                                 (17, 96)])
+@pytest.mark.parametrize("m", [1, 3, 8, 16, 17, 32, 40])
+def test_repacked_gemv_small_full(torch, lib, orc, n, k, m):
+    """The streaming product over repacked weights (the model path) vs the oracle."""
+    w = make(torch, lib, n, k, 11 + n + k)
+    wr = repack(torch, lib, w, n, k)
+    rng = np.random.default_rng(n * 7 + m)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16)
+    y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+    assert lib.aotx_q8r_gemv(p(wr), n, k, p(dev(x, torch)), m, p(y), None) == 0
+    torch.cuda.synchronize()
+    want = orc.q8_gemv_f64(w.cpu().numpy(), n, k, x.view(np.uint16))
+    assert rel_rms(y.cpu().numpy().reshape(m, n), want) < TOL
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)])
+@pytest.mark.parametrize("m", [1, 4, 8, 32])
+def test_repacked_gemv_benchmark_shapes(torch, lib, orc, n, k, m):
+    w = make(torch, lib, n, k, 4321)
+    wr = repack(torch, lib, w, n, k)
+    rng = np.random.default_rng(m + 100)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16)
+    xd = dev(x, torch)
+    y = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+    y2 = torch.zeros(m * n, dtype=torch.float32, device="cuda")
+    assert lib.aotx_q8r_gemv(p(wr), n, k, p(xd), m, p(y), None) == 0
+    assert lib.aotx_q8_gemv(p(w), n, k, p(xd), m, p(y2), None) == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(m, n)
+    wn = w.cpu().numpy().reshape(n, -1)
+    rows = rng.integers(0, n, 64)
+    want = orc.q8_gemv_f64(np.ascontiguousarray(wn[rows]), 64, k, x.view(np.uint16))
+    rms = np.sqrt((want ** 2).mean())
+    assert (np.abs(got[:, rows] - want) / np.maximum(np.abs(want), rms)).max() < TOL
+    # both kernels sum the same fp16 products in fp32: they agree far inside the tolerance
+    assert rel_rms(got, y2.cpu().numpy().reshape(m, n)) < 1e-4
+
+
+def test_repack_layout(torch, lib):
+    """Repacked bytes: lane l = r + 16 g of (tile t, quad q) holds row 16t + r, block 4q + g."""
+    n, k = 40, 384
+    w = make(torch, lib, n, k, 3)
+    wr = repack(torch, lib, w, n, k).cpu().numpy()
+    src = w.cpu().numpy().reshape(n, k // 32, 34)
+    tiles, quads = (n + 15) // 16, (k + 127) // 128
+    quant = wr[:tiles * quads * 64 * 32].reshape(tiles, quads, 64, 32)
+    scale = wr[tiles * quads * 64 * 32:].view(np.uint16).reshape(tiles, quads, 64)
+    for t in range(tiles):
+        for q in range(quads):
+            for lane in range(64):
+                r, g = lane % 16, lane // 16
+                row, blk = 16 * t + r, 4 * q + g
+                if row < n and blk < k // 32:
+                    assert np.array_equal(quant[t, q, lane], src[row, blk, 2:])
+                    assert scale[t, q, lane] == src[row, blk, :2].view(np.uint16)[0]
+                else:
+                    assert not quant[t, q, lane].any() and scale[t, q, lane] == 0
