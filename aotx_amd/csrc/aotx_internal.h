@@ -49,6 +49,7 @@ enum {
     AOTX_SCRATCH_ATTN_PARTIAL,
     AOTX_SCRATCH_ATTN_COUNT,
     AOTX_SCRATCH_EXPERT,
+    AOTX_SCRATCH_PICK,
     AOTX_SCRATCH_KINDS
 };
 

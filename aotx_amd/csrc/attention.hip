@@ -5,24 +5,27 @@
  * 1/sqrt(d), fp32 sums, out = half(sum / mass); keys and values come from the 16-position
  * layout blocks of cuda/model/kv_layout.cuh. Each query head re-reads its KV head there.
  *
- * Here one wave takes (token, KV head, context chunk):
+ * Here one workgroup of 4 waves takes (token, KV head, context chunk):
  *   - all G = heads / kv_heads query heads of the KV head share one read of its keys and
  *     values (grouped-query sharing: the KV bytes are read once per token, not G times);
- *   - 8 lanes hold one position: lane (grp = lane / 8, sub = lane % 8) reads the 16-byte
- *     pieces 8*sub and 64 + 8*sub of a 128-element row, so 8 positions of one layout block
- *     are read per instruction pair and every byte of the block is consumed;
- *   - pass 1 writes the scaled scores of the chunk to LDS; the chunk maximum and the
- *     exponentials follow; pass 2 reads the value rows once and accumulates;
- *   - the context is split over several waves (flash-decoding) so that a batch of one
- *     still covers the GPU; each chunk leaves (max, mass, unnormalised sum) and a merge
- *     kernel adds the chunks of a (token, KV head) in chunk order, so the result does not
- *     depend on timing.
+ *   - d/8 lanes hold one position, one 16-byte piece of the row each, so a wave step
+ *     covers one whole 16-position layout block (4 KB of keys and 4 KB of values at
+ *     d = 128) with fully used 16-byte loads, and the next block's loads are issued before
+ *     the current block is computed;
+ *   - scores are fp16 x fp16 products summed in fp32 (v_dot2_f32_f16), reduced over the
+ *     row's lanes with lane shuffles; online softmax per block in base 2 (scores carry
+ *     log2(e) / sqrt(d)), values accumulated in fp32;
+ *   - the 4 waves' (max, mass, sum) are merged in wave order through LDS; the context is
+ *     split over workgroups (flash-decoding) so that a batch of one still covers the GPU,
+ *     and a merge kernel adds the chunks of a (token, KV head) in chunk order, so the
+ *     result does not depend on timing.
  */
 #include "aotx_internal.h"
 
 #include <algorithm>
 
 typedef unsigned int aotx_u4a __attribute__((ext_vector_type(4)));
+typedef _Float16 aotx_h2a __attribute__((ext_vector_type(2)));
 
 struct aotx_attn_args {
     const unsigned short *q;      /* fp16 [tokens][heads][d] */
@@ -41,34 +44,69 @@ struct aotx_attn_args {
     float *partial;               /* [tokens*kv_heads][splits][G*(d+2)] */
 };
 
-#define ATTN_UNROLL 4          /* positions per lane group per block: 32 per wave */
-#define ATTN_CHUNK_ALIGN 128u  /* a chunk is a whole number of 4-wave blocks */
+#define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
 #define ATTN_MAX_SPLITS 64u
+#define ATTN_TARGET_GROUPS 2048u
 
 static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 {
     return aotx_h2f((unsigned short)(hi ? (word >> 16) : (word & 0xFFFFu)));
 }
 
-/* One workgroup = 4 waves = one (token, KV head, context chunk). Each wave takes a
- * quarter of the chunk in blocks of 32 positions (8 lane groups x 4), loads the key and
- * value rows of a block together, and keeps a running maximum and mass (online softmax,
- * as cuda/model/attention.cu:90-104, per block instead of per position). The 4 waves'
- * (max, mass, sum) are merged in wave order through LDS; a chunk that is not the whole
- * context leaves its merged triple for the merge kernel. */
-template <int D, int G>
-__global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
+/* fp16 pair from one 32-bit word. The word arrives by value: a __builtin_bit_cast of a
+ * vector element (v[e]) directly is miscompiled by this hipcc (it reads element 0). */
+static __device__ __forceinline__ aotx_h2a aotx_as_h2(unsigned int word)
 {
-    constexpr int NP = D / 64;          /* 16-byte pieces per lane per row */
-    constexpr int E = 8 * NP;           /* elements per lane */
-    constexpr int U = ATTN_UNROLL;      /* positions per lane group per block */
+    return __builtin_bit_cast(aotx_h2a, word);
+}
+
+template <int CTRL>
+static __device__ __forceinline__ float aotx_dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+
+/* Sum over aligned groups of LPP (8 or 16) lanes, every lane of a group left with the
+ * same total: quad swaps, then the mirrors within 8 and within 16. */
+template <int LPP>
+static __device__ __forceinline__ float aotx_row_sum(float v)
+{
+    v += aotx_dpp<0xB1>(v);     /* quad_perm [1,0,3,2] */
+    v += aotx_dpp<0x4E>(v);     /* quad_perm [2,3,0,1] */
+    v += aotx_dpp<0x141>(v);    /* row_half_mirror */
+    if (LPP == 16) v += aotx_dpp<0x140>(v);    /* row_mirror */
+    return v;
+}
+
+/* Chunk length of a token with n positions under S splits (whole 64-position units). */
+static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, unsigned int S)
+{
+    unsigned int chunk = (n + S - 1u) / S;
+    return (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
+}
+
+template <int D>
+struct aotx_attn_geom {
+    static constexpr int LPP = D / 8;          /* lanes per position */
+    static constexpr int NG = 64 / LPP;        /* positions per wave instruction */
+    static constexpr int U = 16 / NG;          /* instructions per 16-position block */
+};
+
+/* One workgroup = 4 waves = one (token, KV head, context chunk). */
+template <int D, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 : (G == 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
+{
+    constexpr int LPP = aotx_attn_geom<D>::LPP;
+    constexpr int NG = aotx_attn_geom<D>::NG;
+    constexpr int U = aotx_attn_geom<D>::U;
     __shared__ float wm[4][G], wl[4][G];
     __shared__ float wo[4][G][D];
 
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
-    const unsigned int grp = lane >> 3;
-    const unsigned int sub = lane & 7u;
+    const unsigned int grp = lane / LPP;
+    const unsigned int sub = lane % LPP;
     unsigned int tokens = a.m_dev ? *a.m_dev : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
     const unsigned int S = a.splits;
@@ -78,159 +116,150 @@ __global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
     const unsigned int t = rest / a.kv_heads;
     if (t >= tokens) return;
     const unsigned int n = a.pos[t] + 1u;
-    unsigned int chunk = (n + S - 1u) / S;
-    chunk = (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
+    const unsigned int chunk = aotx_attn_chunk(n, S);
     const unsigned int st = (n + chunk - 1u) / chunk;   /* chunks of this token */
     if (c >= st) return;
     const unsigned int p0 = c * chunk;
     const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
-    /* this wave's quarter, in whole blocks of 8 * U positions */
-    const unsigned int blk = 8u * U;
-    const unsigned int nblk = (p1 - p0 + blk - 1u) / blk;
+    /* this wave's quarter, in whole 16-position blocks */
+    const unsigned int nblk = (p1 - p0 + 15u) / 16u;
     const unsigned int per = (nblk + 3u) / 4u;
-    const unsigned int w0 = p0 + wave * per * blk;
-    const unsigned int w1 = (w0 + per * blk < p1) ? w0 + per * blk : p1;
+    const unsigned int b0 = p0 / 16u + wave * per;
+    unsigned int b1 = b0 + per;
+    if (b1 > (p1 + 15u) / 16u) b1 = (p1 + 15u) / 16u;
     const unsigned int agent = a.agent[t];
     const aotx_kv_table *kv = &a.state->kv;
-    const float scale = 1.0f / sqrtf((float)D);
+    /* base-2 scores: s * log2(e) / sqrt(d) */
+    const float scale = 1.4426950408889634f / sqrtf((float)D);
 
-    float qv[G][E];
+    aotx_h2a qv[G][4];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
         const unsigned short *qrow = a.q + ((unsigned long long)t * a.heads + kh * G + j) * D;
+        aotx_u4a w = *(const aotx_u4a *)(qrow + 8 * sub);
 #pragma unroll
-        for (int pc = 0; pc < NP; ++pc) {
-            aotx_u4a w = *(const aotx_u4a *)(qrow + 64 * pc + 8 * sub);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                qv[j][8 * pc + 2 * e] = aotx_attn_h(w[e], 0);
-                qv[j][8 * pc + 2 * e + 1] = aotx_attn_h(w[e], 1);
-            }
-        }
+        for (int e = 0; e < 4; ++e) qv[j][e] = aotx_as_h2(w[e]);
     }
-    float o[G][E];
+    float o[G][8];
     float mrun[G], lrun[G];
 #pragma unroll
     for (int j = 0; j < G; ++j) {
         mrun[j] = -INFINITY;
         lrun[j] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[j][e] = 0.0f;
+        for (int e = 0; e < 8; ++e) o[j][e] = 0.0f;
     }
     int missing = 0;
-    const unsigned int kbase = kh * AOTX_KVL_BLOCK;
-    const unsigned int vbase = (a.kv_heads + kh) * AOTX_KVL_BLOCK;
+    /* byte offsets of this lane's piece of row grp of the key and value heads */
+    const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
+    const unsigned int vbyte = (((a.kv_heads + kh) * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
 
-    for (unsigned int base = w0; base < w1; base += blk) {
-        aotx_u4a kr[U][NP], vr[U][NP];
-        bool valid[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            unsigned int p = base + 8u * u + grp;
-            valid[u] = p < w1;
-            unsigned int pp = valid[u] ? p : w0;
-            const unsigned char *bk = aotx_kvl_block(a.shape, kv, agent, a.layer, pp);
-            const bool absent = bk == nullptr;
-            if (absent) {
-                missing = 1;
-                valid[u] = false;
-                bk = (const unsigned char *)a.q;    /* readable; replaced by zeros below */
-            }
-            const unsigned short *krow = (const unsigned short *)bk
-                + (absent ? 0ull : (unsigned long long)(kbase + pp % AOTX_KVL_BLOCK) * D);
-            const unsigned short *vrow = (const unsigned short *)bk
-                + (absent ? 0ull : (unsigned long long)(vbase + pp % AOTX_KVL_BLOCK) * D);
-            const aotx_u4a zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int pc = 0; pc < NP; ++pc) {
-                aotx_u4a kk = *(const aotx_u4a *)(krow + (absent ? 0 : 64 * pc + 8 * sub));
-                aotx_u4a vv = *(const aotx_u4a *)(vrow + (absent ? 0 : 64 * pc + 8 * sub));
-                kr[u][pc] = absent ? zero : kk;
-                vr[u][pc] = absent ? zero : vv;
-            }
-        }
-        float sc[U][G];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int j = 0; j < G; ++j) sc[u][j] = 0.0f;
-#pragma unroll
-            for (int pc = 0; pc < NP; ++pc) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float k0 = aotx_attn_h(kr[u][pc][e], 0);
-                    float k1 = aotx_attn_h(kr[u][pc][e], 1);
-#pragma unroll
-                    for (int j = 0; j < G; ++j) {
-                        sc[u][j] += qv[j][8 * pc + 2 * e] * k0;
-                        sc[u][j] += qv[j][8 * pc + 2 * e + 1] * k1;
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-                float v = sc[u][j];
-                v += __shfl_xor(v, 1, 64);
-                v += __shfl_xor(v, 2, 64);
-                v += __shfl_xor(v, 4, 64);
-                sc[u][j] = valid[u] ? v * scale : -INFINITY;
-            }
-        }
-        /* block maximum over the wave's 8 * U positions */
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            float mb = sc[0][j];
-#pragma unroll
-            for (int u = 1; u < U; ++u) mb = fmaxf(mb, sc[u][j]);
-            mb = fmaxf(mb, __shfl_xor(mb, 8, 64));
-            mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-            float mnew = fmaxf(mrun[j], mb);
-            float shift = (mrun[j] == -INFINITY) ? 0.0f : expf(mrun[j] - mnew);
-            if (mnew == -INFINITY) shift = 1.0f;
-            lrun[j] *= shift;
-#pragma unroll
-            for (int e = 0; e < E; ++e) o[j][e] *= shift;
-            mrun[j] = mnew;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float pw[G];
-#pragma unroll
-            for (int j = 0; j < G; ++j) {
-                pw[j] = (sc[u][j] == -INFINITY) ? 0.0f : expf(sc[u][j] - mrun[j]);
-                lrun[j] += pw[j];
-            }
-#pragma unroll
-            for (int pc = 0; pc < NP; ++pc) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float v0 = aotx_attn_h(vr[u][pc][e], 0);
-                    float v1 = aotx_attn_h(vr[u][pc][e], 1);
-#pragma unroll
-                    for (int j = 0; j < G; ++j) {
-                        o[j][8 * pc + 2 * e] += pw[j] * v0;
-                        o[j][8 * pc + 2 * e + 1] += pw[j] * v1;
-                    }
-                }
-            }
+    aotx_u4a kr[2][U], vr[2][U];
+    bool absent[2];
+    /* layout-block pointers of the wave's blocks, 64 at a time, lane i holding block
+     * wbase + i; a block is fetched from the lane that holds it */
+    unsigned long long pages = 0ull;
+    unsigned int wbase = b0;
+#define ATTN_WINDOW(B0)                                                                     \
+    do {                                                                                    \
+        wbase = (B0);                                                                       \
+        unsigned int bl = wbase + lane;                                                     \
+        pages = bl < b1 ? (unsigned long long)aotx_kvl_block(a.shape, kv, agent, a.layer, bl * 16u) \
+                        : 0ull;                                                             \
+    } while (0)
+#define ATTN_LOAD(BUF, B)                                                                   \
+    do {                                                                                    \
+        if ((B) - wbase >= 64u) ATTN_WINDOW(B);                                             \
+        unsigned long long pb = __shfl(pages, (int)((B) - wbase), 64);                     \
+        /* the block is the same for the whole wave: its address goes to scalar registers, \
+         * as a buffer resource whose range is empty for a missing page (loads give 0) */   \
+        pb = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb >> 32)) << 32) \
+           | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb); \
+        absent[BUF] = pb == 0ull;                                                           \
+        __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
+            (void *)pb, (short)0, absent[BUF] ? 0 : (int)a.shape.block_bytes, 0x00020000);  \
+        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
+            kr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + u * NG * D * 2, 0, 0); \
+            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * NG * D * 2, 0, 0); \
+        }                                                                                   \
+    } while (0)
+
+#define ATTN_COMPUTE(BUF, B)                                                                \
+    do {                                                                                    \
+        if (absent[BUF]) missing = 1;                                                       \
+        float sc[U][G];                                                                     \
+        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
+            unsigned int p = (B) * 16u + (unsigned int)u * NG + grp;                        \
+            bool ok = p >= p0 && p < p1 && !absent[BUF];                                    \
+            aotx_u4a kk = kr[BUF][u];                                                       \
+            _Pragma("unroll") for (int j = 0; j < G; ++j) {                                 \
+                float v = 0.0f;                                                             \
+                _Pragma("unroll") for (int e = 0; e < 4; ++e)                               \
+                    v = __builtin_amdgcn_fdot2(qv[j][e], aotx_as_h2(kk[e]), v, false);       \
+                v = aotx_row_sum<LPP>(v);                                                   \
+                sc[u][j] = ok ? v * scale : -INFINITY;                                      \
+            }                                                                               \
+        }                                                                                   \
+        _Pragma("unroll") for (int j = 0; j < G; ++j) {                                     \
+            float mb = sc[0][j];                                                            \
+            _Pragma("unroll") for (int u = 1; u < U; ++u) mb = fmaxf(mb, sc[u][j]);         \
+            _Pragma("unroll") for (int off = LPP; off < 64; off <<= 1)                      \
+                mb = fmaxf(mb, __shfl_xor(mb, off, 64));                                    \
+            float mnew = fmaxf(mrun[j], mb);                                                \
+            if (mnew != mrun[j]) {                                                          \
+                float shift = mrun[j] == -INFINITY ? 0.0f : exp2f(mrun[j] - mnew);          \
+                lrun[j] *= shift;                                                           \
+                _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] *= shift;             \
+                mrun[j] = mnew;                                                             \
+            }                                                                               \
+        }                                                                                   \
+        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
+            aotx_u4a vv = vr[BUF][u];                                                       \
+            float vf[8];                                                                    \
+            _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                 \
+                vf[2 * e] = aotx_attn_h(vv[e], 0);                                          \
+                vf[2 * e + 1] = aotx_attn_h(vv[e], 1);                                      \
+            }                                                                               \
+            _Pragma("unroll") for (int j = 0; j < G; ++j) {                                 \
+                float pw = sc[u][j] == -INFINITY ? 0.0f : exp2f(sc[u][j] - mrun[j]);        \
+                lrun[j] += pw;                                                              \
+                _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] += pw * vf[e];        \
+            }                                                                               \
+        }                                                                                   \
+    } while (0)
+
+    if (b0 < b1) {
+        unsigned int b = b0;
+        ATTN_WINDOW(b0);
+        ATTN_LOAD(0, b);
+        for (;;) {
+            if (b + 1u < b1) ATTN_LOAD(1, b + 1u);
+            ATTN_COMPUTE(0, b);
+            b += 1u;
+            if (b >= b1) break;
+            if (b + 1u < b1) ATTN_LOAD(0, b + 1u);
+            ATTN_COMPUTE(1, b);
+            b += 1u;
+            if (b >= b1) break;
         }
     }
+#undef ATTN_WINDOW
+#undef ATTN_LOAD
+#undef ATTN_COMPUTE
+
     /* the lane groups' sums of one wave (mass counted once per group: lanes of a group
      * hold the same weights) */
 #pragma unroll
     for (int j = 0; j < G; ++j) {
         float l = lrun[j];
-        l += __shfl_xor(l, 8, 64);
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+#pragma unroll
+        for (int off = LPP; off < 64; off <<= 1) l += __shfl_xor(l, off, 64);
         lrun[j] = l;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < 8; ++e) {
             float v = o[j][e];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
+#pragma unroll
+            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
             o[j][e] = v;
         }
     }
@@ -247,12 +276,10 @@ __global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
 #pragma unroll
         for (int j = 0; j < G; ++j)
 #pragma unroll
-            for (int pc = 0; pc < NP; ++pc)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) wo[wave][j][64 * pc + 8 * sub + e] = missing ? 0.0f : o[j][8 * pc + e];
+            for (int e = 0; e < 8; ++e) wo[wave][j][8 * sub + e] = missing ? 0.0f : o[j][e];
     }
     __syncthreads();
-    /* merge the 4 waves in wave order */
+    /* merge the 4 waves in wave order; the chunk's triple keeps the base-2 maximum */
     const unsigned int unit = t * a.kv_heads + kh;
     const unsigned int stride = G * (D + 2);
     float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
@@ -262,7 +289,7 @@ __global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
         float msum = 0.0f, osum = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            float f = (wm[w][j] == -INFINITY) ? 0.0f : expf(wm[w][j] - top);
+            float f = (wm[w][j] == -INFINITY) ? 0.0f : exp2f(wm[w][j] - top);
             msum += wl[w][j] * f;
             osum += wo[w][j][e] * f;
         }
@@ -280,8 +307,9 @@ __global__ __launch_bounds__(256) void aotx_attend_kernel(aotx_attn_args a)
 }
 
 /* Merge the chunks of every (token, KV head) that was split, in chunk order:
- * M = max m_c, out = half(sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M)). The chunk
- * weights are computed once into LDS; every load of the sums is independent. */
+ * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). One wave per
+ * query head computes the chunk weights (a lane per chunk, wave reductions), then every
+ * thread adds its column over the chunks with independent loads. */
 template <int D, int G>
 __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
 {
@@ -295,24 +323,24 @@ __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
     if (t >= tokens) return;
     const unsigned int S = a.splits;
     const unsigned int n = a.pos[t] + 1u;
-    unsigned int chunk = (n + S - 1u) / S;
-    chunk = (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
+    const unsigned int chunk = aotx_attn_chunk(n, S);
     const unsigned int st = (n + chunk - 1u) / chunk;
     if (st <= 1u) return;
     const unsigned int stride = G * (D + 2);
     const float *all = a.partial + (unsigned long long)unit * S * stride;
-    if (threadIdx.x < (unsigned int)G) {
-        const unsigned int j = threadIdx.x;
-        float top = -INFINITY;
-        for (unsigned int cc = 0; cc < st; ++cc) top = fmaxf(top, all[cc * stride + j * (D + 2)]);
+    const unsigned int lane = threadIdx.x & 63u;
+    for (unsigned int j = threadIdx.x >> 6; j < (unsigned int)G; j += 4u) {
+        float mc = lane < st ? all[lane * stride + j * (D + 2)] : -INFINITY;
+        float lc = lane < st ? all[lane * stride + j * (D + 2) + 1] : 0.0f;
+        float top = mc;
+        for (int off = 32; off > 0; off >>= 1) top = fmaxf(top, __shfl_xor(top, off, 64));
+        float f = (mc == -INFINITY) ? 0.0f : exp2f(mc - top);
+        if (lane < st) fw[lane][j] = f;
+        /* chunk-order sum of the masses */
+        float w = lc * f;
         float msum = 0.0f;
-        for (unsigned int cc = 0; cc < st; ++cc) {
-            float mc = all[cc * stride + j * (D + 2)];
-            float f = (mc == -INFINITY) ? 0.0f : expf(mc - top);
-            fw[cc][j] = f;
-            msum += all[cc * stride + j * (D + 2) + 1] * f;
-        }
-        inv[j] = msum > 0.0f ? 1.0f / msum : 0.0f;
+        for (unsigned int cc = 0; cc < st; ++cc) msum += __shfl(w, (int)cc, 64);
+        if (lane == 0u) inv[j] = msum > 0.0f ? 1.0f / msum : 0.0f;
     }
     __syncthreads();
     for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += blockDim.x) {
@@ -329,17 +357,12 @@ __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
  * Host side
  * ------------------------------------------------------------------------------------- */
 
-struct aotx_attn_plan {
-    aotx_attn_args a;
-    unsigned int group;
-};
-
 unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
                               unsigned int max_context)
 {
-    /* about 1024 workgroups over the launch, chunks of at least 128 positions */
+    /* about ATTN_TARGET_GROUPS workgroups over the launch, chunks of at least 64 positions */
     unsigned int units = tokens * kv_heads;
-    unsigned int s = (1024u + units - 1u) / units;
+    unsigned int s = (ATTN_TARGET_GROUPS + units - 1u) / units;
     unsigned int cap = (max_context + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN;
     if (s > cap) s = cap;
     if (s > ATTN_MAX_SPLITS) s = ATTN_MAX_SPLITS;

@@ -65,6 +65,7 @@ struct aotx_hold {
     unsigned short *sel;
     float *qkv;                   /* fp32 QKV rows of the general path */
     float *logits;                /* [max_rows][vocab] */
+    unsigned int *pick_best;      /* [max_rows][16][2] largest logit per slice */
     unsigned int *pos, *tagent, *last;
     float *gemv_partial;
     size_t gemv_partial_bytes;
@@ -463,7 +464,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
         aotx_rproduct(h, hw, hrows, 1u, d->hidden, AOTX_EPI_F32, R, m_rows, t);
     }
     aotx_launch_pick(h->logits, d->vocab, d->vocab, m_rows, R, nullptr, nullptr, 0u, 1.0f, 0.0f,
-                     0ull, nullptr, nullptr, &h->step->run, s);
+                     0ull, nullptr, nullptr, &h->step->run, h->pick_best, s);
     aotx_launch_shut_rows(h->step, s);
 }
 
@@ -505,6 +506,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     h->sel = (unsigned short *)aotx_take(h, R * d->hidden * 2u);
     h->qkv = (float *)aotx_take(h, T * (wide + 2u * narrow) * 4u);
     h->logits = (float *)aotx_take(h, R * d->vocab * 4u);
+    h->pick_best = (unsigned int *)aotx_take(h, aotx_pick_scratch(R));
     h->pos = (unsigned int *)aotx_take(h, T * 4u);
     h->tagent = (unsigned int *)aotx_take(h, T * 4u);
     h->last = (unsigned int *)aotx_take(h, AOTX_SLOTS * 4u);

@@ -5,7 +5,9 @@
  * MFMA operands with fully coalesced 16-byte loads and no LDS:
  *   tiles  T  = ceil(n / 16)         (16 weight rows; rows past n are zero)
  *   quads  Qn = ceil(k / 128)        (4 blocks of 32; blocks past k are zero)
- *   quants: [T][Qn][64 lanes][32 B]  lane l = r + 16 g holds row 16t + r, block 4Q + g
+ *   quants: [T][Qn][2 halves][64 lanes][16 B]  lane l = r + 16 g holds row 16t + r,
+ *           block 4Q + g: quants 0..15 in the first half, 16..31 in the second, so each of a
+ *           wave's two 16-byte loads reads 1 KB of contiguous bytes
  *   scales: [T][Qn][64 lanes] fp16   the scale of that block
  * A tensor is 34/32 bytes per weight plus the zero padding of the last tile and quad.
  */
@@ -43,6 +45,8 @@ struct aotx_rgemv_args {
     unsigned int k;
     unsigned int qn;              /* quads of k */
     unsigned int rt;              /* 16-row tiles per workgroup */
+    unsigned int wide;            /* 1: the tile-split wide-batch kernel (fp16 x only) */
+    unsigned int pd;              /* quads loaded ahead per wave (narrow kernel) */
     unsigned int groups;          /* workgroups along n */
     unsigned int splits;          /* workgroups along k */
     unsigned int qps;             /* quads per split */

@@ -20,6 +20,8 @@
  */
 #include "rgemv.h"
 
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 typedef _Float16 rg_h8 __attribute__((ext_vector_type(8)));
@@ -28,6 +30,13 @@ typedef float rg_f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int rg_u4 __attribute__((ext_vector_type(4)));
 
 #define RG_THREADS 256
+
+/* Workgroup barrier that waits for this wave's LDS operations only: global loads already
+ * in flight (the weight stream) stay in flight across it. */
+static __device__ __forceinline__ void rg_sync_lds()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 /* ---- repack ------------------------------------------------------------------------- */
 
@@ -49,15 +58,16 @@ __global__ void aotx_q8r_repack_kernel(const unsigned char *src, unsigned int n,
         unsigned int r = lane & 15u, g = lane >> 4;
         unsigned long long row = t * 16ull + r;
         unsigned long long blk = q * 4ull + g;
-        unsigned char *qd = dst + it * 32ull;
+        /* the lane's first 16 quants, then (1 KB on) its second 16 */
+        unsigned char *qd = dst + tq * 2048ull + lane * 16u;
         unsigned short *sd = (unsigned short *)(dst + quant_bytes) + it;
         if (row < n && blk < blocks) {
             const unsigned char *b = src + row * row_bytes + blk * 34ull;
             *sd = (unsigned short)(b[0] | (b[1] << 8));
-            for (int j = 0; j < 32; ++j) qd[j] = b[2 + j];
+            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = b[2 + j];
         } else {
             *sd = 0u;
-            for (int j = 0; j < 32; ++j) qd[j] = 0u;
+            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = 0u;
         }
     }
 }
@@ -155,7 +165,7 @@ static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a,
 }
 
 /* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. */
-template <int MT>
+template <int MT, int NT>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
                                                    unsigned int mrows, const unsigned int *list)
@@ -166,7 +176,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
     if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr) {
         /* one thread per (tile, row of x): add the 16 results of the tile into the residual
          * stream and leave the tile's sum of squares for the next norm */
-        for (unsigned int idx = tid; idx < rt * MT; idx += RG_THREADS) {
+        for (unsigned int idx = tid; idx < rt * MT; idx += NT) {
             unsigned int j = idx % rt, mm = idx / rt;
             unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
             if (mm >= mrows || v0 >= a.n) continue;
@@ -180,7 +190,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             a.sumsq_out[(unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u] = s;
         }
     } else if (a.epi == AOTX_EPI_F32 || a.epi == AOTX_EPI_F16 || a.epi == AOTX_EPI_RESID) {
-        for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) {
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
             unsigned int row = idx % gr, mm = idx / gr;
             unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
             if (mm >= mrows || v >= a.n) continue;
@@ -192,7 +202,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
         }
     } else if (a.epi == AOTX_EPI_SWIGLU) {
         const unsigned int half = rt / 2u;
-        for (unsigned int idx = tid; idx < half * 16u * MT; idx += RG_THREADS) {
+        for (unsigned int idx = tid; idx < half * 16u * MT; idx += NT) {
             unsigned int row = idx % (half * 16u), mm = idx / (half * 16u);
             unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
             if (mm >= mrows || v >= a.n) continue;
@@ -205,7 +215,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
         const aotx_qkv_epi &e = a.qkv;
         const unsigned int d = e.head_dim;
         const float step = powf(e.theta, -2.0f / (float)d);
-        for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += RG_THREADS) {
+        for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += NT) {
             unsigned int pr = idx % (gr / 2u), mm = idx / (gr / 2u);
             unsigned int row = 2u * pr;
             unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
@@ -288,64 +298,6 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     const unsigned int xs = kr + 8u;               /* LDS x row stride (halves) */
     unsigned short *xl = (unsigned short *)lds;
 
-    /* ---- stage the batch rows of x for [q0, q1) ---- */
-    {
-        const unsigned int kbeg = q0 * 128u;
-        const unsigned int kend = q1 * 128u;
-        const unsigned int width = kend - kbeg;          /* multiple of 128 */
-        const unsigned int pieces = width / 8u;          /* 16-byte pieces per row */
-        if (a.xmode == AOTX_X_NORM) {
-            __shared__ float share[4];
-            const unsigned int nss = (a.k + 15u) / 16u;
-            for (unsigned int mm = 0; mm < mrows; ++mm) {
-                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
-                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
-                const float *ss = a.sumsq + (unsigned long long)src * nss;
-                float sum = 0.0f;
-                for (unsigned int i = tid; i < nss; i += RG_THREADS) sum += ss[i];
-                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                if (lane == 0u) share[wave] = sum;
-                __syncthreads();
-                sum = share[0] + share[1] + share[2] + share[3];
-                __syncthreads();
-                const float scale = rsqrtf(sum / (float)a.k + a.eps);
-                const float *r = a.resid + (unsigned long long)src * a.k;
-                for (unsigned int p = tid; p < pieces; p += RG_THREADS) {
-                    unsigned int kk = kbeg + p * 8u;
-                    unsigned int h[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        unsigned int kc = kk + (unsigned int)e;
-                        h[e] = kc < a.k ? aotx_f2h(scale * r[kc] * a.norm_w[kc]) : 0u;
-                    }
-                    rg_u4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                               h[6] | (h[7] << 16)};
-                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
-                }
-            }
-        } else {
-            for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
-                unsigned int mm = idx / pieces, p = idx - mm * pieces;
-                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
-                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
-                unsigned int kk = kbeg + p * 8u;
-                rg_u4 v = {0u, 0u, 0u, 0u};
-                if (kk + 8u <= a.k) {
-                    v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
-                } else if (kk < a.k) {
-                    unsigned int h[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
-                    v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                                h[6] | (h[7] << 16)};
-                }
-                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
-            }
-        }
-        __syncthreads();
-    }
-
     /* ---- per-wave k quarter ---- */
     const unsigned int nq = q1 - q0;
     const unsigned int per = (nq + 3u) / 4u;
@@ -358,7 +310,7 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
 #pragma unroll
     for (int j = 0; j < RT; ++j) {
         unsigned int dummy = 0u;
-        qb[j] = rg_tile(a, group, (unsigned int)j, RT, expert, dummy) + lane * 32u;
+        qb[j] = rg_tile(a, group, (unsigned int)j, RT, expert, dummy) + lane * 16u;
         sb[j] = rg_scales(a, group, (unsigned int)j, RT, expert) + lane;
     }
 
@@ -379,7 +331,7 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
             _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
                 const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
                 wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
-                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 1);                \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
                 ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
             }                                                                            \
         }                                                                                \
@@ -421,9 +373,69 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
+    /* the first weight loads go out before x is staged, so their latency overlaps it */
+    if (wq0 < wq1) RG_LOAD(0, wq0);
+
+    /* ---- stage the batch rows of x for [q0, q1) ---- */
+    {
+        const unsigned int kbeg = q0 * 128u;
+        const unsigned int kend = q1 * 128u;
+        const unsigned int width = kend - kbeg;          /* multiple of 128 */
+        const unsigned int pieces = width / 8u;          /* 16-byte pieces per row */
+        if (a.xmode == AOTX_X_NORM) {
+            __shared__ float share[4];
+            const unsigned int nss = (a.k + 15u) / 16u;
+            for (unsigned int mm = 0; mm < mrows; ++mm) {
+                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
+                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+                const float *ss = a.sumsq + (unsigned long long)src * nss;
+                float sum = 0.0f;
+                for (unsigned int i = tid; i < nss; i += RG_THREADS) sum += ss[i];
+                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                if (lane == 0u) share[wave] = sum;
+                rg_sync_lds();
+                sum = share[0] + share[1] + share[2] + share[3];
+                rg_sync_lds();
+                const float scale = rsqrtf(sum / (float)a.k + a.eps);
+                const float *r = a.resid + (unsigned long long)src * a.k;
+                for (unsigned int p = tid; p < pieces; p += RG_THREADS) {
+                    unsigned int kk = kbeg + p * 8u;
+                    unsigned int h[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        unsigned int kc = kk + (unsigned int)e;
+                        h[e] = kc < a.k ? aotx_f2h(scale * r[kc] * a.norm_w[kc]) : 0u;
+                    }
+                    rg_u4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                               h[6] | (h[7] << 16)};
+                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+                }
+            }
+        } else {
+            for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
+                unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
+                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+                unsigned int kk = kbeg + p * 8u;
+                rg_u4 v = {0u, 0u, 0u, 0u};
+                if (kk + 8u <= a.k) {
+                    v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
+                } else if (kk < a.k) {
+                    unsigned int h[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
+                    v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                h[6] | (h[7] << 16)};
+                }
+                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+            }
+        }
+        rg_sync_lds();
+    }
+
     if (wq0 < wq1) {
         unsigned int q = wq0;
-        RG_LOAD(0, q);
         for (;;) {
             unsigned int qn1 = q + PD;
             if (qn1 < wq1) RG_LOAD(1, qn1);
@@ -465,14 +477,29 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) mine[idx] = out[idx];
         return;
     }
-    rg_epilogue<MT>(a, out, group, RT, mrows, list);
+    rg_epilogue<MT, RG_THREADS>(a, out, group, RT, mrows, list);
 }
 
-/* Add the split partials of one workgroup's rows in split order, then the epilogue. */
-template <int MT>
-__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args a)
+/* Wide batches (17..32 rows of x, fp16 x in memory): W waves split the workgroup's
+ * W * RT tiles (tile j belongs to wave j / RT) and every wave runs the workgroup's whole k
+ * range, so no wave's sum has to be added to another's. x passes through LDS in chunks of
+ * RGW_KC quads, double-buffered: the next chunk is loaded into registers while the
+ * current one feeds the MFMAs, and the weight stream runs `PD` quads ahead across chunk
+ * boundaries. Two workgroups fit a CU, so one's staging overlaps the other's streaming. */
+#define RGW_KC 4
+#define RGW_XS (RGW_KC * 128 + 8)     /* LDS x row stride (halves) */
+
+template <int MT, int RT, int W, int PD>
+__global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
 {
-    __shared__ float out[64 * MT];
+    static_assert(RGW_KC % (2 * PD) == 0, "a chunk holds whole load pairs");
+    constexpr int NT = 64 * W;
+    constexpr int PIECES = RGW_KC * 16;                      /* 16-byte pieces per row */
+    constexpr int PPT = (MT * PIECES + NT - 1) / NT;          /* pieces per thread */
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
     const unsigned int expert = blockIdx.y;
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
@@ -487,17 +514,191 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args 
     if (mrows > a.m) mrows = a.m;
     if (mrows > (unsigned int)MT) mrows = MT;
     if (mrows == 0u) return;
-    const unsigned int group = blockIdx.x;
+
+    const unsigned int rtw = (unsigned int)(RT * W);
+    const unsigned int group = blockIdx.x / a.splits;
+    const unsigned int split = blockIdx.x % a.splits;
+    const unsigned int q0 = split * a.qps;
+    const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
+    const unsigned int nch = (q1 - q0 + RGW_KC - 1u) / RGW_KC;
+    unsigned short *xl = (unsigned short *)lds;               /* [2][MT][RGW_XS] */
+    const unsigned int r = lane & 15u, g = lane >> 4;
+
+    const unsigned char *qb[RT];
+    const unsigned short *sb[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        unsigned int dummy = 0u;
+        unsigned int tj = wave * (unsigned int)RT + (unsigned int)j;
+        qb[j] = rg_tile(a, group, tj, rtw, expert, dummy) + lane * 16u;
+        sb[j] = rg_scales(a, group, tj, rtw, expert) + lane;
+    }
+    rg_f4 acc[RT][MT / 16];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+    rg_u4 wa[2][PD][RT][2];
+    unsigned short ws[2][PD][RT];
+
+#define RGW_LOAD(BUF, QS)                                                                \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = (QS) + (unsigned int)qi;                                   \
+            if (qq >= q1) qq = q1 - 1u;                                                  \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
+                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
+                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+#define RGW_COMPUTE(BUF, QS, XB)                                                         \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = (QS) + (unsigned int)qi;                                   \
+            if (qq < q1) {                                                               \
+                const unsigned short *xq = (XB) + ((qq - q0) % RGW_KC) * 128u + 32u * g; \
+                rg_h8 B[MT / 16][4];                                                     \
+                _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                    \
+                    _Pragma("unroll") for (int s = 0; s < 4; ++s)                        \
+                        B[t][s] = *(const rg_h8 *)(xq + ((unsigned int)t * 16u + r) * RGW_XS + 8u * s); \
+                }                                                                        \
+                _Pragma("unroll") for (int j = 0; j < RT; ++j) {                         \
+                    unsigned int sbits = ws[BUF][qi][j];                                 \
+                    rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));         \
+                    const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];        \
+                    unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                \
+                                          q1v[0], q1v[1], q1v[2], q1v[3]};               \
+                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
+                        unsigned int d0, d1, d2, d3;                                     \
+                        rg_dequant4(qd[2 * s], s2, d0, d1);                              \
+                        rg_dequant4(qd[2 * s + 1], s2, d2, d3);                          \
+                        rg_u4 av = {d0, d1, d2, d3};                                     \
+                        rg_h8 A = __builtin_bit_cast(rg_h8, av);                         \
+                        _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)              \
+                            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(           \
+                                A, B[t][s], acc[j][t], 0, 0, 0);                         \
+                    }                                                                    \
+                }                                                                        \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+    /* x chunk c: rows past mrows and k past a.k are zeros */
+    rg_u4 xr[PPT];
+#define RGW_XLOAD(C)                                                                     \
+    do {                                                                                 \
+        _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
+            unsigned int idx = tid + (unsigned int)i * NT;                               \
+            unsigned int mm = idx / PIECES, p = idx % PIECES;                            \
+            unsigned int kk = (q0 + (C) * RGW_KC) * 128u + p * 8u;                       \
+            xr[i] = (rg_u4){0u, 0u, 0u, 0u};                                             \
+            if (idx < (unsigned int)(MT * PIECES) && mm < mrows && kk < q1 * 128u && kk < a.k) { \
+                unsigned int src = list != nullptr ? list[mm] / a.xrow_div               \
+                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);  \
+                xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);    \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+#define RGW_XSTORE(C)                                                                    \
+    do {                                                                                 \
+        unsigned short *xb = xl + ((C) & 1u) * (unsigned int)(MT * RGW_XS);              \
+        _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
+            unsigned int idx = tid + (unsigned int)i * NT;                               \
+            unsigned int mm = idx / PIECES, p = idx % PIECES;                            \
+            if (idx < (unsigned int)(MT * PIECES))                                       \
+                *(rg_u4 *)(xb + mm * RGW_XS + p * 8u) = xr[i];                           \
+        }                                                                                \
+    } while (0)
+
+    RGW_XLOAD(0u);
+    RGW_LOAD(0, q0);
+    RGW_XSTORE(0u);
+    rg_sync_lds();
+    for (unsigned int c = 0; c < nch; ++c) {
+        const unsigned short *xb = xl + (c & 1u) * (unsigned int)(MT * RGW_XS);
+        if (c + 1u < nch) RGW_XLOAD(c + 1u);
+#pragma unroll
+        for (int h = 0; h < RGW_KC / (2 * PD); ++h) {
+            unsigned int qa = q0 + c * RGW_KC + (unsigned int)(2 * PD * h);
+            if (qa + PD < q1) RGW_LOAD(1, qa + PD);
+            RGW_COMPUTE(0, qa, xb);
+            if (qa + 2 * PD < q1) RGW_LOAD(0, qa + 2 * PD);
+            RGW_COMPUTE(1, qa + PD, xb);
+        }
+        if (c + 1u < nch) RGW_XSTORE(c + 1u);
+        rg_sync_lds();
+    }
+#undef RGW_LOAD
+#undef RGW_COMPUTE
+#undef RGW_XLOAD
+#undef RGW_XSTORE
+
+    /* every wave's tiles into LDS (the x buffers are free after the last barrier) */
+    float *out = (float *)lds;                         /* [rtw*16][MT] */
+    const unsigned int gr = rtw * 16u;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                unsigned int row = (wave * (unsigned int)RT + (unsigned int)j) * 16u + 4u * g + (unsigned int)i;
+                out[row * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
+            }
+    __syncthreads();
+    if (a.splits > 1u) {
+        float *mine = a.partial
+            + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
+        return;
+    }
+    rg_epilogue<MT, NT>(a, out, group, rtw, mrows, list);
+}
+
+/* Add the split partials in split order, then the epilogue. One workgroup per 16-row tile
+ * of a product group (per gate/up tile pair for the gated unit), so the adds of a launch
+ * spread over many CUs and every thread's split loads are independent. */
+template <int MT>
+__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args a)
+{
+    __shared__ float out[32 * MT];
+    const unsigned int expert = blockIdx.y;
+    const unsigned int *list = nullptr;
+    unsigned int mrows = a.m;
+    if (a.expert_stride != 0ull) {
+        unsigned int total = a.list_count[expert];
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+        list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
+    } else if (a.m_dev != nullptr) {
+        unsigned int total = *a.m_dev;
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+    if (mrows == 0u) return;
+    const bool pair = a.epi == AOTX_EPI_SWIGLU;
+    const unsigned int slabs = pair ? a.rt / 2u : a.rt;
+    const unsigned int group = blockIdx.x / slabs;
+    const unsigned int sl = blockIdx.x % slabs;
+    const unsigned int nt = pair ? 2u : 1u;
     const unsigned int gr = a.rt * 16u;
     const float *all = a.partial
         + ((unsigned long long)expert * a.groups + group) * a.splits * gr * MT;
-    for (unsigned int idx = threadIdx.x; idx < gr * MT; idx += RG_THREADS) {
+    for (unsigned int idx = threadIdx.x; idx < nt * 16u * MT; idx += RG_THREADS) {
+        unsigned int tile = idx / (16u * MT) == 0u ? sl : sl + slabs;
+        unsigned int at = tile * 16u * MT + idx % (16u * MT);
         float sum = 0.0f;
-        for (unsigned int sp = 0; sp < a.splits; ++sp) sum += all[(unsigned long long)sp * gr * MT + idx];
+#pragma unroll 8
+        for (unsigned int sp = 0; sp < a.splits; ++sp) sum += all[(unsigned long long)sp * gr * MT + at];
         out[idx] = sum;
     }
     __syncthreads();
-    rg_epilogue<MT>(a, out, group, a.rt, mrows, list);
+    /* the slab as a workgroup of its own: one tile (or one gate/up pair) */
+    rg_epilogue<MT, RG_THREADS>(a, out, pair ? group * slabs + sl : group * a.rt + sl, nt, mrows, list);
 }
 
 /* ---- host ---------------------------------------------------------------------------- */
@@ -507,6 +708,24 @@ static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
     size_t x = (size_t)a.m * (a.qps * 128u + 8u) * 2u;
     size_t red = (size_t)5u * a.rt * 16u * mt * 4u;
     return x > red ? x : red;
+}
+
+/* Planning overrides for measurement sweeps, read once from AOTX_RGEMV_TUNE
+ * ("rt,pd,target,minq"; 0 keeps the default). */
+struct aotx_rgemv_tune {
+    unsigned int rt, pd, target, minq;
+};
+
+static const aotx_rgemv_tune &aotx_rgemv_tuning()
+{
+    static aotx_rgemv_tune t = [] {
+        aotx_rgemv_tune v = {0u, 0u, 0u, 0u};
+        const char *e = getenv("AOTX_RGEMV_TUNE");
+        if (e != nullptr) sscanf(e, "%u,%u,%u,%u", &v.rt, &v.pd, &v.target, &v.minq);
+        if (v.rt != 0u && v.rt != 1u && v.rt != 2u && v.rt != 4u) v.rt = 0u;
+        return v;
+    }();
+    return t;
 }
 
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
@@ -536,16 +755,32 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         a->n = total;
         tiles = (total + 15u) / 16u;
     }
-    /* rows per workgroup: gate/up pairs need an even tile count. Wide batches take 4 tiles
-     * (each workgroup stages its x range once for 64 rows); narrow ones take fewer tiles
-     * while that leaves fewer than ~1024 workgroups. */
+    if (mt > 16u) {
+        /* wide batch: 8 waves x 1 tile per workgroup, x through LDS in chunks; split k
+         * while there are fewer than 256 workgroups and every split keeps a whole chunk */
+        a->wide = 1u;
+        a->rt = 8u;
+        if (epi == AOTX_EPI_SWIGLU) a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + 3u) / 4u;
+        else a->groups = (tiles + 7u) / 8u;
+        unsigned int s = 1u;
+        while (a->groups * s < 256u && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
+        a->qps = (a->qn + s - 1u) / s;
+        a->splits = (a->qn + a->qps - 1u) / a->qps;
+        return 0;
+    }
+    /* rows per workgroup: gate/up pairs need an even tile count. Narrow batches take fewer
+     * tiles while that leaves fewer than ~1024 workgroups. */
+    const aotx_rgemv_tune &tune = aotx_rgemv_tuning();
     unsigned int rt;
     if (mt > 8u) rt = 4u;
     else if (tiles >= 4u * 1024u) rt = 4u;
     else if (tiles >= 2u * 1024u) rt = 2u;
     else rt = 1u;
+    if (tune.rt != 0u) rt = tune.rt;
     if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
     a->rt = rt;
+    a->pd = rt == 1u ? 4u : (rt == 2u ? 2u : 1u);
+    if (tune.pd != 0u) a->pd = tune.pd;
     if (epi == AOTX_EPI_SWIGLU) {
         unsigned int half_tiles = (unsigned int)aotx_q8r_tiles(rows[0]);
         a->groups = (half_tiles + rt / 2u - 1u) / (rt / 2u);
@@ -553,11 +788,13 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         a->groups = (tiles + rt - 1u) / rt;
     }
     /* k split: the staged x rows of a workgroup's k range fit 96 KB of LDS; split further
-     * while there are fewer than 256 workgroups and a split keeps >= 8 quads */
+     * while there are fewer than `target` workgroups and a split keeps >= `minq` quads */
+    const unsigned int target = tune.target != 0u ? tune.target : 256u;
+    const unsigned int minq = tune.minq != 0u ? tune.minq : 8u;
     unsigned int kmax = 98304u / (mt * 256u);
     if (kmax < 1u) kmax = 1u;
     unsigned int s = (a->qn + kmax - 1u) / kmax;
-    while (a->groups * s < 256u && (a->qn + s) / (s + 1u) >= 8u) s += 1u;
+    while (a->groups * s < target && (a->qn + s) / (s + 1u) >= minq) s += 1u;
     a->qps = (a->qn + s - 1u) / s;
     a->splits = (a->qn + a->qps - 1u) / a->qps;
     return 0;
@@ -569,17 +806,17 @@ size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
     return a.splits > 1u ? e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float) : 0u;
 }
 
-template <int MT, int RT>
+template <int MT, int RT, int PD>
 static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
 {
-    constexpr int PD = RT == 1 ? 4 : (RT == 2 ? 2 : 1);
     unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
     size_t lds = aotx_rgemv_lds(a, MT);
     hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD>), dim3(a.groups * a.splits, ey), dim3(RG_THREADS),
                        lds, s, a);
     AOTX_LAUNCH_CHECK();
     if (a.splits > 1u) {
-        hipLaunchKernelGGL((aotx_rgemv_reduce<MT>), dim3(a.groups, ey), dim3(RG_THREADS), 0, s, a);
+        hipLaunchKernelGGL((aotx_rgemv_reduce<MT>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
+                           dim3(RG_THREADS), 0, s, a);
         AOTX_LAUNCH_CHECK();
     }
 }
@@ -590,15 +827,33 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
     if (a.splits > 1u && a.partial == nullptr) {
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
     }
-    const unsigned int mt = a.m <= 16u ? 16u : 32u;
-    if (mt == 16u) {
-        if (a.rt == 1u) aotx_rgemv_go<16, 1>(a, s);
-        else if (a.rt == 2u) aotx_rgemv_go<16, 2>(a, s);
-        else aotx_rgemv_go<16, 4>(a, s);
+    if (a.wide) {
+        if (a.xmode != AOTX_X_F16) {
+            fprintf(stderr, "aotx: the wide-batch product takes fp16 x only\n");
+            exit(1);
+        }
+        unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
+        size_t xb = 2u * 32u * RGW_XS * 2u;
+        size_t ob = (size_t)a.rt * 16u * 32u * 4u;
+        hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), dim3(a.groups * a.splits, ey), dim3(512),
+                           xb > ob ? xb : ob, s, a);
+        AOTX_LAUNCH_CHECK();
+        if (a.splits > 1u) {
+            hipLaunchKernelGGL((aotx_rgemv_reduce<32>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
+                               dim3(RG_THREADS), 0, s, a);
+            AOTX_LAUNCH_CHECK();
+        }
+        return;
+    }
+    if (a.rt == 1u) {
+        if (a.pd >= 8u) aotx_rgemv_go<16, 1, 8>(a, s);
+        else aotx_rgemv_go<16, 1, 4>(a, s);
+    } else if (a.rt == 2u) {
+        if (a.pd >= 4u) aotx_rgemv_go<16, 2, 4>(a, s);
+        else aotx_rgemv_go<16, 2, 2>(a, s);
     } else {
-        if (a.rt == 1u) aotx_rgemv_go<32, 1>(a, s);
-        else if (a.rt == 2u) aotx_rgemv_go<32, 2>(a, s);
-        else aotx_rgemv_go<32, 4>(a, s);
+        if (a.pd >= 2u) aotx_rgemv_go<16, 4, 2>(a, s);
+        else aotx_rgemv_go<16, 4, 1>(a, s);
     }
 }
 

@@ -9,6 +9,8 @@ void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
                       const unsigned int *agent, const aotx_model_how *how,
                       unsigned int top_k, float top_p, float temperature,
                       unsigned long long seed, int *token, unsigned int *draw,
-                      const aotx_model_run *run, hipStream_t s);
+                      const aotx_model_run *run, unsigned int *best, hipStream_t s);
+/* Bytes of the per-row candidate buffer (`best`) of aotx_launch_pick. */
+size_t aotx_pick_scratch(unsigned int rows);
 
 #endif

@@ -27,6 +27,7 @@
 #define PICK_THREADS 256u
 #define PICK_BUCKETS 256u
 #define PICK_PASSES 2u
+#define PICK_CHUNKS 16u   /* workgroups per row of the largest-logit search */
 
 #pragma clang fp contract(off)
 
@@ -88,7 +89,73 @@ struct aotx_pick_args {
     unsigned int *draw;
     aotx_state *state;
     const aotx_model_run *run;    /* when set, every per-call value comes from here */
+    unsigned int *best;           /* [rows][PICK_CHUNKS][2]: each chunk's (value bits, token) */
 };
+
+/* (v, i) ranks ahead of (bv, bi) in the reference's largest-logit search: a larger value;
+ * among equal values the lower token mod 256 (the reference's lower thread), then the
+ * lower token (that thread's earlier stride). NaN ranks nowhere. */
+static __device__ __forceinline__ bool aotx_pick_ahead(float v, unsigned int i, float bv,
+                                                       unsigned int bi)
+{
+    return v > bv || (v == bv && ((i & 255u) < (bi & 255u) || ((i & 255u) == (bi & 255u) && i < bi)));
+}
+
+/* The largest logit of each of PICK_CHUNKS slices of a row (grid: chunks x rows). The
+ * winner over the slices under aotx_pick_ahead is the reference's (thread-strided scan,
+ * then the thread-order merge), so the slices can be searched in parallel. A slice whose
+ * values are all -inf (or NaN) leaves (-inf, 0), as a reference thread does. */
+__global__ __launch_bounds__(PICK_THREADS) void aotx_argmax_kernel(aotx_pick_args a)
+{
+    __shared__ float wv[PICK_THREADS / 64];
+    __shared__ unsigned int wi[PICK_THREADS / 64];
+    const unsigned int tid = threadIdx.x;
+    const unsigned int r = blockIdx.y;
+    const unsigned int c = blockIdx.x;
+    const aotx_model_run *run = a.run;
+    unsigned int rows = run ? run->rows : (a.rows_dev ? *a.rows_dev : a.rows);
+    int *token_out = run ? run->token : a.token;
+    if (r >= rows || token_out == nullptr) return;
+    if (run && run->select != AOTX_MODEL_ROWS_LAST) return;
+    const float *row = a.logits + (unsigned long long)r * a.ld;
+    const unsigned int span = (a.vocab + PICK_CHUNKS - 1u) / PICK_CHUNKS;
+    const unsigned int lo = c * span;
+    const unsigned int hi = lo + span < a.vocab ? lo + span : a.vocab;
+    float best = -INFINITY;
+    unsigned int at = 0u;
+#pragma unroll 8
+    for (unsigned int i = lo + tid; i < hi; i += PICK_THREADS) {
+        float one = row[i];
+        if (aotx_pick_ahead(one, i, best, at)) {
+            best = one;
+            at = i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float ov = __shfl_xor(best, off, 64);
+        unsigned int oi = __shfl_xor(at, off, 64);
+        if (aotx_pick_ahead(ov, oi, best, at)) {
+            best = ov;
+            at = oi;
+        }
+    }
+    if ((tid & 63u) == 0u) {
+        wv[tid >> 6] = best;
+        wi[tid >> 6] = at;
+    }
+    __syncthreads();
+    if (tid == 0u) {
+        for (unsigned int w = 1u; w < PICK_THREADS / 64u; ++w) {
+            if (aotx_pick_ahead(wv[w], wi[w], best, at)) {
+                best = wv[w];
+                at = wi[w];
+            }
+        }
+        unsigned int *out = a.best + ((unsigned long long)r * PICK_CHUNKS + c) * 2u;
+        out[0] = __float_as_uint(best);
+        out[1] = at;
+    }
+}
 
 __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args a)
 {
@@ -127,27 +194,21 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
         min_p = how[r].min_p;
     }
 
-    /* largest logit and its place */
-    float best = -INFINITY;
-    unsigned int at = 0u;
-    for (unsigned int i = tid; i < vocab; i += PICK_THREADS) {
-        float one = row[i];
-        if (one > best) {
-            best = one;
-            at = i;
-        }
-    }
-    part[tid] = best;
-    mark[tid] = at;
-    __syncthreads();
+    /* largest logit and its place, from the slices of aotx_argmax_kernel */
     if (tid == 0u) {
-        for (unsigned int i = 1u; i < PICK_THREADS; ++i) {
-            if (part[i] > part[0]) {
-                part[0] = part[i];
-                mark[0] = mark[i];
+        const unsigned int *cand = a.best + (unsigned long long)r * PICK_CHUNKS * 2u;
+        float best = -INFINITY;
+        unsigned int at = 0u;
+        for (unsigned int c = 0u; c < PICK_CHUNKS; ++c) {
+            float v = __uint_as_float(cand[2u * c]);
+            unsigned int i = cand[2u * c + 1u];
+            if (aotx_pick_ahead(v, i, best, at)) {
+                best = v;
+                at = i;
             }
         }
-        s_top = part[0];
+        s_top = best;
+        mark[0] = at;
         s_position = atomicAdd(&a.state->draw[agent], 1u);
         if (draw_out != nullptr) draw_out[r] = s_position;
     }
@@ -167,6 +228,7 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
         __syncthreads();
         float band = hi - lo;
         float row_total = 0.0f;
+#pragma unroll 8
         for (unsigned int i = tid; i < vocab; i += PICK_THREADS) {
             float scaled = row[i] - top;
             if (pass == 0u) row_total += expf(scaled);
@@ -214,6 +276,7 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
     const unsigned int first = tid * per;
     const unsigned int after = first + per < vocab ? first + per : vocab;
     unsigned int mine = 0u;
+#pragma unroll 8
     for (unsigned int i = first; i < after; ++i) {
         if (row[i] - top >= cut) mine += 1u;
     }
@@ -312,12 +375,17 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
     token_out[r] = (int)chosen;
 }
 
+size_t aotx_pick_scratch(unsigned int rows)
+{
+    return (size_t)rows * PICK_CHUNKS * 2u * sizeof(unsigned int);
+}
+
 void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
                       const unsigned int *rows_dev, unsigned int rows,
                       const unsigned int *agent, const aotx_model_how *how,
                       unsigned int top_k, float top_p, float temperature,
                       unsigned long long seed, int *token, unsigned int *draw,
-                      const aotx_model_run *run, hipStream_t s)
+                      const aotx_model_run *run, unsigned int *best, hipStream_t s)
 {
     aotx_pick_args a;
     a.logits = logits;
@@ -335,6 +403,9 @@ void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
     a.draw = draw;
     a.state = aotx_state_device();
     a.run = run;
+    a.best = best;
+    hipLaunchKernelGGL(aotx_argmax_kernel, dim3(PICK_CHUNKS, rows), dim3(PICK_THREADS), 0, s, a);
+    AOTX_LAUNCH_CHECK();
     hipLaunchKernelGGL(aotx_pick_kernel, dim3(rows), dim3(PICK_THREADS), 0, s, a);
     AOTX_LAUNCH_CHECK();
 }
@@ -346,8 +417,9 @@ extern "C" int aotx_pick(const float *logits, unsigned int rows, unsigned int vo
 {
     if (logits == nullptr || agent == nullptr || token == nullptr || rows == 0u || vocab == 0u)
         return 1;
+    unsigned int *best = (unsigned int *)aotx_scratch(AOTX_SCRATCH_PICK, aotx_pick_scratch(rows));
     aotx_launch_pick(logits, vocab, vocab, nullptr, rows, agent, how, top_k, top_p,
-                     temperature, seed, token, draw, nullptr, aotx_stream(stream));
+                     temperature, seed, token, draw, nullptr, best, aotx_stream(stream));
     return 0;
 }
 

@@ -147,13 +147,15 @@ def test_repacked_gemv_benchmark_shapes(torch, lib, orc, n, k, m):
 
 
 def test_repack_layout(torch, lib):
-    """Repacked bytes: lane l = r + 16 g of (tile t, quad q) holds row 16t + r, block 4q + g."""
+    """Repacked bytes: lane l = r + 16 g of (tile t, quad q) holds row 16t + r, block 4q + g;
+    its quants 0..15 sit in the first 1 KB half of the (t, q) record, 16..31 in the second."""
     n, k = 40, 384
     w = make(torch, lib, n, k, 3)
     wr = repack(torch, lib, w, n, k).cpu().numpy()
     src = w.cpu().numpy().reshape(n, k // 32, 34)
     tiles, quads = (n + 15) // 16, (k + 127) // 128
-    quant = wr[:tiles * quads * 64 * 32].reshape(tiles, quads, 64, 32)
+    quant = wr[:tiles * quads * 64 * 32].reshape(tiles, quads, 2, 64, 16).transpose(0, 1, 3, 2, 4)
+    quant = quant.reshape(tiles, quads, 64, 32)
     scale = wr[tiles * quads * 64 * 32:].view(np.uint16).reshape(tiles, quads, 64)
     for t in range(tiles):
         for q in range(quads):
