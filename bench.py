@@ -11,10 +11,13 @@ surface: aotx_model_pages -> aotx_kv_serve -> aotx_model_sample, one step = one 
 every slot. `value` is the batch-32 whole-step throughput in tokens/s; the batch-1 rate,
 the sampled (top-k 40 / top-p 0.9 / T 0.8) rate and the Q8 GEMV table ride along.
 
-`roofline` is measured on the dominant kernel, the Q8_0 product at the FFN shape
-(N=14336, K=4096) with the batch-32 activations, timed with HIP events on the stream it is
-launched on. `cpu_baseline` times the repository's C oracle (oracle/) on the host cores
-over a bounded sample of the same decode step.
+`roofline` is measured on the dominant kernel of the batch step, paged decode attention
+(aotx_attend_paged) over the seated 32 x 2048-position KV of the timed workload: a HIP graph
+of 20 launches replayed on its own stream, timed with HIP events recorded on that stream.
+Its algorithmic bytes are the keys and values of every attended position plus q and out.
+The Q8 products of the step are reported the same way under `kernels`. `cpu_baseline` times
+the repository's C oracle (oracle/) on the host cores over a bounded sample of the same
+decode step.
 """
 import argparse
 import ctypes
@@ -29,16 +32,29 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "attention_b32_ctx2048_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed counter passes
+    (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None when absent."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_table(torch, L, shapes, ms, iters=20, warm=3):
-    """Per-launch time and achieved GB/s of the Q8_0 product (fp16 out, config 2), for the
-    file-layout entry point (aotx_q8_gemv_f16) and for the repacked form the decode step
-    streams (aotx_q8r_gemv_f16)."""
+def gemv_table(torch, L, shapes, ms, iters=20):
+    """Per-launch device time (graph-timed) and achieved GB/s of the Q8_0 product (fp16 out,
+    config 2), for the file-layout entry point (aotx_q8_gemv_f16) and for the repacked form
+    the decode step streams (aotx_q8r_gemv_f16)."""
     import aotx_amd as A
     out = []
     for n, k in shapes:
@@ -49,20 +65,12 @@ def gemv_table(torch, L, shapes, ms, iters=20, warm=3):
         for m in ms:
             x = torch.randn(m, k, device="cuda").half()
             y = torch.empty(m, n, device="cuda", dtype=torch.float16)
-            s = A.stream_of()
             row = {"n": n, "k": k, "m": m}
             for name, fn, wt in (("file", L.aotx_q8_gemv_f16, w), ("repacked", L.aotx_q8r_gemv_f16, wr)):
-                for _ in range(warm):
-                    fn(A.ptr(wt), n, k, A.ptr(x), m, A.ptr(y), s)
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                torch.cuda.synchronize()
-                e0.record()
-                for _ in range(iters):
-                    fn(A.ptr(wt), n, k, A.ptr(x), m, A.ptr(y), s)
-                e1.record()
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1000.0 / iters
+                def launch(st, fn=fn, wt=wt):
+                    A.check(fn(A.ptr(wt), n, k, A.ptr(x), m, A.ptr(y),
+                               ctypes.c_void_p(st.cuda_stream)), "q8 product")
+                us = graph_time(torch, launch, reps=iters)
                 algo = n * k * 34 // 32 + m * k * 2 + m * n * 2
                 row[name + "_us"] = round(us, 2)
                 row[name + "_gbs"] = round(algo / us / 1e3, 1)
@@ -70,6 +78,50 @@ def gemv_table(torch, L, shapes, ms, iters=20, warm=3):
             out.append(row)
         del w, wr
     return out
+
+
+def graph_time(torch, launch, reps=20, replays=5):
+    """Average device time (us) of one `launch(stream)`: `reps` launches captured in a HIP
+    graph on a side stream, replayed `replays` times between HIP events on that stream."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            launch(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(reps):
+            launch(s)
+    with torch.cuda.stream(s):
+        g.replay()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(replays):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / (reps * replays)
+
+
+def attention_rate(torch, L, slots, context, heads, kvh, hd, layers):
+    """The step's attention over the seated pages (layer 0, every slot at its last seated
+    position): (us per launch, algorithmic bytes per launch)."""
+    import aotx_amd as A
+    B = len(slots)
+    q = torch.randn(B, heads, hd, device="cuda").half()
+    out = torch.empty_like(q)
+    pos = torch.full((B,), context - 1, dtype=torch.int32, device="cuda")
+    ag = torch.tensor(slots, dtype=torch.int32, device="cuda")
+
+    def launch(s):
+        A.check(L.aotx_attend_paged(A.ptr(q), A.ptr(pos), A.ptr(ag), B, heads, kvh, hd, 0,
+                                    layers, A.ptr(out), ctypes.c_void_p(s.cuda_stream)),
+                "aotx_attend_paged")
+
+    us = graph_time(torch, launch)
+    algo = B * context * kvh * hd * 2 * 2 + 2 * q.numel() * 2
+    return us, algo
 
 
 def seat_context(torch, rt, slots, context, reserve, layers, kvh, hd):
@@ -149,6 +201,56 @@ def cpu_baseline(region_dev, lay, torch, batch, context, threads):
     return batch / dt, dt
 
 
+def traffic_run(args):
+    """Counter pass workload (`--traffic`): the roofline kernel alone on the same seated
+    KV (32 slots x 2048 positions, 32 layers' layout, layer 0 attended), five launches, then
+    five plain device copies of 256 MiB (the calibration of FETCH_SIZE / WRITE_SIZE per
+    dispatch). No model weights are built."""
+    import torch
+    import aotx_amd as A
+    from aotx_amd.model import LLAMA_8B, layout_pages
+    L = A.lib()
+    shape = LLAMA_8B
+    slots = list(range(args.batch))
+    kvm = A.KvMap()
+    per = layout_pages(args.context + 8, shape.layers, shape.kv_heads, shape.head_dim)
+    kvm.limit = per * len(slots) + 8
+    A.check(L.aotx_kv_open(ctypes.byref(kvm)), "aotx_kv_open")
+    for sl in slots:
+        if L.aotx_kv_request(sl, per) != 1:
+            raise RuntimeError("page request refused")
+    L.aotx_kv_serve(ctypes.byref(kvm), None)
+    n = len(slots) * args.context
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    k = torch.randn(n, shape.kv_heads * shape.head_dim, device="cuda", generator=g).half()
+    v = torch.randn(n, shape.kv_heads * shape.head_dim, device="cuda", generator=g).half()
+    pos = torch.arange(args.context, device="cuda", dtype=torch.int32).repeat(len(slots))
+    ag = torch.tensor(slots, device="cuda", dtype=torch.int32).repeat_interleave(args.context)
+    A.check(L.aotx_kv_write(A.ptr(k), A.ptr(v), A.ptr(pos), A.ptr(ag), n, shape.kv_heads,
+                            shape.head_dim, 0, shape.layers, None), "aotx_kv_write")
+    del k, v, pos, ag
+    B = len(slots)
+    q = torch.randn(B, shape.heads, shape.head_dim, device="cuda").half()
+    out = torch.empty_like(q)
+    qpos = torch.full((B,), args.context - 1, dtype=torch.int32, device="cuda")
+    qag = torch.tensor(slots, dtype=torch.int32, device="cuda")
+    for _ in range(5):
+        A.check(L.aotx_attend_paged(A.ptr(q), A.ptr(qpos), A.ptr(qag), B, shape.heads,
+                                    shape.kv_heads, shape.head_dim, 0, shape.layers,
+                                    A.ptr(out), None), "aotx_attend_paged")
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    L.aotx_kv_close(ctypes.byref(kvm))
+    algo = B * args.context * shape.kv_heads * shape.head_dim * 4 + 2 * q.numel() * 2
+    print(json.dumps({"traffic_workload": "attention", "algorithmic_bytes": algo,
+                      "copy_bytes": src.numel()}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,12 +260,18 @@ def main():
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--traffic", action="store_true",
+                    help="run only the roofline kernel and a calibration copy (counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the token loop's slots are independent; see the sharding note in DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.traffic:
+        traffic_run(args)
+        return
 
     import torch
     import aotx_amd as A
@@ -195,6 +303,10 @@ def main():
                  pool_pages=per_slot * (len(batch_slots) + 1) + 8)
     seat_context(torch, rt, batch_slots + one_slot, args.context, reserve, shape.layers,
                  shape.kv_heads, shape.head_dim)
+    att_us, att_bytes = attention_rate(torch, L, batch_slots, args.context, shape.heads,
+                                       shape.kv_heads, shape.head_dim, shape.layers)
+    log(f"bench: attention batch {args.batch} ctx {args.context}: {att_us:.2f} us, "
+        f"{att_bytes / att_us / 1e3:.1f} GB/s")
     greedy = A.neutral_how()
     tps, ms = decode(torch, rt, batch_slots, args.steps, args.warmup, greedy)
     log(f"bench: batch {args.batch} greedy: {tps:.1f} tokens/s, {ms:.3f} ms/step")
@@ -235,12 +347,19 @@ def main():
         "step_roofline_frac_batch1": round(step_bytes1 / (ms1 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "gemv": table,
     }
+    result["roofline"] = {
+        "bound": "hbm",
+        "kernel": f"aotx_attend_kernel<128,4> (paged decode attention, batch {args.batch}, "
+                  f"context {args.context}, 32/8 heads x 128)",
+        "achieved": round(att_bytes / att_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(att_bytes / att_us / 1e3 / HBM_PEAK_GBS, 4),
+        "traffic": measured_traffic() if args.batch == 32 and args.context == 2048 else None,
+        "bytes_per_launch": att_bytes, "us_per_launch": round(att_us, 2)}
     if dom is not None:
-        result["roofline"] = {
-            "bound": "hbm",
+        result["q8_product_roofline"] = {
             "kernel": f"aotx_rgemv (repacked Q8_0 product) n={dom['n']} k={dom['k']} m={dom['m']}",
             "achieved": dom["repacked_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["repacked_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(dom["repacked_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": dom["bytes"], "us_per_launch": dom["repacked_us"]}
     rt.close()
 
