@@ -9,7 +9,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libaotx_hip.so")
+LIB_PATH = os.environ.get("AOTX_HIP_LIB") or os.path.join(HERE, "libaotx_hip.so")
 
 AOTX_SLOTS = 64
 AOTX_SEQ_MAX_TOKENS = 8192

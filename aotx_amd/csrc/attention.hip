@@ -23,6 +23,7 @@
 #include "aotx_internal.h"
 
 #include <algorithm>
+#include <stdlib.h>
 
 typedef unsigned int aotx_u4a __attribute__((ext_vector_type(4)));
 typedef _Float16 aotx_h2a __attribute__((ext_vector_type(2)));
@@ -46,7 +47,7 @@ struct aotx_attn_args {
 
 #define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
 #define ATTN_MAX_SPLITS 64u
-#define ATTN_TARGET_GROUPS 2048u
+#define ATTN_TARGET_GROUPS 512u
 
 static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 {
@@ -58,6 +59,13 @@ static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 static __device__ __forceinline__ aotx_h2a aotx_as_h2(unsigned int word)
 {
     return __builtin_bit_cast(aotx_h2a, word);
+}
+
+/* 2^x with the hardware v_exp_f32: exp2(-inf) = 0, results below 2^-126 flush to 0 (weights
+ * that small do not change an fp32 sum of weights of order one). */
+static __device__ __forceinline__ float aotx_exp2(float x)
+{
+    return __builtin_amdgcn_exp2f(x);
 }
 
 template <int CTRL>
@@ -79,6 +87,23 @@ static __device__ __forceinline__ float aotx_row_sum(float v)
     return v;
 }
 
+/* Max and sum over the lane groups of LPP lanes (every lane ends with the result). */
+template <int LPP>
+static __device__ __forceinline__ float aotx_groups_max(float v)
+{
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int LPP>
+static __device__ __forceinline__ float aotx_groups_sum(float v)
+{
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
 /* Chunk length of a token with n positions under S splits (whole 64-position units). */
 static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, unsigned int S)
 {
@@ -95,7 +120,7 @@ struct aotx_attn_geom {
 
 /* One workgroup = 4 waves = one (token, KV head, context chunk). */
 template <int D, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 : (G == 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 : (G <= 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
 {
     constexpr int LPP = aotx_attn_geom<D>::LPP;
     constexpr int NG = aotx_attn_geom<D>::NG;
@@ -154,8 +179,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 
     const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
     const unsigned int vbyte = (((a.kv_heads + kh) * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
 
-    aotx_u4a kr[2][U], vr[2][U];
-    bool absent[2];
+    aotx_u4a kr[3][U], vr[3][U];     /* a ring of three blocks: two in flight */
+    bool absent[3];
     /* layout-block pointers of the wave's blocks, 64 at a time, lane i holding block
      * wbase + i; a block is fetched from the lane that holds it */
     unsigned long long pages = 0ull;
@@ -203,11 +228,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 
         _Pragma("unroll") for (int j = 0; j < G; ++j) {                                     \
             float mb = sc[0][j];                                                            \
             _Pragma("unroll") for (int u = 1; u < U; ++u) mb = fmaxf(mb, sc[u][j]);         \
-            _Pragma("unroll") for (int off = LPP; off < 64; off <<= 1)                      \
-                mb = fmaxf(mb, __shfl_xor(mb, off, 64));                                    \
+            mb = aotx_groups_max<LPP>(mb);                                                  \
             float mnew = fmaxf(mrun[j], mb);                                                \
             if (mnew != mrun[j]) {                                                          \
-                float shift = mrun[j] == -INFINITY ? 0.0f : exp2f(mrun[j] - mnew);          \
+                float shift = aotx_exp2(mrun[j] - mnew);    /* 0 from -inf */               \
                 lrun[j] *= shift;                                                           \
                 _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] *= shift;             \
                 mrun[j] = mnew;                                                             \
@@ -221,7 +245,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 
                 vf[2 * e + 1] = aotx_attn_h(vv[e], 1);                                      \
             }                                                                               \
             _Pragma("unroll") for (int j = 0; j < G; ++j) {                                 \
-                float pw = sc[u][j] == -INFINITY ? 0.0f : exp2f(sc[u][j] - mrun[j]);        \
+                float pw = aotx_exp2(sc[u][j] - mrun[j]);   /* 0 for a masked position */   \
                 lrun[j] += pw;                                                              \
                 _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] += pw * vf[e];        \
             }                                                                               \
@@ -232,13 +256,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 
         unsigned int b = b0;
         ATTN_WINDOW(b0);
         ATTN_LOAD(0, b);
+        if (b + 1u < b1) ATTN_LOAD(1, b + 1u);
         for (;;) {
-            if (b + 1u < b1) ATTN_LOAD(1, b + 1u);
+            if (b + 2u < b1) ATTN_LOAD(2, b + 2u);
             ATTN_COMPUTE(0, b);
             b += 1u;
             if (b >= b1) break;
-            if (b + 1u < b1) ATTN_LOAD(0, b + 1u);
+            if (b + 2u < b1) ATTN_LOAD(0, b + 2u);
             ATTN_COMPUTE(1, b);
+            b += 1u;
+            if (b >= b1) break;
+            if (b + 2u < b1) ATTN_LOAD(1, b + 2u);
+            ATTN_COMPUTE(2, b);
             b += 1u;
             if (b >= b1) break;
         }
@@ -251,17 +280,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 2 ? 3 
      * hold the same weights) */
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-        float l = lrun[j];
+        lrun[j] = aotx_groups_sum<LPP>(lrun[j]);
 #pragma unroll
-        for (int off = LPP; off < 64; off <<= 1) l += __shfl_xor(l, off, 64);
-        lrun[j] = l;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = o[j][e];
-#pragma unroll
-            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-            o[j][e] = v;
-        }
+        for (int e = 0; e < 8; ++e) o[j][e] = aotx_groups_sum<LPP>(o[j][e]);
     }
     missing = __any(missing);
     if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
@@ -360,9 +381,15 @@ __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
 unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
                               unsigned int max_context)
 {
-    /* about ATTN_TARGET_GROUPS workgroups over the launch, chunks of at least 64 positions */
+    /* about ATTN_TARGET_GROUPS workgroups over the launch (AOTX_ATTN_GROUPS overrides it
+     * for measurement sweeps), chunks of at least 64 positions */
+    static const unsigned int target = [] {
+        const char *e = getenv("AOTX_ATTN_GROUPS");
+        unsigned int v = e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 0u;
+        return v != 0u ? v : ATTN_TARGET_GROUPS;
+    }();
     unsigned int units = tokens * kv_heads;
-    unsigned int s = (ATTN_TARGET_GROUPS + units - 1u) / units;
+    unsigned int s = (target + units - 1u) / units;
     unsigned int cap = (max_context + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN;
     if (s > cap) s = cap;
     if (s > ATTN_MAX_SPLITS) s = ATTN_MAX_SPLITS;
