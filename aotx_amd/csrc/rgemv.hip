@@ -31,6 +31,14 @@ typedef unsigned int rg_u4 __attribute__((ext_vector_type(4)));
 
 #define RG_THREADS 256
 
+/* A kernel-constant word read through the scalar cache (counted by lgkmcnt, so waiting for
+ * it does not wait for the vector loads issued before it). Only for memory no kernel of
+ * the same launch writes. */
+static __device__ __forceinline__ unsigned int rg_scalar(const unsigned int *p)
+{
+    return *(const __attribute__((address_space(4))) unsigned int *)p;
+}
+
 /* Workgroup barrier that waits for this wave's LDS operations only: global loads already
  * in flight (the weight stream) stay in flight across it. */
 static __device__ __forceinline__ void rg_sync_lds()
@@ -174,20 +182,29 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
     const unsigned int gr = rt * 16u;
 #define RG_YROW(mm) (list != nullptr ? list[(mm)] : a.m0 + (mm))
     if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr) {
-        /* one thread per (tile, row of x): add the 16 results of the tile into the residual
-         * stream and leave the tile's sum of squares for the next norm */
-        for (unsigned int idx = tid; idx < rt * MT; idx += NT) {
-            unsigned int j = idx % rt, mm = idx / rt;
-            unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
-            if (mm >= mrows || v0 >= a.n) continue;
-            float *row = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0;
-            float s = 0.0f;
-            for (unsigned int rr = 0; rr < 16u && v0 + rr < a.n; ++rr) {
-                float v = row[rr] + out[(j * 16u + rr) * MT + mm];
-                row[rr] = v;
-                s += v * v;
+        /* one thread per output: 16 consecutive threads hold the 16 rows of one tile for
+         * one row of x, add them into the residual stream, and leave the tile's sum of
+         * squares for the next norm with a 16-lane shuffle sum */
+        const unsigned int total = rt * 16u * MT;          /* a multiple of 16 */
+        for (unsigned int base = 0; base < total; base += NT) {
+            const unsigned int idx = base + tid;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % rt, mm = rest / rt;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
+            const bool row_ok = idx < total && mm < mrows && v0 < a.n;
+            float v = 0.0f;
+            if (row_ok && v0 + rr < a.n) {
+                float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
+                v = *p + out[(j * 16u + rr) * MT + mm];
+                *p = v;
             }
-            a.sumsq_out[(unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u] = s;
+            float sq = v * v;
+            sq += __shfl_xor(sq, 1, 64);
+            sq += __shfl_xor(sq, 2, 64);
+            sq += __shfl_xor(sq, 4, 64);
+            sq += __shfl_xor(sq, 8, 64);
+            if (row_ok && rr == 0u)
+                a.sumsq_out[(unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u] = sq;
         }
     } else if (a.epi == AOTX_EPI_F32 || a.epi == AOTX_EPI_F16 || a.epi == AOTX_EPI_RESID) {
         for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
@@ -279,16 +296,12 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
     if (a.expert_stride != 0ull) {
-        unsigned int total = a.list_count[expert];
+        /* an expert no row chose streams nothing */
+        unsigned int total = rg_scalar(a.list_count + expert);
         mrows = total > a.m0 ? total - a.m0 : 0u;
         list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
-    } else if (a.m_dev != nullptr) {
-        unsigned int total = *a.m_dev;
-        mrows = total > a.m0 ? total - a.m0 : 0u;
+        if (mrows == 0u) return;
     }
-    if (mrows > a.m) mrows = a.m;
-    if (mrows > (unsigned int)MT) mrows = MT;
-    if (mrows == 0u) return;
 
     const unsigned int group = blockIdx.x / a.splits;
     const unsigned int split = blockIdx.x % a.splits;
@@ -297,6 +310,8 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     const unsigned int kr = a.qps * 128u;          /* LDS k capacity */
     const unsigned int xs = kr + 8u;               /* LDS x row stride (halves) */
     unsigned short *xl = (unsigned short *)lds;
+    __shared__ unsigned int xsrc[MT];              /* source row of each batch row */
+    __shared__ float xscale[MT];                   /* its RMSNorm scale (AOTX_X_NORM) */
 
     /* ---- per-wave k quarter ---- */
     const unsigned int nq = q1 - q0;
@@ -321,13 +336,16 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
     rg_u4 wa[2][PD][RT][2];
-    unsigned short ws[2][PD][RT];
+    unsigned int ws[2][PD][RT];    /* one 32-bit register per scale: no packing waits */
 
+    /* loads past the wave's range repeat its last quad (a cache hit), so every load can be
+     * issued unconditionally: no register copies that would wait for them */
+    const unsigned int qlast = wq0 < wq1 ? wq1 - 1u : q0;
 #define RG_LOAD(BUF, QS)                                                                 \
     do {                                                                                 \
         _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
             unsigned int qq = (QS) + (unsigned int)qi;                                   \
-            if (qq >= wq1) qq = wq1 - 1u;                                                \
+            if (qq > qlast) qq = qlast;                                                  \
             _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
                 const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
                 wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
@@ -373,80 +391,107 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
-    /* the first weight loads go out before x is staged, so their latency overlaps it */
-    if (wq0 < wq1) RG_LOAD(0, wq0);
+    /* the first weight loads go out before anything else, so their latency overlaps the
+     * row count, the row sources and the x staging */
+    RG_LOAD(0, wq0);
+    RG_LOAD(1, wq0 + PD);
+    if (a.expert_stride == 0ull && a.m_dev != nullptr) {
+        unsigned int total = rg_scalar(a.m_dev);
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+    if (mrows == 0u) return;
 
     /* ---- stage the batch rows of x for [q0, q1) ---- */
     {
         const unsigned int kbeg = q0 * 128u;
-        const unsigned int kend = q1 * 128u;
-        const unsigned int width = kend - kbeg;          /* multiple of 128 */
+        const unsigned int width = (q1 - q0) * 128u;
         const unsigned int pieces = width / 8u;          /* 16-byte pieces per row */
-        if (a.xmode == AOTX_X_NORM) {
-            __shared__ float share[4];
-            const unsigned int nss = (a.k + 15u) / 16u;
-            for (unsigned int mm = 0; mm < mrows; ++mm) {
-                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
-                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
-                const float *ss = a.sumsq + (unsigned long long)src * nss;
+        /* sources (and norm scales: 16 threads per row add its partial sums of squares) */
+        {
+            const unsigned int mm = tid >> 4, l = tid & 15u;
+            unsigned int src = 0u;
+            if (mm < mrows)
+                src = list != nullptr ? list[mm] / a.xrow_div
+                    : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+            if (l == 0u && mm < mrows) xsrc[mm] = src;
+            if (a.xmode == AOTX_X_NORM) {
+                const unsigned int nss = (a.k + 15u) / 16u;
                 float sum = 0.0f;
-                for (unsigned int i = tid; i < nss; i += RG_THREADS) sum += ss[i];
-                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                if (lane == 0u) share[wave] = sum;
-                rg_sync_lds();
-                sum = share[0] + share[1] + share[2] + share[3];
-                rg_sync_lds();
-                const float scale = rsqrtf(sum / (float)a.k + a.eps);
-                const float *r = a.resid + (unsigned long long)src * a.k;
-                for (unsigned int p = tid; p < pieces; p += RG_THREADS) {
-                    unsigned int kk = kbeg + p * 8u;
-                    unsigned int h[8];
+                if (mm < mrows) {
+                    const float *ss = a.sumsq + (unsigned long long)src * nss;
+#pragma unroll 4
+                    for (unsigned int i = l; i < nss; i += 16u) sum += ss[i];
+                }
+                sum += __shfl_xor(sum, 1, 64);
+                sum += __shfl_xor(sum, 2, 64);
+                sum += __shfl_xor(sum, 4, 64);
+                sum += __shfl_xor(sum, 8, 64);
+                if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
+            }
+        }
+        rg_sync_lds();
+        for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
+            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            const unsigned int src = xsrc[mm];
+            const unsigned int kk = kbeg + p * 8u;
+            rg_u4 v = {0u, 0u, 0u, 0u};
+            if (a.xmode == AOTX_X_NORM) {
+                const float scale = xscale[mm];
+                const float *rrow = a.resid + (unsigned long long)src * a.k;
+                float rv[8], wv[8];
+                if (kk + 8u <= a.k) {
+                    rg_f4 r0 = *(const rg_f4 *)(rrow + kk), r1 = *(const rg_f4 *)(rrow + kk + 4u);
+                    rg_f4 w0 = *(const rg_f4 *)(a.norm_w + kk), w1 = *(const rg_f4 *)(a.norm_w + kk + 4u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        rv[e] = r0[e];
+                        rv[4 + e] = r1[e];
+                        wv[e] = w0[e];
+                        wv[4 + e] = w1[e];
+                    }
+                } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         unsigned int kc = kk + (unsigned int)e;
-                        h[e] = kc < a.k ? aotx_f2h(scale * r[kc] * a.norm_w[kc]) : 0u;
+                        rv[e] = kc < a.k ? rrow[kc] : 0.0f;
+                        wv[e] = kc < a.k ? a.norm_w[kc] : 0.0f;
                     }
-                    rg_u4 v = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                               h[6] | (h[7] << 16)};
-                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
                 }
-            }
-        } else {
-            for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
-                unsigned int mm = idx / pieces, p = idx - mm * pieces;
-                unsigned int src = list != nullptr ? list[mm] / a.xrow_div
-                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
-                unsigned int kk = kbeg + p * 8u;
-                rg_u4 v = {0u, 0u, 0u, 0u};
-                if (kk + 8u <= a.k) {
-                    v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
-                } else if (kk < a.k) {
-                    unsigned int h[8];
+                unsigned int h[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
-                    v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                                h[6] | (h[7] << 16)};
-                }
-                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+                for (int e = 0; e < 8; ++e) h[e] = aotx_f2h(scale * rv[e] * wv[e]);
+                v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                            h[6] | (h[7] << 16)};
+            } else if (kk + 8u <= a.k) {
+                v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
+            } else if (kk < a.k) {
+                unsigned int h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
+                v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                            h[6] | (h[7] << 16)};
             }
+            *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
         }
         rg_sync_lds();
     }
 
+    /* both load buffers were filled before the staging; each is refilled right after its
+     * quads are computed, two steps ahead */
     if (wq0 < wq1) {
         unsigned int q = wq0;
         for (;;) {
-            unsigned int qn1 = q + PD;
-            if (qn1 < wq1) RG_LOAD(1, qn1);
             RG_COMPUTE(0, q);
-            q = qn1;
+            q += PD;
             if (q >= wq1) break;
-            unsigned int qn2 = q + PD;
-            if (qn2 < wq1) RG_LOAD(0, qn2);
+            RG_LOAD(0, q + PD);
             RG_COMPUTE(1, q);
-            q = qn2;
+            q += PD;
             if (q >= wq1) break;
+            RG_LOAD(1, q + PD);
         }
     }
 #undef RG_LOAD
@@ -504,11 +549,11 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
     if (a.expert_stride != 0ull) {
-        unsigned int total = a.list_count[expert];
+        unsigned int total = rg_scalar(a.list_count + expert);
         mrows = total > a.m0 ? total - a.m0 : 0u;
         list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
     } else if (a.m_dev != nullptr) {
-        unsigned int total = *a.m_dev;
+        unsigned int total = rg_scalar(a.m_dev);
         mrows = total > a.m0 ? total - a.m0 : 0u;
     }
     if (mrows > a.m) mrows = a.m;
@@ -539,7 +584,7 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
 #pragma unroll
         for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
     rg_u4 wa[2][PD][RT][2];
-    unsigned short ws[2][PD][RT];
+    unsigned int ws[2][PD][RT];    /* one 32-bit register per scale: no packing waits */
 
 #define RGW_LOAD(BUF, QS)                                                                \
     do {                                                                                 \
@@ -624,9 +669,9 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
 #pragma unroll
         for (int h = 0; h < RGW_KC / (2 * PD); ++h) {
             unsigned int qa = q0 + c * RGW_KC + (unsigned int)(2 * PD * h);
-            if (qa + PD < q1) RGW_LOAD(1, qa + PD);
+            RGW_LOAD(1, qa + PD);
             RGW_COMPUTE(0, qa, xb);
-            if (qa + 2 * PD < q1) RGW_LOAD(0, qa + 2 * PD);
+            RGW_LOAD(0, qa + 2 * PD);
             RGW_COMPUTE(1, qa + PD, xb);
         }
         if (c + 1u < nch) RGW_XSTORE(c + 1u);
@@ -670,11 +715,11 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args 
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
     if (a.expert_stride != 0ull) {
-        unsigned int total = a.list_count[expert];
+        unsigned int total = rg_scalar(a.list_count + expert);
         mrows = total > a.m0 ? total - a.m0 : 0u;
         list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
     } else if (a.m_dev != nullptr) {
-        unsigned int total = *a.m_dev;
+        unsigned int total = rg_scalar(a.m_dev);
         mrows = total > a.m0 ? total - a.m0 : 0u;
     }
     if (mrows > a.m) mrows = a.m;
