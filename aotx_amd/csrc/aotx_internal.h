@@ -43,6 +43,8 @@ aotx_state *aotx_state_device(void);
  * per use; counters are zeroed once at allocation and every kernel that uses one puts
  * it back to zero before it exits. */
 void *aotx_scratch(int which, size_t bytes);
+/* 4 KB of pinned host memory for step read-backs (one host thread per runtime). */
+void *aotx_pinned(void);
 enum {
     AOTX_SCRATCH_GEMV_PARTIAL = 0,
     AOTX_SCRATCH_GEMV_COUNT,

@@ -46,12 +46,18 @@ struct aotx_attn_args {
 };
 
 #define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
-#define ATTN_MAX_SPLITS 64u
+#define ATTN_MAX_SPLITS 32u
 #define ATTN_TARGET_GROUPS 512u
 
 static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 {
     return aotx_h2f((unsigned short)(hi ? (word >> 16) : (word & 0xFFFFu)));
+}
+
+/* A kernel-constant word (the device token count) read through the scalar cache. */
+static __device__ __forceinline__ unsigned int aotx_attn_scalar(const unsigned int *p)
+{
+    return *(const __attribute__((address_space(4))) unsigned int *)p;
 }
 
 /* fp16 pair from one 32-bit word. The word arrives by value: a __builtin_bit_cast of a
@@ -132,7 +138,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 
     const unsigned int wave = threadIdx.x >> 6;
     const unsigned int grp = lane / LPP;
     const unsigned int sub = lane % LPP;
-    unsigned int tokens = a.m_dev ? *a.m_dev : a.tokens;
+    unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
     const unsigned int S = a.splits;
     const unsigned int c = blockIdx.x % S;
@@ -328,17 +334,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 
 }
 
 /* Merge the chunks of every (token, KV head) that was split, in chunk order:
- * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). One wave per
- * query head computes the chunk weights (a lane per chunk, wave reductions), then every
- * thread adds its column over the chunks with independent loads. */
+ * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). One workgroup
+ * per (token, KV head, query head), one thread per output column; every thread issues all
+ * of its loads (each chunk's maximum, mass and sum) at once and forms the chunk weights
+ * itself, so the merge is one round trip to memory with no LDS and no barrier. */
 template <int D, int G>
-__global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
+__global__ __launch_bounds__(D) void aotx_attend_merge(aotx_attn_args a)
 {
-    __shared__ float fw[ATTN_MAX_SPLITS][G];
-    __shared__ float inv[G];
-    unsigned int tokens = a.m_dev ? *a.m_dev : a.tokens;
+    unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
     const unsigned int unit = blockIdx.x;
+    const unsigned int j = blockIdx.y;
+    const unsigned int e = threadIdx.x;
     const unsigned int kh = unit % a.kv_heads;
     const unsigned int t = unit / a.kv_heads;
     if (t >= tokens) return;
@@ -348,30 +355,29 @@ __global__ __launch_bounds__(256) void aotx_attend_merge(aotx_attn_args a)
     const unsigned int st = (n + chunk - 1u) / chunk;
     if (st <= 1u) return;
     const unsigned int stride = G * (D + 2);
-    const float *all = a.partial + (unsigned long long)unit * S * stride;
-    const unsigned int lane = threadIdx.x & 63u;
-    for (unsigned int j = threadIdx.x >> 6; j < (unsigned int)G; j += 4u) {
-        float mc = lane < st ? all[lane * stride + j * (D + 2)] : -INFINITY;
-        float lc = lane < st ? all[lane * stride + j * (D + 2) + 1] : 0.0f;
-        float top = mc;
-        for (int off = 32; off > 0; off >>= 1) top = fmaxf(top, __shfl_xor(top, off, 64));
-        float f = (mc == -INFINITY) ? 0.0f : exp2f(mc - top);
-        if (lane < st) fw[lane][j] = f;
-        /* chunk-order sum of the masses */
-        float w = lc * f;
-        float msum = 0.0f;
-        for (unsigned int cc = 0; cc < st; ++cc) msum += __shfl(w, (int)cc, 64);
-        if (lane == 0u) inv[j] = msum > 0.0f ? 1.0f / msum : 0.0f;
+    const float *all = a.partial + (unsigned long long)unit * S * stride + j * (D + 2);
+    float mc[ATTN_MAX_SPLITS], lc[ATTN_MAX_SPLITS], oc[ATTN_MAX_SPLITS];
+#pragma unroll
+    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) {
+        const bool live = c < st;
+        mc[c] = live ? all[c * stride] : -INFINITY;
+        lc[c] = live ? all[c * stride + 1u] : 0.0f;
+        oc[c] = live ? all[c * stride + 2u + e] : 0.0f;
     }
-    __syncthreads();
-    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += blockDim.x) {
-        unsigned int j = idx / D;
-        unsigned int e = idx - j * D;
-        float osum = 0.0f;
-#pragma unroll 8
-        for (unsigned int cc = 0; cc < st; ++cc) osum += all[cc * stride + j * (D + 2) + 2 + e] * fw[cc][j];
-        a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * inv[j]);
+    float top = -INFINITY;
+#pragma unroll
+    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) top = fmaxf(top, mc[c]);
+    float msum = 0.0f, osum = 0.0f;
+#pragma unroll
+    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) {
+        if (c < st) {
+            const float f = mc[c] == -INFINITY ? 0.0f : aotx_exp2(mc[c] - top);
+            msum += lc[c] * f;
+            osum += oc[c] * f;
+        }
     }
+    const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
+    a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
 }
 
 /* ---------------------------------------------------------------------------------------
@@ -439,8 +445,8 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
         hipLaunchKernelGGL((aotx_attend_kernel<DD, GG>), grid, dim3(256), 0, stream, a);   \
         AOTX_LAUNCH_CHECK();                                                               \
         if (a.splits > 1u) {                                                               \
-            hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads),       \
-                               dim3(256), 0, stream, a);                                   \
+            hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads, GG),   \
+                               dim3(DD), 0, stream, a);                                    \
         }                                                                                  \
     } while (0)
     if (head_dim == 128u) {

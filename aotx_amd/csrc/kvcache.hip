@@ -84,10 +84,10 @@ extern "C" int aotx_kv_serve(aotx_kv_map *map, void *stream)
     if (map == nullptr || map->range == 0ull) return 0;
     hipStream_t s = aotx_stream(stream);
     aotx_state *state = aotx_state_device();
-    unsigned int marks[2] = {0u, 0u};
+    unsigned int *marks = (unsigned int *)aotx_pinned();
+    AOTX_CHECK(hipMemcpyAsync(marks, (unsigned char *)&state->kv + offsetof(aotx_kv_table, made),
+                              2u * sizeof *marks, hipMemcpyDeviceToHost, s));
     AOTX_CHECK(hipStreamSynchronize(s));
-    AOTX_CHECK(hipMemcpy(marks, (unsigned char *)&state->kv + offsetof(aotx_kv_table, made),
-                         sizeof marks, hipMemcpyDeviceToHost));
     if (marks[0] == marks[1]) return 0;
     static aotx_kv_table table;
     AOTX_CHECK(hipMemcpy(&table, &state->kv, sizeof table, hipMemcpyDeviceToHost));

@@ -730,13 +730,15 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
 static int aotx_call_set(aotx_model_run *set, const int *ids, const unsigned int *offset,
                          unsigned int seqs, const unsigned int *agent)
 {
-    unsigned int rows[AOTX_SLOTS + 1u];
+    unsigned int *rows = (unsigned int *)aotx_pinned();
     memset(set, 0, sizeof *set);
     if (seqs == 0u || seqs > AOTX_SLOTS || ids == nullptr || offset == nullptr || agent == nullptr) {
         fprintf(stderr, "a pass of %u sequences is outside the bounds\n", seqs);
         return 1;
     }
-    AOTX_CHECK(hipMemcpy(rows, offset, (seqs + 1u) * sizeof *rows, hipMemcpyDeviceToHost));
+    AOTX_CHECK(hipMemcpyAsync(rows, offset, (seqs + 1u) * sizeof *rows, hipMemcpyDeviceToHost,
+                              nullptr));
+    AOTX_CHECK(hipStreamSynchronize(nullptr));
     for (unsigned int s = 0u; s < seqs; ++s) {
         if (rows[s + 1u] <= rows[s]) {
             fprintf(stderr, "the sequence %u of the pass holds no token\n", s);

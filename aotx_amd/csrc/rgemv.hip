@@ -176,7 +176,8 @@ static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a,
 template <int MT, int NT>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
-                                                   unsigned int mrows, const unsigned int *list)
+                                                   unsigned int mrows, const unsigned int *list,
+                                                   const float *rpre = nullptr)
 {
     const unsigned int tid = threadIdx.x;
     const unsigned int gr = rt * 16u;
@@ -195,7 +196,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             float v = 0.0f;
             if (row_ok && v0 + rr < a.n) {
                 float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
-                v = *p + out[(j * 16u + rr) * MT + mm];
+                v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : *p) + out[(j * 16u + rr) * MT + mm];
                 *p = v;
             }
             float sq = v * v;
@@ -283,6 +284,47 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
 #undef RG_YROW
 }
 
+/* Eight fp16 values x = half(scale * r * w) of the fused norm (cuda/model/norm.cu:49-77),
+ * from the residual and norm-weight words already loaded. */
+static __device__ __forceinline__ rg_u4 rg_norm_piece(rg_u4 r0, rg_u4 r1, rg_u4 w0, rg_u4 w1,
+                                                      float scale)
+{
+    unsigned int rw[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    unsigned int ww[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+    unsigned int h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        h[e] = aotx_f2h(scale * __builtin_bit_cast(float, rw[e]) * __builtin_bit_cast(float, ww[e]));
+    return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
+/* Eight values of row `src` of x from k = kk (fp16 x, or the fused norm of the residual
+ * stream when scale != 0 is given for AOTX_X_NORM); k past a.k gives zeros. */
+static __device__ __forceinline__ rg_u4 rg_x_piece(const aotx_rgemv_args &a, unsigned int src,
+                                                   unsigned int kk, float scale)
+{
+    if (a.xmode == AOTX_X_NORM) {
+        const float *rrow = a.resid + (unsigned long long)src * a.k;
+        if (kk + 8u <= a.k)
+            return rg_norm_piece(*(const rg_u4 *)(rrow + kk), *(const rg_u4 *)(rrow + kk + 4u),
+                                 *(const rg_u4 *)(a.norm_w + kk), *(const rg_u4 *)(a.norm_w + kk + 4u),
+                                 scale);
+        unsigned int h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            unsigned int kc = kk + (unsigned int)e;
+            h[e] = kc < a.k ? aotx_f2h(scale * rrow[kc] * a.norm_w[kc]) : 0u;
+        }
+        return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    if (kk + 8u <= a.k) return *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
+    unsigned int h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
+    return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
  * loaded ahead per wave. */
 template <int MT, int RT, int PD>
@@ -355,44 +397,109 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
+#ifdef AOTX_EXPERIMENT_NOCOMPUTE
+#define RG_COMPUTE(BUF, QS)                                                              \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi)                                \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j)                               \
+                acc[j][0][0] += __builtin_bit_cast(float, (wa[BUF][qi][j][0].x ^ wa[BUF][qi][j][0].y ^ wa[BUF][qi][j][0].z ^ wa[BUF][qi][j][0].w ^ wa[BUF][qi][j][1].x ^ wa[BUF][qi][j][1].y ^ wa[BUF][qi][j][1].z ^ wa[BUF][qi][j][1].w ^ ws[BUF][qi][j]) & 0x3f800000u); \
+    } while (0)
+#else
+    /* Branch-free: a quad past the wave's range reads the last quad's x and has its scale
+     * forced to zero (it adds nothing); a batch column past mrows reads row 0 of x (its
+     * results are never written). */
 #define RG_COMPUTE(BUF, QS)                                                              \
     do {                                                                                 \
         _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            unsigned int qq = (QS) + (unsigned int)qi;                                   \
-            if (qq < wq1) {                                                              \
-                const unsigned short *xq = xl + (qq - q0) * 128u + 32u * g;             \
-                rg_h8 B[MT / 16][4];                                                     \
-                _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                    \
-                    unsigned int mm = (unsigned int)t * 16u + r;                         \
-                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
-                        B[t][s] = mm < mrows ? *(const rg_h8 *)(xq + mm * xs + 8u * s)   \
-                                             : (rg_h8){0, 0, 0, 0, 0, 0, 0, 0};          \
-                    }                                                                    \
-                }                                                                        \
-                _Pragma("unroll") for (int j = 0; j < RT; ++j) {                         \
-                    unsigned int sbits = ws[BUF][qi][j];                                 \
-                    rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));         \
-                    const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];        \
-                    unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                \
-                                          q1v[0], q1v[1], q1v[2], q1v[3]};               \
-                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
-                        unsigned int d0, d1, d2, d3;                                     \
-                        rg_dequant4(qd[2 * s], s2, d0, d1);                              \
-                        rg_dequant4(qd[2 * s + 1], s2, d2, d3);                          \
-                        rg_u4 av = {d0, d1, d2, d3};                                     \
-                        rg_h8 A = __builtin_bit_cast(rg_h8, av);                         \
-                        _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {            \
-                            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(           \
-                                A, B[t][s], acc[j][t], 0, 0, 0);                         \
-                        }                                                                \
-                    }                                                                    \
+            const unsigned int qq = (QS) + (unsigned int)qi;                             \
+            const unsigned int qx = qq > qlast ? qlast : qq;                             \
+            const unsigned short *xq = xl + (qx - q0) * 128u + 32u * g;                  \
+            rg_h8 B[MT / 16][4];                                                         \
+            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
+                const unsigned int mm = (unsigned int)t * 16u + r;                       \
+                const unsigned int mr = mm < mrows ? mm : 0u;                            \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
+                    B[t][s] = *(const rg_h8 *)(xq + mr * xs + 8u * s);                   \
+            }                                                                            \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const unsigned int sbits = qq < wq1 ? ws[BUF][qi][j] : 0u;               \
+                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
+                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
+                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
+                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
+                    unsigned int d0, d1, d2, d3;                                         \
+                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
+                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
+                    rg_u4 av = {d0, d1, d2, d3};                                         \
+                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
+                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
+                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
+                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
                 }                                                                        \
             }                                                                            \
         }                                                                                \
     } while (0)
+#endif
 
-    /* the first weight loads go out before anything else, so their latency overlaps the
-     * row count, the row sources and the x staging */
+    /* ---- loads that do not depend on the weights go out first. With direct rows (batch
+     * row i is row m0 + i: no expert list, no row map) that is the first RG_PRE staging
+     * rounds of x (or of the residual and norm weights, plus the sums of squares, for the
+     * fused norm) and the residual values the epilogue adds to, for every row the pass
+     * may hold. vmcnt counts in issue order, so these must precede the weight stream to
+     * be waited for without it. ---- */
+    constexpr int RG_PRE = 2;
+    const bool direct = list == nullptr && a.xrow == nullptr;
+    const bool norm = a.xmode == AOTX_X_NORM;
+    const bool resid_pre = direct && a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
+    const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
+    const unsigned int kbeg = q0 * 128u;
+    const unsigned int pieces = (q1 - q0) * 16u;       /* 16-byte pieces (8 values) per row */
+    const unsigned int nss = (a.k + 15u) / 16u;
+    __shared__ float rres[RT * 16 * MT];               /* the epilogue's residual values */
+    rg_u4 pre[RG_PRE][4];
+    float ssp[16];
+    float rold[RT];
+    if (direct) {
+#pragma unroll
+        for (int i = 0; i < RG_PRE; ++i) {
+            const unsigned int idx = tid + (unsigned int)i * RG_THREADS;
+            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            const unsigned int kk = kbeg + p * 8u;
+            pre[i][0] = pre[i][1] = pre[i][2] = pre[i][3] = (rg_u4){0u, 0u, 0u, 0u};
+            if (mm < cap && kk + 8u <= a.k) {
+                if (norm) {
+                    const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
+                    pre[i][0] = *(const rg_u4 *)rrow;
+                    pre[i][1] = *(const rg_u4 *)(rrow + 4);
+                    pre[i][2] = *(const rg_u4 *)(a.norm_w + kk);
+                    pre[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
+                } else {
+                    pre[i][0] = *(const rg_u4 *)(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
+                }
+            }
+        }
+        if (norm) {
+            const unsigned int mm = tid >> 4, l = tid & 15u;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const unsigned int at = l + 16u * (unsigned int)i;
+                ssp[i] = mm < cap && at < nss ? a.sumsq[(unsigned long long)(a.m0 + mm) * nss + at] : 0.0f;
+            }
+        }
+    }
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < RT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * RG_THREADS;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % RT, mm = rest / RT;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
+            rold[it] = mm < cap && v0 + rr < a.n
+                ? ((const float *)a.y)[(unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr] : 0.0f;
+        }
+    }
+
     RG_LOAD(0, wq0);
     RG_LOAD(1, wq0 + PD);
     if (a.expert_stride == 0ull && a.m_dev != nullptr) {
@@ -405,21 +512,22 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
 
     /* ---- stage the batch rows of x for [q0, q1) ---- */
     {
-        const unsigned int kbeg = q0 * 128u;
-        const unsigned int width = (q1 - q0) * 128u;
-        const unsigned int pieces = width / 8u;          /* 16-byte pieces per row */
-        /* sources (and norm scales: 16 threads per row add its partial sums of squares) */
+        /* sources, and norm scales (16 threads per row add its partial sums of squares) */
         {
             const unsigned int mm = tid >> 4, l = tid & 15u;
-            unsigned int src = 0u;
-            if (mm < mrows)
-                src = list != nullptr ? list[mm] / a.xrow_div
-                    : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+            unsigned int src = a.m0 + mm;
+            if (!direct && mm < mrows)
+                src = list != nullptr ? list[mm] / a.xrow_div : a.xrow[a.m0 + mm];
             if (l == 0u && mm < mrows) xsrc[mm] = src;
-            if (a.xmode == AOTX_X_NORM) {
-                const unsigned int nss = (a.k + 15u) / 16u;
+            if (norm) {
                 float sum = 0.0f;
-                if (mm < mrows) {
+                if (direct) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) sum += ssp[i];
+                    if (mm < mrows)
+                        for (unsigned int i = l + 256u; i < nss; i += 16u)
+                            sum += a.sumsq[(unsigned long long)src * nss + i];
+                } else if (mm < mrows) {
                     const float *ss = a.sumsq + (unsigned long long)src * nss;
 #pragma unroll 4
                     for (unsigned int i = l; i < nss; i += 16u) sum += ss[i];
@@ -431,50 +539,35 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
                 if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
             }
         }
-        rg_sync_lds();
-        for (unsigned int idx = tid; idx < mrows * pieces; idx += RG_THREADS) {
-            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-            const unsigned int src = xsrc[mm];
-            const unsigned int kk = kbeg + p * 8u;
-            rg_u4 v = {0u, 0u, 0u, 0u};
-            if (a.xmode == AOTX_X_NORM) {
-                const float scale = xscale[mm];
-                const float *rrow = a.resid + (unsigned long long)src * a.k;
-                float rv[8], wv[8];
-                if (kk + 8u <= a.k) {
-                    rg_f4 r0 = *(const rg_f4 *)(rrow + kk), r1 = *(const rg_f4 *)(rrow + kk + 4u);
-                    rg_f4 w0 = *(const rg_f4 *)(a.norm_w + kk), w1 = *(const rg_f4 *)(a.norm_w + kk + 4u);
+        if (resid_pre) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        rv[e] = r0[e];
-                        rv[4 + e] = r1[e];
-                        wv[e] = w0[e];
-                        wv[4 + e] = w1[e];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        unsigned int kc = kk + (unsigned int)e;
-                        rv[e] = kc < a.k ? rrow[kc] : 0.0f;
-                        wv[e] = kc < a.k ? a.norm_w[kc] : 0.0f;
-                    }
-                }
-                unsigned int h[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = aotx_f2h(scale * rv[e] * wv[e]);
-                v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                            h[6] | (h[7] << 16)};
-            } else if (kk + 8u <= a.k) {
-                v = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);
-            } else if (kk < a.k) {
-                unsigned int h[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
-                v = (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                            h[6] | (h[7] << 16)};
+            for (int it = 0; it < RT; ++it) {
+                const unsigned int idx = tid + (unsigned int)it * RG_THREADS;
+                const unsigned int rr = idx & 15u, rest = idx >> 4;
+                rres[((rest % RT) * 16u + rr) * MT + rest / RT] = rold[it];
             }
-            *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+        }
+        rg_sync_lds();
+        const unsigned int total = mrows * pieces;
+#pragma unroll
+        for (int i = 0; i < RG_PRE; ++i) {
+            const unsigned int idx = tid + (unsigned int)i * RG_THREADS;
+            if (idx < total) {
+                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                const unsigned int kk = kbeg + p * 8u;
+                rg_u4 v;
+                if (direct && kk + 8u <= a.k)
+                    v = norm ? rg_norm_piece(pre[i][0], pre[i][1], pre[i][2], pre[i][3], xscale[mm])
+                             : pre[i][0];
+                else
+                    v = rg_x_piece(a, xsrc[mm], kk, norm ? xscale[mm] : 0.0f);
+                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+            }
+        }
+        for (unsigned int idx = tid + RG_PRE * RG_THREADS; idx < total; idx += RG_THREADS) {
+            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            *(rg_u4 *)(xl + mm * xs + p * 8u) = rg_x_piece(a, xsrc[mm], kbeg + p * 8u,
+                                                          norm ? xscale[mm] : 0.0f);
         }
         rg_sync_lds();
     }
@@ -522,7 +615,7 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) mine[idx] = out[idx];
         return;
     }
-    rg_epilogue<MT, RG_THREADS>(a, out, group, RT, mrows, list);
+    rg_epilogue<MT, RG_THREADS>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
 }
 
 /* Wide batches (17..32 rows of x, fp16 x in memory): W waves split the workgroup's
@@ -813,14 +906,10 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
     }
-    /* rows per workgroup: gate/up pairs need an even tile count. Narrow batches take fewer
-     * tiles while that leaves fewer than ~1024 workgroups. */
+    /* rows per workgroup: 4 tiles share the staged x of 9-16 batch rows; fewer rows take
+     * one tile (measured best at every 8B shape), gate/up pairs two. */
     const aotx_rgemv_tune &tune = aotx_rgemv_tuning();
-    unsigned int rt;
-    if (mt > 8u) rt = 4u;
-    else if (tiles >= 4u * 1024u) rt = 4u;
-    else if (tiles >= 2u * 1024u) rt = 2u;
-    else rt = 1u;
+    unsigned int rt = mt > 8u ? 4u : 1u;
     if (tune.rt != 0u) rt = tune.rt;
     if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
     a->rt = rt;

@@ -21,6 +21,15 @@ aotx_state *aotx_state_device(void)
     return aotx_state_ptr;
 }
 
+/* A small pinned host buffer for the few words the host reads back each step (the queue
+ * marks of the page pool, a pass's offsets): copies into it skip the pageable staging. */
+void *aotx_pinned(void)
+{
+    static void *p = nullptr;
+    if (p == nullptr) AOTX_CHECK(hipHostMalloc(&p, 4096, hipHostMallocDefault));
+    return p;
+}
+
 /* Grow-only scratch. A larger request waits for the device, frees the old buffer and
  * allocates a zeroed new one. Counters stay zero because every kernel that counts
  * arrivals resets its counter before it exits. Growth inside a stream capture is an
