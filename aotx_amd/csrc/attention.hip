@@ -47,7 +47,7 @@ struct aotx_attn_args {
 
 #define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
 #define ATTN_MAX_SPLITS 32u
-#define ATTN_TARGET_GROUPS 512u
+#define ATTN_TARGET_GROUPS 256u
 
 static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
 {
@@ -124,15 +124,15 @@ struct aotx_attn_geom {
     static constexpr int U = 16 / NG;          /* instructions per 16-position block */
 };
 
-/* One workgroup = 4 waves = one (token, KV head, context chunk). */
-template <int D, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 : (G <= 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
+/* One workgroup = W waves = one (token, KV head, context chunk). */
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 : (G <= 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
 {
     constexpr int LPP = aotx_attn_geom<D>::LPP;
     constexpr int NG = aotx_attn_geom<D>::NG;
     constexpr int U = aotx_attn_geom<D>::U;
-    __shared__ float wm[4][G], wl[4][G];
-    __shared__ float wo[4][G][D];
+    __shared__ float wm[W][G], wl[W][G];
+    __shared__ float wo[W][G][D];
 
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 
     const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
     /* this wave's quarter, in whole 16-position blocks */
     const unsigned int nblk = (p1 - p0 + 15u) / 16u;
-    const unsigned int per = (nblk + 3u) / 4u;
+    const unsigned int per = (nblk + W - 1u) / W;
     const unsigned int b0 = p0 / 16u + wave * per;
     unsigned int b1 = b0 + per;
     if (b1 > (p1 + 15u) / 16u) b1 = (p1 + 15u) / 16u;
@@ -310,12 +310,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 
     const unsigned int unit = t * a.kv_heads + kh;
     const unsigned int stride = G * (D + 2);
     float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
-    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += 256u) {
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += 64u * W) {
         unsigned int j = idx / D, e = idx - j * D;
-        float top = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+        float top = wm[0][j];
+#pragma unroll
+        for (int w = 1; w < W; ++w) top = fmaxf(top, wm[w][j]);
         float msum = 0.0f, osum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < W; ++w) {
             float f = (wm[w][j] == -INFINITY) ? 0.0f : exp2f(wm[w][j] - top);
             msum += wl[w][j] * f;
             osum += wo[w][j][e] * f;
@@ -440,9 +442,18 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
         : (float *)aotx_scratch(AOTX_SCRATCH_ATTN_PARTIAL,
                                 aotx_attn_scratch(tokens, kv_heads, a.splits, g, head_dim));
     dim3 grid(tokens * kv_heads * a.splits);
+    /* 8 waves per workgroup (4 for 8 query heads per KV head, whose registers allow no
+     * more); AOTX_ATTN_WAVES=4 selects 4 for measurement sweeps */
+    static const unsigned int waves = [] {
+        const char *e = getenv("AOTX_ATTN_WAVES");
+        return e != nullptr && strtoul(e, nullptr, 10) == 4u ? 4u : 8u;
+    }();
 #define AOTX_ATTN_GO(DD, GG)                                                               \
     do {                                                                                   \
-        hipLaunchKernelGGL((aotx_attend_kernel<DD, GG>), grid, dim3(256), 0, stream, a);   \
+        if (waves == 8u && GG <= 4)                                                        \
+            hipLaunchKernelGGL((aotx_attend_kernel<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
+        else                                                                               \
+            hipLaunchKernelGGL((aotx_attend_kernel<DD, GG, 4>), grid, dim3(256), 0, stream, a); \
         AOTX_LAUNCH_CHECK();                                                               \
         if (a.splits > 1u) {                                                               \
             hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads, GG),   \

@@ -725,20 +725,29 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
-    /* x chunk c: rows past mrows and k past a.k are zeros */
+    /* x chunk c: rows past mrows and k past a.k are zeros. A thread's pieces keep their
+     * batch row from chunk to chunk, so the source rows are looked up once, here, before
+     * any weight load (a lookup after them would wait for all of them). */
     rg_u4 xr[PPT];
+    unsigned int xsrcv[PPT];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+        const unsigned int idx = tid + (unsigned int)i * NT;
+        const unsigned int mm = idx / PIECES;
+        xsrcv[i] = 0xFFFFFFFFu;
+        if (idx < (unsigned int)(MT * PIECES) && mm < mrows)
+            xsrcv[i] = list != nullptr ? list[mm] / a.xrow_div
+                     : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+    }
 #define RGW_XLOAD(C)                                                                     \
     do {                                                                                 \
         _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
             unsigned int idx = tid + (unsigned int)i * NT;                               \
-            unsigned int mm = idx / PIECES, p = idx % PIECES;                            \
+            unsigned int p = idx % PIECES;                                               \
             unsigned int kk = (q0 + (C) * RGW_KC) * 128u + p * 8u;                       \
             xr[i] = (rg_u4){0u, 0u, 0u, 0u};                                             \
-            if (idx < (unsigned int)(MT * PIECES) && mm < mrows && kk < q1 * 128u && kk < a.k) { \
-                unsigned int src = list != nullptr ? list[mm] / a.xrow_div               \
-                                 : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);  \
-                xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)src * a.ldx + kk);    \
-            }                                                                            \
+            if (xsrcv[i] != 0xFFFFFFFFu && kk < q1 * 128u && kk < a.k)                   \
+                xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)xsrcv[i] * a.ldx + kk); \
         }                                                                                \
     } while (0)
 #define RGW_XSTORE(C)                                                                    \
@@ -752,8 +761,13 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
+    /* x chunk 0 and both weight buffers go out before the first wait; each buffer is
+     * refilled right after its quads are computed, two steps ahead (loads past the range
+     * repeat the last quad: cache hits). x chunk c + 1 is requested before the weights of
+     * chunk c's later steps, so storing it waits for nothing issued after it. */
     RGW_XLOAD(0u);
     RGW_LOAD(0, q0);
+    RGW_LOAD(1, q0 + PD);
     RGW_XSTORE(0u);
     rg_sync_lds();
     for (unsigned int c = 0; c < nch; ++c) {
@@ -762,10 +776,10 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
 #pragma unroll
         for (int h = 0; h < RGW_KC / (2 * PD); ++h) {
             unsigned int qa = q0 + c * RGW_KC + (unsigned int)(2 * PD * h);
-            RGW_LOAD(1, qa + PD);
             RGW_COMPUTE(0, qa, xb);
             RGW_LOAD(0, qa + 2 * PD);
             RGW_COMPUTE(1, qa + PD, xb);
+            RGW_LOAD(1, qa + 3 * PD);
         }
         if (c + 1u < nch) RGW_XSTORE(c + 1u);
         rg_sync_lds();
@@ -896,12 +910,15 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     if (mt > 16u) {
         /* wide batch: 8 waves x 1 tile per workgroup, x through LDS in chunks; split k
          * while there are fewer than 256 workgroups and every split keeps a whole chunk */
+        const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
         a->wide = 1u;
-        a->rt = 8u;
-        if (epi == AOTX_EPI_SWIGLU) a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + 3u) / 4u;
-        else a->groups = (tiles + 7u) / 8u;
+        a->rt = tw.rt == 4u ? 4u : 8u;                 /* waves (one tile each) per workgroup */
+        if (epi == AOTX_EPI_SWIGLU)
+            a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + a->rt / 2u - 1u) / (a->rt / 2u);
+        else a->groups = (tiles + a->rt - 1u) / a->rt;
+        const unsigned int wtarget = tw.target != 0u ? tw.target : 256u;
         unsigned int s = 1u;
-        while (a->groups * s < 256u && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
+        while (a->groups * s < wtarget && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
@@ -969,8 +986,12 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
         size_t xb = 2u * 32u * RGW_XS * 2u;
         size_t ob = (size_t)a.rt * 16u * 32u * 4u;
-        hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), dim3(a.groups * a.splits, ey), dim3(512),
-                           xb > ob ? xb : ob, s, a);
+        if (a.rt == 4u)
+            hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 4, 2>), dim3(a.groups * a.splits, ey), dim3(256),
+                               xb > ob ? xb : ob, s, a);
+        else
+            hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), dim3(a.groups * a.splits, ey), dim3(512),
+                               xb > ob ? xb : ob, s, a);
         AOTX_LAUNCH_CHECK();
         if (a.splits > 1u) {
             hipLaunchKernelGGL((aotx_rgemv_reduce<32>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),

@@ -60,14 +60,28 @@ def gemv_table(torch, L, shapes, ms, iters=20):
     for n, k in shapes:
         w = torch.empty(n * (k // 32) * 34, dtype=torch.uint8, device="cuda")
         A.check(L.aotx_synth_q8(A.ptr(w), n, k, 0.02, 7, None), "synth")
-        wr = torch.empty(L.aotx_q8r_size(n, k), dtype=torch.uint8, device="cuda")
-        A.check(L.aotx_q8_repack(A.ptr(w), n, k, A.ptr(wr), None), "repack")
+        # enough copies that consecutive launches stream from HBM, not from the 256 MB
+        # last-level cache (each copy read once per pass through them)
+        rsize = L.aotx_q8r_size(n, k)
+        copies = max(1, min(iters, (640 << 20) // rsize + 1))
+        wrs = []
+        for _ in range(copies):
+            wr = torch.empty(rsize, dtype=torch.uint8, device="cuda")
+            A.check(L.aotx_q8_repack(A.ptr(w), n, k, A.ptr(wr), None), "repack")
+            wrs.append(wr)
+        fsize = w.numel()
+        fcopies = max(1, min(iters, (640 << 20) // fsize + 1))
+        ws = [w] + [w.clone() for _ in range(fcopies - 1)]
         for m in ms:
             x = torch.randn(m, k, device="cuda").half()
             y = torch.empty(m, n, device="cuda", dtype=torch.float16)
             row = {"n": n, "k": k, "m": m}
-            for name, fn, wt in (("file", L.aotx_q8_gemv_f16, w), ("repacked", L.aotx_q8r_gemv_f16, wr)):
-                def launch(st, fn=fn, wt=wt):
+            for name, fn, tens in (("file", L.aotx_q8_gemv_f16, ws), ("repacked", L.aotx_q8r_gemv_f16, wrs)):
+                turn = [0]
+
+                def launch(st, fn=fn, tens=tens):
+                    wt = tens[turn[0] % len(tens)]
+                    turn[0] += 1
                     A.check(fn(A.ptr(wt), n, k, A.ptr(x), m, A.ptr(y),
                                ctypes.c_void_p(st.cuda_stream)), "q8 product")
                 us = graph_time(torch, launch, reps=iters)
@@ -76,7 +90,7 @@ def gemv_table(torch, L, shapes, ms, iters=20):
                 row[name + "_gbs"] = round(algo / us / 1e3, 1)
                 row["bytes"] = algo
             out.append(row)
-        del w, wr
+        del w, ws, wrs
     return out
 
 
@@ -105,8 +119,8 @@ def graph_time(torch, launch, reps=20, replays=5):
 
 
 def attention_rate(torch, L, slots, context, heads, kvh, hd, layers):
-    """The step's attention over the seated pages (layer 0, every slot at its last seated
-    position): (us per launch, algorithmic bytes per launch)."""
+    """The step's attention over the seated pages (every slot at its last seated position,
+    the layers in turn): (us per launch, algorithmic bytes per launch)."""
     import aotx_amd as A
     B = len(slots)
     q = torch.randn(B, heads, hd, device="cuda").half()
@@ -114,8 +128,14 @@ def attention_rate(torch, L, slots, context, heads, kvh, hd, layers):
     pos = torch.full((B,), context - 1, dtype=torch.int32, device="cuda")
     ag = torch.tensor(slots, dtype=torch.int32, device="cuda")
 
+    turn = [0]
+
     def launch(s):
-        A.check(L.aotx_attend_paged(A.ptr(q), A.ptr(pos), A.ptr(ag), B, heads, kvh, hd, 0,
+        # a different layer each launch: 32 x 268 MB of keys and values, so no launch finds
+        # the previous one's in the 256 MB last-level cache
+        layer = turn[0] % layers
+        turn[0] += 1
+        A.check(L.aotx_attend_paged(A.ptr(q), A.ptr(pos), A.ptr(ag), B, heads, kvh, hd, layer,
                                     layers, A.ptr(out), ctypes.c_void_p(s.cuda_stream)),
                 "aotx_attend_paged")
 
