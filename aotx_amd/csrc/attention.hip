@@ -5,20 +5,19 @@
  * 1/sqrt(d), fp32 sums, out = half(sum / mass); keys and values come from the 16-position
  * layout blocks of cuda/model/kv_layout.cuh. Each query head re-reads its KV head there.
  *
- * Here one workgroup of 4 waves takes (token, KV head, context chunk):
+ * Here one workgroup of 8 waves takes (token, KV head, context chunk):
  *   - all G = heads / kv_heads query heads of the KV head share one read of its keys and
  *     values (grouped-query sharing: the KV bytes are read once per token, not G times);
- *   - d/8 lanes hold one position, one 16-byte piece of the row each, so a wave step
- *     covers one whole 16-position layout block (4 KB of keys and 4 KB of values at
- *     d = 128) with fully used 16-byte loads, and the next block's loads are issued before
- *     the current block is computed;
- *   - scores are fp16 x fp16 products summed in fp32 (v_dot2_f32_f16), reduced over the
- *     row's lanes with lane shuffles; online softmax per block in base 2 (scores carry
- *     log2(e) / sqrt(d)), values accumulated in fp32;
- *   - the 4 waves' (max, mass, sum) are merged in wave order through LDS; the context is
- *     split over workgroups (flash-decoding) so that a batch of one still covers the GPU,
- *     and a merge kernel adds the chunks of a (token, KV head) in chunk order, so the
- *     result does not depend on timing.
+ *   - a wave step is one whole 16-position layout block (4 KB of keys and 4 KB of values
+ *     at d = 128), loaded with 16-byte buffer loads from the block's scalar base address,
+ *     the next block's loads issued before the current block is computed;
+ *   - scores and the probability-weighted sum of values run on the matrix cores
+ *     (v_mfma_f32_16x16x32_f16 for K . q^T, v_mfma_f32_16x16x16_f16 for P . V), online
+ *     softmax per block in base 2 (scores carry log2(e) / sqrt(d)), fp32 accumulation;
+ *   - the waves' (max, mass, sum) are merged in wave order through LDS. At small batches
+ *     the context is split over workgroups (flash-decoding) so that the launch still
+ *     covers the GPU, and a merge kernel adds the chunks of a (token, KV head) in chunk
+ *     order, so the result does not depend on timing.
  */
 #include "aotx_internal.h"
 
@@ -26,7 +25,9 @@
 #include <stdlib.h>
 
 typedef unsigned int aotx_u4a __attribute__((ext_vector_type(4)));
-typedef _Float16 aotx_h2a __attribute__((ext_vector_type(2)));
+typedef _Float16 aotx_h4a __attribute__((ext_vector_type(4)));
+typedef _Float16 aotx_h8a __attribute__((ext_vector_type(8)));
+typedef float aotx_f4a __attribute__((ext_vector_type(4)));
 
 struct aotx_attn_args {
     const unsigned short *q;      /* fp16 [tokens][heads][d] */
@@ -49,22 +50,10 @@ struct aotx_attn_args {
 #define ATTN_MAX_SPLITS 32u
 #define ATTN_TARGET_GROUPS 256u
 
-static __device__ __forceinline__ float aotx_attn_h(unsigned int word, int hi)
-{
-    return aotx_h2f((unsigned short)(hi ? (word >> 16) : (word & 0xFFFFu)));
-}
-
 /* A kernel-constant word (the device token count) read through the scalar cache. */
 static __device__ __forceinline__ unsigned int aotx_attn_scalar(const unsigned int *p)
 {
     return *(const __attribute__((address_space(4))) unsigned int *)p;
-}
-
-/* fp16 pair from one 32-bit word. The word arrives by value: a __builtin_bit_cast of a
- * vector element (v[e]) directly is miscompiled by this hipcc (it reads element 0). */
-static __device__ __forceinline__ aotx_h2a aotx_as_h2(unsigned int word)
-{
-    return __builtin_bit_cast(aotx_h2a, word);
 }
 
 /* 2^x with the hardware v_exp_f32: exp2(-inf) = 0, results below 2^-126 flush to 0 (weights
@@ -74,42 +63,6 @@ static __device__ __forceinline__ float aotx_exp2(float x)
     return __builtin_amdgcn_exp2f(x);
 }
 
-template <int CTRL>
-static __device__ __forceinline__ float aotx_dpp(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                                 CTRL, 0xF, 0xF, false));
-}
-
-/* Sum over aligned groups of LPP (8 or 16) lanes, every lane of a group left with the
- * same total: quad swaps, then the mirrors within 8 and within 16. */
-template <int LPP>
-static __device__ __forceinline__ float aotx_row_sum(float v)
-{
-    v += aotx_dpp<0xB1>(v);     /* quad_perm [1,0,3,2] */
-    v += aotx_dpp<0x4E>(v);     /* quad_perm [2,3,0,1] */
-    v += aotx_dpp<0x141>(v);    /* row_half_mirror */
-    if (LPP == 16) v += aotx_dpp<0x140>(v);    /* row_mirror */
-    return v;
-}
-
-/* Max and sum over the lane groups of LPP lanes (every lane ends with the result). */
-template <int LPP>
-static __device__ __forceinline__ float aotx_groups_max(float v)
-{
-#pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-template <int LPP>
-static __device__ __forceinline__ float aotx_groups_sum(float v)
-{
-#pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 /* Chunk length of a token with n positions under S splits (whole 64-position units). */
 static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, unsigned int S)
 {
@@ -117,27 +70,33 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
     return (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
 }
 
-template <int D>
-struct aotx_attn_geom {
-    static constexpr int LPP = D / 8;          /* lanes per position */
-    static constexpr int NG = 64 / LPP;        /* positions per wave instruction */
-    static constexpr int U = 16 / NG;          /* instructions per 16-position block */
-};
-
-/* One workgroup = W waves = one (token, KV head, context chunk). */
+/* One workgroup = W waves = one (token, KV head, context chunk); each wave takes a
+ * contiguous run of 16-position layout blocks. Per wave and block, on the matrix cores:
+ *   - scores S[pos][head] = K . q^T: one v_mfma_f32_16x16x32_f16 per 32 of d, keys as the A
+ *     operand straight from memory (lane (r, g) holds row r, d 32kk + 8g..+7), the query
+ *     heads of the KV head as the B columns (heads past G are zero);
+ *   - the score layout (lane (r, g): head r, positions 4g..4g+3) is the A-operand layout of
+ *     v_mfma_f32_16x16x16_f16, so the probabilities feed P . V as fp16 (the mass adds the
+ *     same rounded probabilities, so numerator and denominator agree);
+ *   - the values need positions along k: the wave writes its block (row-major, rows padded
+ *     against bank conflicts) to a private LDS slot and reads 16-bit columns back;
+ *   - online softmax in base 2 per head with a max over the 4 lane groups of the head.
+ * The output accumulators hold heads 4g..4g+3 x 16 d columns per lane and PV step. */
 template <int D, int G, int W>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G == 1 ? 3 : (G <= 4 ? 2 : 1)))) void aotx_attend_kernel(aotx_attn_args a)
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_mma(aotx_attn_args a)
 {
-    constexpr int LPP = aotx_attn_geom<D>::LPP;
-    constexpr int NG = aotx_attn_geom<D>::NG;
-    constexpr int U = aotx_attn_geom<D>::U;
+    static_assert(G <= 16, "one MFMA tile of query heads");
+    constexpr int KK = D / 32;          /* score MFMA steps */
+    constexpr int VP = D / 32;          /* 16-byte value pieces per lane per block */
+    constexpr int NS = D / 16;          /* P.V MFMAs (16 d columns each) */
+    constexpr int VS = D + 8;           /* LDS row stride of a value block (halves) */
     __shared__ float wm[W][G], wl[W][G];
     __shared__ float wo[W][G][D];
+    __shared__ __attribute__((aligned(16))) unsigned short vl[W][16 * VS];
 
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
-    const unsigned int grp = lane / LPP;
-    const unsigned int sub = lane % LPP;
+    const unsigned int r = lane & 15u, g = lane >> 4;
     unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
     const unsigned int S = a.splits;
@@ -148,11 +107,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G == 1 ?
     if (t >= tokens) return;
     const unsigned int n = a.pos[t] + 1u;
     const unsigned int chunk = aotx_attn_chunk(n, S);
-    const unsigned int st = (n + chunk - 1u) / chunk;   /* chunks of this token */
+    const unsigned int st = (n + chunk - 1u) / chunk;
     if (c >= st) return;
     const unsigned int p0 = c * chunk;
     const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
-    /* this wave's quarter, in whole 16-position blocks */
     const unsigned int nblk = (p1 - p0 + 15u) / 16u;
     const unsigned int per = (nblk + W - 1u) / W;
     const unsigned int b0 = p0 / 16u + wave * per;
@@ -160,153 +118,139 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G == 1 ?
     if (b1 > (p1 + 15u) / 16u) b1 = (p1 + 15u) / 16u;
     const unsigned int agent = a.agent[t];
     const aotx_kv_table *kv = &a.state->kv;
-    /* base-2 scores: s * log2(e) / sqrt(d) */
     const float scale = 1.4426950408889634f / sqrtf((float)D);
 
-    aotx_h2a qv[G][4];
+    aotx_h8a qb[KK];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        const unsigned short *qrow = a.q + ((unsigned long long)t * a.heads + kh * G + j) * D;
-        aotx_u4a w = *(const aotx_u4a *)(qrow + 8 * sub);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qv[j][e] = aotx_as_h2(w[e]);
+    for (int kk = 0; kk < KK; ++kk) {
+        aotx_u4a w = {0u, 0u, 0u, 0u};
+        if (r < (unsigned int)G)
+            w = *(const aotx_u4a *)(a.q + ((unsigned long long)t * a.heads + kh * G + r) * D
+                                    + 32 * kk + 8 * g);
+        qb[kk] = __builtin_bit_cast(aotx_h8a, w);
     }
-    float o[G][8];
-    float mrun[G], lrun[G];
+    float mrun = -INFINITY, lrun = 0.0f;     /* head r of this lane */
+    aotx_f4a o[NS];
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        mrun[j] = -INFINITY;
-        lrun[j] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[j][e] = 0.0f;
-    }
+    for (int cc = 0; cc < NS; ++cc) o[cc] = (aotx_f4a){0.0f, 0.0f, 0.0f, 0.0f};
     int missing = 0;
-    /* byte offsets of this lane's piece of row grp of the key and value heads */
-    const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
-    const unsigned int vbyte = (((a.kv_heads + kh) * AOTX_KVL_BLOCK + grp) * D + 8u * sub) * 2u;
+    const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + r) * D + 8u * g) * 2u;
+    const unsigned int vbyte = ((a.kv_heads + kh) * AOTX_KVL_BLOCK * D + lane * 8u) * 2u;
+    unsigned short *vw = vl[wave];
 
-    aotx_u4a kr[3][U], vr[3][U];     /* a ring of three blocks: two in flight */
-    bool absent[3];
-    /* layout-block pointers of the wave's blocks, 64 at a time, lane i holding block
-     * wbase + i; a block is fetched from the lane that holds it */
+    aotx_u4a kr[2][KK], vr[2][VP];
+    bool absent[2];
     unsigned long long pages = 0ull;
     unsigned int wbase = b0;
-#define ATTN_WINDOW(B0)                                                                     \
+#define MMA_WINDOW(B0)                                                                      \
     do {                                                                                    \
         wbase = (B0);                                                                       \
         unsigned int bl = wbase + lane;                                                     \
         pages = bl < b1 ? (unsigned long long)aotx_kvl_block(a.shape, kv, agent, a.layer, bl * 16u) \
                         : 0ull;                                                             \
     } while (0)
-#define ATTN_LOAD(BUF, B)                                                                   \
+#define MMA_LOAD(BUF, B)                                                                    \
     do {                                                                                    \
-        if ((B) - wbase >= 64u) ATTN_WINDOW(B);                                             \
+        if ((B) - wbase >= 64u) MMA_WINDOW(B);                                              \
         unsigned long long pb = __shfl(pages, (int)((B) - wbase), 64);                     \
-        /* the block is the same for the whole wave: its address goes to scalar registers, \
-         * as a buffer resource whose range is empty for a missing page (loads give 0) */   \
         pb = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb >> 32)) << 32) \
            | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb); \
         absent[BUF] = pb == 0ull;                                                           \
         __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
             (void *)pb, (short)0, absent[BUF] ? 0 : (int)a.shape.block_bytes, 0x00020000);  \
-        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
-            kr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + u * NG * D * 2, 0, 0); \
-            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * NG * D * 2, 0, 0); \
-        }                                                                                   \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            kr[BUF][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + kk * 64, 0, 0); \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u)                                      \
+            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * 1024, 0, 0); \
     } while (0)
 
-#define ATTN_COMPUTE(BUF, B)                                                                \
+#define MMA_COMPUTE(BUF, B)                                                                 \
     do {                                                                                    \
         if (absent[BUF]) missing = 1;                                                       \
-        float sc[U][G];                                                                     \
-        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
-            unsigned int p = (B) * 16u + (unsigned int)u * NG + grp;                        \
-            bool ok = p >= p0 && p < p1 && !absent[BUF];                                    \
-            aotx_u4a kk = kr[BUF][u];                                                       \
-            _Pragma("unroll") for (int j = 0; j < G; ++j) {                                 \
-                float v = 0.0f;                                                             \
-                _Pragma("unroll") for (int e = 0; e < 4; ++e)                               \
-                    v = __builtin_amdgcn_fdot2(qv[j][e], aotx_as_h2(kk[e]), v, false);       \
-                v = aotx_row_sum<LPP>(v);                                                   \
-                sc[u][j] = ok ? v * scale : -INFINITY;                                      \
-            }                                                                               \
+        aotx_f4a sc = {0.0f, 0.0f, 0.0f, 0.0f};                                             \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                    \
+                __builtin_bit_cast(aotx_h8a, kr[BUF][kk]), qb[kk], sc, 0, 0, 0);             \
+        /* the block's values into this wave's LDS slot (row-major, padded rows) */         \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u) {                                    \
+            const unsigned int piece = (unsigned int)u * 64u + lane;                        \
+            *(aotx_u4a *)(vw + (piece / (D / 8)) * VS + (piece % (D / 8)) * 8u) = vr[BUF][u]; \
         }                                                                                   \
-        _Pragma("unroll") for (int j = 0; j < G; ++j) {                                     \
-            float mb = sc[0][j];                                                            \
-            _Pragma("unroll") for (int u = 1; u < U; ++u) mb = fmaxf(mb, sc[u][j]);         \
-            mb = aotx_groups_max<LPP>(mb);                                                  \
-            float mnew = fmaxf(mrun[j], mb);                                                \
-            if (mnew != mrun[j]) {                                                          \
-                float shift = aotx_exp2(mrun[j] - mnew);    /* 0 from -inf */               \
-                lrun[j] *= shift;                                                           \
-                _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] *= shift;             \
-                mrun[j] = mnew;                                                             \
-            }                                                                               \
+        float pr[4];                                                                        \
+        float mb = -INFINITY;                                                               \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
+            const bool ok = p >= p0 && p < p1 && !absent[BUF];                              \
+            pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
+            mb = fmaxf(mb, pr[i]);                                                          \
         }                                                                                   \
-        _Pragma("unroll") for (int u = 0; u < U; ++u) {                                     \
-            aotx_u4a vv = vr[BUF][u];                                                       \
-            float vf[8];                                                                    \
-            _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                 \
-                vf[2 * e] = aotx_attn_h(vv[e], 0);                                          \
-                vf[2 * e + 1] = aotx_attn_h(vv[e], 1);                                      \
-            }                                                                               \
-            _Pragma("unroll") for (int j = 0; j < G; ++j) {                                 \
-                float pw = aotx_exp2(sc[u][j] - mrun[j]);   /* 0 for a masked position */   \
-                lrun[j] += pw;                                                              \
-                _Pragma("unroll") for (int e = 0; e < 8; ++e) o[j][e] += pw * vf[e];        \
-            }                                                                               \
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
+        const float mnew = fmaxf(mrun, mb);                                                 \
+        const float shift = aotx_exp2(mrun - mnew);        /* 0 from -inf */                \
+        mrun = mnew;                                                                        \
+        aotx_h4a pa;                                                                        \
+        float mass = 0.0f;                                                                  \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const _Float16 ph = (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
+            pa[i] = ph;                                                                     \
+            mass += (float)ph;                                                              \
+        }                                                                                   \
+        lrun = lrun * shift + mass;                                                         \
+        /* the accumulators of heads 4g + i take those heads' shifts */                     \
+        if (__any(shift != 1.0f)) {                                                         \
+            float sh[4];                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) sh[i] = __shfl(shift, (int)(4u * g) + i, 64); \
+            _Pragma("unroll") for (int cc = 0; cc < NS; ++cc)                               \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
+        }                                                                                   \
+        _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
+            const unsigned short *col = vw + (4u * g) * VS + 16u * (unsigned int)cc + r;    \
+            aotx_h4a vb;                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                   \
+                vb[i] = __builtin_bit_cast(_Float16, col[(unsigned int)i * VS]);            \
+            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[cc], 0, 0, 0);          \
         }                                                                                   \
     } while (0)
 
     if (b0 < b1) {
         unsigned int b = b0;
-        ATTN_WINDOW(b0);
-        ATTN_LOAD(0, b);
-        if (b + 1u < b1) ATTN_LOAD(1, b + 1u);
+        MMA_WINDOW(b0);
+        MMA_LOAD(0, b);
         for (;;) {
-            if (b + 2u < b1) ATTN_LOAD(2, b + 2u);
-            ATTN_COMPUTE(0, b);
+            if (b + 1u < b1) MMA_LOAD(1, b + 1u);
+            MMA_COMPUTE(0, b);
             b += 1u;
             if (b >= b1) break;
-            if (b + 2u < b1) ATTN_LOAD(0, b + 2u);
-            ATTN_COMPUTE(1, b);
-            b += 1u;
-            if (b >= b1) break;
-            if (b + 2u < b1) ATTN_LOAD(1, b + 2u);
-            ATTN_COMPUTE(2, b);
+            if (b + 1u < b1) MMA_LOAD(0, b + 1u);
+            MMA_COMPUTE(1, b);
             b += 1u;
             if (b >= b1) break;
         }
     }
-#undef ATTN_WINDOW
-#undef ATTN_LOAD
-#undef ATTN_COMPUTE
+#undef MMA_WINDOW
+#undef MMA_LOAD
+#undef MMA_COMPUTE
 
-    /* the lane groups' sums of one wave (mass counted once per group: lanes of a group
-     * hold the same weights) */
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-        lrun[j] = aotx_groups_sum<LPP>(lrun[j]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[j][e] = aotx_groups_sum<LPP>(o[j][e]);
-    }
+    /* a head's mass over its 4 lane groups */
+    lrun += __shfl_xor(lrun, 16, 64);
+    lrun += __shfl_xor(lrun, 32, 64);
     missing = __any(missing);
     if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
-    if (lane == 0u) {
+    if (g == 0u && r < (unsigned int)G) {
+        wm[wave][r] = missing ? -INFINITY : mrun;
+        wl[wave][r] = missing ? 0.0f : lrun;
+    }
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            wm[wave][j] = missing ? -INFINITY : mrun[j];
-            wl[wave][j] = missing ? 0.0f : lrun[j];
+    for (int i = 0; i < 4; ++i) {
+        const unsigned int head = 4u * g + (unsigned int)i;
+        if (head < (unsigned int)G) {
+#pragma unroll
+            for (int cc = 0; cc < NS; ++cc) wo[wave][head][16 * cc + r] = missing ? 0.0f : o[cc][i];
         }
     }
-    if (grp == 0u) {
-#pragma unroll
-        for (int j = 0; j < G; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) wo[wave][j][8 * sub + e] = missing ? 0.0f : o[j][e];
-    }
     __syncthreads();
-    /* merge the 4 waves in wave order; the chunk's triple keeps the base-2 maximum */
+    /* merge the W waves in wave order */
     const unsigned int unit = t * a.kv_heads + kh;
     const unsigned int stride = G * (D + 2);
     float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
@@ -442,18 +386,9 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
         : (float *)aotx_scratch(AOTX_SCRATCH_ATTN_PARTIAL,
                                 aotx_attn_scratch(tokens, kv_heads, a.splits, g, head_dim));
     dim3 grid(tokens * kv_heads * a.splits);
-    /* 8 waves per workgroup (4 for 8 query heads per KV head, whose registers allow no
-     * more); AOTX_ATTN_WAVES=4 selects 4 for measurement sweeps */
-    static const unsigned int waves = [] {
-        const char *e = getenv("AOTX_ATTN_WAVES");
-        return e != nullptr && strtoul(e, nullptr, 10) == 4u ? 4u : 8u;
-    }();
 #define AOTX_ATTN_GO(DD, GG)                                                               \
     do {                                                                                   \
-        if (waves == 8u && GG <= 4)                                                        \
-            hipLaunchKernelGGL((aotx_attend_kernel<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
-        else                                                                               \
-            hipLaunchKernelGGL((aotx_attend_kernel<DD, GG, 4>), grid, dim3(256), 0, stream, a); \
+        hipLaunchKernelGGL((aotx_attend_mma<DD, GG, 8>), grid, dim3(512), 0, stream, a);   \
         AOTX_LAUNCH_CHECK();                                                               \
         if (a.splits > 1u) {                                                               \
             hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads, GG),   \
