@@ -397,14 +397,6 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
-#ifdef AOTX_EXPERIMENT_NOCOMPUTE
-#define RG_COMPUTE(BUF, QS)                                                              \
-    do {                                                                                 \
-        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi)                                \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j)                               \
-                acc[j][0][0] += __builtin_bit_cast(float, (wa[BUF][qi][j][0].x ^ wa[BUF][qi][j][0].y ^ wa[BUF][qi][j][0].z ^ wa[BUF][qi][j][0].w ^ wa[BUF][qi][j][1].x ^ wa[BUF][qi][j][1].y ^ wa[BUF][qi][j][1].z ^ wa[BUF][qi][j][1].w ^ ws[BUF][qi][j]) & 0x3f800000u); \
-    } while (0)
-#else
     /* Branch-free: a quad past the wave's range reads the last quad's x and has its scale
      * forced to zero (it adds nothing); a batch column past mrows reads row 0 of x (its
      * results are never written). */
@@ -440,7 +432,6 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
             }                                                                            \
         }                                                                                \
     } while (0)
-#endif
 
     /* ---- loads that do not depend on the weights go out first. With direct rows (batch
      * row i is row m0 + i: no expert list, no row map) that is the first RG_PRE staging
@@ -693,33 +684,34 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
         }                                                                                \
     } while (0)
 
+    /* branch-free: a quad past the range reads its chunk's last x quad and has its scale
+     * forced to zero */
 #define RGW_COMPUTE(BUF, QS, XB)                                                         \
     do {                                                                                 \
         _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            unsigned int qq = (QS) + (unsigned int)qi;                                   \
-            if (qq < q1) {                                                               \
-                const unsigned short *xq = (XB) + ((qq - q0) % RGW_KC) * 128u + 32u * g; \
-                rg_h8 B[MT / 16][4];                                                     \
-                _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                    \
-                    _Pragma("unroll") for (int s = 0; s < 4; ++s)                        \
-                        B[t][s] = *(const rg_h8 *)(xq + ((unsigned int)t * 16u + r) * RGW_XS + 8u * s); \
-                }                                                                        \
-                _Pragma("unroll") for (int j = 0; j < RT; ++j) {                         \
-                    unsigned int sbits = ws[BUF][qi][j];                                 \
-                    rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));         \
-                    const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];        \
-                    unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                \
-                                          q1v[0], q1v[1], q1v[2], q1v[3]};               \
-                    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                      \
-                        unsigned int d0, d1, d2, d3;                                     \
-                        rg_dequant4(qd[2 * s], s2, d0, d1);                              \
-                        rg_dequant4(qd[2 * s + 1], s2, d2, d3);                          \
-                        rg_u4 av = {d0, d1, d2, d3};                                     \
-                        rg_h8 A = __builtin_bit_cast(rg_h8, av);                         \
-                        _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)              \
-                            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(           \
-                                A, B[t][s], acc[j][t], 0, 0, 0);                         \
-                    }                                                                    \
+            const unsigned int qq = (QS) + (unsigned int)qi;                             \
+            const unsigned int qx = qq < q1 ? qq : q1 - 1u;                              \
+            const unsigned short *xq = (XB) + ((qx - q0) % RGW_KC) * 128u + 32u * g;     \
+            rg_h8 B[MT / 16][4];                                                         \
+            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
+                    B[t][s] = *(const rg_h8 *)(xq + ((unsigned int)t * 16u + r) * RGW_XS + 8u * s); \
+            }                                                                            \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const unsigned int sbits = qq < q1 ? ws[BUF][qi][j] : 0u;                \
+                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
+                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
+                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
+                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
+                    unsigned int d0, d1, d2, d3;                                         \
+                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
+                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
+                    rg_u4 av = {d0, d1, d2, d3};                                         \
+                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
+                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
+                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
+                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
                 }                                                                        \
             }                                                                            \
         }                                                                                \
@@ -874,7 +866,7 @@ static const aotx_rgemv_tune &aotx_rgemv_tuning()
         aotx_rgemv_tune v = {0u, 0u, 0u, 0u};
         const char *e = getenv("AOTX_RGEMV_TUNE");
         if (e != nullptr) sscanf(e, "%u,%u,%u,%u", &v.rt, &v.pd, &v.target, &v.minq);
-        if (v.rt != 0u && v.rt != 1u && v.rt != 2u && v.rt != 4u) v.rt = 0u;
+        if (v.rt != 0u && v.rt != 1u && v.rt != 2u && v.rt != 4u && v.rt != 8u) v.rt = 0u;
         return v;
     }();
     return t;
@@ -908,17 +900,20 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         tiles = (total + 15u) / 16u;
     }
     if (mt > 16u) {
-        /* wide batch: 8 waves x 1 tile per workgroup, x through LDS in chunks; split k
-         * while there are fewer than 256 workgroups and every split keeps a whole chunk */
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
+        /* 8 waves x 1 tile per workgroup, x through LDS in chunks. A product with at least
+         * 192 workgroups (the gate/up pair, the head) runs unsplit: no partials and no
+         * second launch. Fewer split k towards 256 workgroups while a split keeps a whole
+         * chunk; their partials are added by aotx_rgemv_reduce. */
         a->wide = 1u;
-        a->rt = tw.rt == 4u ? 4u : 8u;                 /* waves (one tile each) per workgroup */
+        a->rt = 8u;                                    /* waves (one tile each) per workgroup */
         if (epi == AOTX_EPI_SWIGLU)
             a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + a->rt / 2u - 1u) / (a->rt / 2u);
         else a->groups = (tiles + a->rt - 1u) / a->rt;
         const unsigned int wtarget = tw.target != 0u ? tw.target : 256u;
         unsigned int s = 1u;
-        while (a->groups * s < wtarget && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
+        if (a->groups < 192u)
+            while (a->groups * s < wtarget && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
@@ -979,19 +974,16 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
     }
     if (a.wide) {
+        unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
+        size_t xb = 2u * 32u * RGW_XS * 2u;
+        size_t ob = (size_t)a.rt * 16u * 32u * 4u;
+        const size_t lds = xb > ob ? xb : ob;
+        const dim3 grid(a.groups * a.splits, ey);
         if (a.xmode != AOTX_X_F16) {
             fprintf(stderr, "aotx: the wide-batch product takes fp16 x only\n");
             exit(1);
         }
-        unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
-        size_t xb = 2u * 32u * RGW_XS * 2u;
-        size_t ob = (size_t)a.rt * 16u * 32u * 4u;
-        if (a.rt == 4u)
-            hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 4, 2>), dim3(a.groups * a.splits, ey), dim3(256),
-                               xb > ob ? xb : ob, s, a);
-        else
-            hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), dim3(a.groups * a.splits, ey), dim3(512),
-                               xb > ob ? xb : ob, s, a);
+        hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), grid, dim3(512), lds, s, a);
         AOTX_LAUNCH_CHECK();
         if (a.splits > 1u) {
             hipLaunchKernelGGL((aotx_rgemv_reduce<32>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
