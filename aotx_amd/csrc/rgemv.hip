@@ -609,21 +609,26 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     rg_epilogue<MT, RG_THREADS>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
 }
 
-/* Wide batches (17..32 rows of x, fp16 x in memory): W waves split the workgroup's
- * W * RT tiles (tile j belongs to wave j / RT) and every wave runs the workgroup's whole k
- * range, so no wave's sum has to be added to another's. x passes through LDS in chunks of
- * RGW_KC quads, double-buffered: the next chunk is loaded into registers while the
- * current one feeds the MFMAs, and the weight stream runs `PD` quads ahead across chunk
- * boundaries. Two workgroups fit a CU, so one's staging overlaps the other's streaming. */
-#define RGW_KC 4
-#define RGW_XS (RGW_KC * 128 + 8)     /* LDS x row stride (halves) */
-
-template <int MT, int RT, int W, int PD>
-__global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
+/* Wide batches (17..32 rows of fp16 x): a workgroup owns T 16-row tiles; its W = T * P
+ * waves are T tile owners times P phases. x passes through LDS in chunks of KC quads,
+ * double-buffered (the next chunk is loaded into registers while the current one feeds
+ * the MFMAs); the P waves of a tile take its quads of each chunk in turn (phase p: chunk
+ * quads p, p + P, ...), so every wave streams its weights one quad ahead of the MFMAs
+ * and all waves read the same x chunk. At the end the P phase sums of a tile are added in
+ * phase order through LDS and the workgroup applies the epilogue, or with k split over
+ * workgroups writes its partial tiles for aotx_rgemv_reduce. More phases put more waves
+ * on the same tiles (more loads in flight per CU) at the price of more x staging. */
+template <int T, int P, int KC, int PDQ>
+__global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
 {
-    static_assert(RGW_KC % (2 * PD) == 0, "a chunk holds whole load pairs");
+    constexpr int MT = 32;
+    constexpr int W = T * P;
     constexpr int NT = 64 * W;
-    constexpr int PIECES = RGW_KC * 16;                      /* 16-byte pieces per row */
+    constexpr int NQ = KC / P;                               /* a wave's quads per chunk */
+    constexpr int NS = NQ / PDQ;                             /* its load steps per chunk */
+    static_assert(KC % P == 0 && NQ % PDQ == 0 && NS % 2 == 0, "whole load pairs per chunk");
+    constexpr int XS = KC * 128 + 8;                         /* LDS x row stride (halves) */
+    constexpr int PIECES = KC * 16;                          /* 16-byte pieces per row */
     constexpr int PPT = (MT * PIECES + NT - 1) / NT;          /* pieces per thread */
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const unsigned int tid = threadIdx.x;
@@ -644,75 +649,58 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
     if (mrows > (unsigned int)MT) mrows = MT;
     if (mrows == 0u) return;
 
-    const unsigned int rtw = (unsigned int)(RT * W);
     const unsigned int group = blockIdx.x / a.splits;
     const unsigned int split = blockIdx.x % a.splits;
     const unsigned int q0 = split * a.qps;
     const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
-    const unsigned int nch = (q1 - q0 + RGW_KC - 1u) / RGW_KC;
-    unsigned short *xl = (unsigned short *)lds;               /* [2][MT][RGW_XS] */
+    const unsigned int nch = (q1 - q0 + KC - 1u) / KC;
+    unsigned short *xl = (unsigned short *)lds;               /* [2][MT][XS] */
     const unsigned int r = lane & 15u, g = lane >> 4;
+    const unsigned int tj = wave / P, ph = wave % P;
 
-    const unsigned char *qb[RT];
-    const unsigned short *sb[RT];
-#pragma unroll
-    for (int j = 0; j < RT; ++j) {
-        unsigned int dummy = 0u;
-        unsigned int tj = wave * (unsigned int)RT + (unsigned int)j;
-        qb[j] = rg_tile(a, group, tj, rtw, expert, dummy) + lane * 16u;
-        sb[j] = rg_scales(a, group, tj, rtw, expert) + lane;
-    }
-    rg_f4 acc[RT][MT / 16];
-#pragma unroll
-    for (int j = 0; j < RT; ++j)
-#pragma unroll
-        for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
-    rg_u4 wa[2][PD][RT][2];
-    unsigned int ws[2][PD][RT];    /* one 32-bit register per scale: no packing waits */
+    unsigned int dummy = 0u;
+    const unsigned char *qb = rg_tile(a, group, tj, T, expert, dummy) + lane * 16u;
+    const unsigned short *sb = rg_scales(a, group, tj, T, expert) + lane;
+    rg_f4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    rg_u4 wa[2][PDQ][2];             /* two buffers of PDQ quads */
+    unsigned int ws[2][PDQ];         /* one 32-bit register per scale: no packing waits */
 
-#define RGW_LOAD(BUF, QS)                                                                \
+/* the wave's n-th quad: chunk n / NQ, its phase's (n % NQ)-th quad of that chunk */
+#define RGW_QUAD(N) (q0 + ((N) / NQ) * KC + ph + P * ((N) % NQ))
+#define RGW_LOAD(BUF, N)                                                                 \
     do {                                                                                 \
-        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            unsigned int qq = (QS) + (unsigned int)qi;                                   \
-            if (qq >= q1) qq = q1 - 1u;                                                  \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
-                const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
-                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
-                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
-                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
-            }                                                                            \
+        _Pragma("unroll") for (int qi = 0; qi < PDQ; ++qi) {                             \
+            unsigned int qq = RGW_QUAD((N) + (unsigned int)qi);                          \
+            if (qq >= q1) qq = q1 - 1u;         /* past the range: a cache hit, unused */ \
+            const rg_u4 *src = (const rg_u4 *)(qb + (unsigned long long)qq * 2048ull);   \
+            wa[BUF][qi][0] = __builtin_nontemporal_load(src);                            \
+            wa[BUF][qi][1] = __builtin_nontemporal_load(src + 64);                       \
+            ws[BUF][qi] = sb[(unsigned long long)qq * 64ull];                            \
         }                                                                                \
     } while (0)
-
-    /* branch-free: a quad past the range reads its chunk's last x quad and has its scale
-     * forced to zero */
-#define RGW_COMPUTE(BUF, QS, XB)                                                         \
+    /* branch-free: a quad past the range reads a valid x quad and has its scale zeroed */
+#define RGW_COMPUTE(BUF, N, XB)                                                          \
     do {                                                                                 \
-        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            const unsigned int qq = (QS) + (unsigned int)qi;                             \
+        _Pragma("unroll") for (int qi = 0; qi < PDQ; ++qi) {                             \
+            const unsigned int qq = RGW_QUAD((N) + (unsigned int)qi);                    \
             const unsigned int qx = qq < q1 ? qq : q1 - 1u;                              \
-            const unsigned short *xq = (XB) + ((qx - q0) % RGW_KC) * 128u + 32u * g;     \
-            rg_h8 B[MT / 16][4];                                                         \
-            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
+            const unsigned short *xq = (XB) + ((qx - q0) % KC) * 128u + 32u * g;         \
+            rg_h8 B[2][4];                                                               \
+            _Pragma("unroll") for (int t = 0; t < 2; ++t)                                \
                 _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
-                    B[t][s] = *(const rg_h8 *)(xq + ((unsigned int)t * 16u + r) * RGW_XS + 8u * s); \
-            }                                                                            \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
-                const unsigned int sbits = qq < q1 ? ws[BUF][qi][j] : 0u;                \
-                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
-                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
-                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
-                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
-                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
-                    unsigned int d0, d1, d2, d3;                                         \
-                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
-                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
-                    rg_u4 av = {d0, d1, d2, d3};                                         \
-                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
-                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
-                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
-                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
-                }                                                                        \
+                    B[t][s] = *(const rg_h8 *)(xq + ((unsigned int)t * 16u + r) * XS + 8u * s); \
+            const unsigned int sbits = qq < q1 ? ws[BUF][qi] : 0u;                       \
+            rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));                 \
+            const rg_u4 q0v = wa[BUF][qi][0], q1v = wa[BUF][qi][1];                      \
+            unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]}; \
+            _Pragma("unroll") for (int s = 0; s < 4; ++s) {                              \
+                unsigned int d0, d1, d2, d3;                                             \
+                rg_dequant4(qd[2 * s], s2, d0, d1);                                      \
+                rg_dequant4(qd[2 * s + 1], s2, d2, d3);                                  \
+                rg_u4 av = {d0, d1, d2, d3};                                             \
+                rg_h8 A = __builtin_bit_cast(rg_h8, av);                                 \
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[0][s], acc[0], 0, 0, 0); \
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[1][s], acc[1], 0, 0, 0); \
             }                                                                            \
         }                                                                                \
     } while (0)
@@ -736,7 +724,7 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
         _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
             unsigned int idx = tid + (unsigned int)i * NT;                               \
             unsigned int p = idx % PIECES;                                               \
-            unsigned int kk = (q0 + (C) * RGW_KC) * 128u + p * 8u;                       \
+            unsigned int kk = (q0 + (C) * KC) * 128u + p * 8u;                           \
             xr[i] = (rg_u4){0u, 0u, 0u, 0u};                                             \
             if (xsrcv[i] != 0xFFFFFFFFu && kk < q1 * 128u && kk < a.k)                   \
                 xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)xsrcv[i] * a.ldx + kk); \
@@ -744,63 +732,72 @@ __global__ __launch_bounds__(64 * W, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
     } while (0)
 #define RGW_XSTORE(C)                                                                    \
     do {                                                                                 \
-        unsigned short *xb = xl + ((C) & 1u) * (unsigned int)(MT * RGW_XS);              \
+        unsigned short *xb = xl + ((C) & 1u) * (unsigned int)(MT * XS);                  \
         _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
             unsigned int idx = tid + (unsigned int)i * NT;                               \
             unsigned int mm = idx / PIECES, p = idx % PIECES;                            \
             if (idx < (unsigned int)(MT * PIECES))                                       \
-                *(rg_u4 *)(xb + mm * RGW_XS + p * 8u) = xr[i];                           \
+                *(rg_u4 *)(xb + mm * XS + p * 8u) = xr[i];                               \
         }                                                                                \
     } while (0)
 
-    /* x chunk 0 and both weight buffers go out before the first wait; each buffer is
-     * refilled right after its quads are computed, two steps ahead (loads past the range
-     * repeat the last quad: cache hits). x chunk c + 1 is requested before the weights of
-     * chunk c's later steps, so storing it waits for nothing issued after it. */
+    /* x chunk 0 and the first two weight quads go out before the first wait; each buffer
+     * is refilled right after its quad is computed, two quads ahead. x chunk c + 1 is
+     * requested before chunk c's later weight loads, so storing it waits for nothing
+     * issued after it. */
     RGW_XLOAD(0u);
-    RGW_LOAD(0, q0);
-    RGW_LOAD(1, q0 + PD);
+    RGW_LOAD(0, 0u);
+    RGW_LOAD(1, (unsigned int)PDQ);
     RGW_XSTORE(0u);
     rg_sync_lds();
     for (unsigned int c = 0; c < nch; ++c) {
-        const unsigned short *xb = xl + (c & 1u) * (unsigned int)(MT * RGW_XS);
+        const unsigned short *xb = xl + (c & 1u) * (unsigned int)(MT * XS);
         if (c + 1u < nch) RGW_XLOAD(c + 1u);
 #pragma unroll
-        for (int h = 0; h < RGW_KC / (2 * PD); ++h) {
-            unsigned int qa = q0 + c * RGW_KC + (unsigned int)(2 * PD * h);
-            RGW_COMPUTE(0, qa, xb);
-            RGW_LOAD(0, qa + 2 * PD);
-            RGW_COMPUTE(1, qa + PD, xb);
-            RGW_LOAD(1, qa + 3 * PD);
+        for (int i = 0; i < NS; ++i) {
+            const unsigned int n = c * NQ + (unsigned int)(i * PDQ);
+            RGW_COMPUTE(i & 1, n, xb);
+            RGW_LOAD(i & 1, n + 2u * PDQ);
         }
         if (c + 1u < nch) RGW_XSTORE(c + 1u);
         rg_sync_lds();
     }
+#undef RGW_QUAD
 #undef RGW_LOAD
 #undef RGW_COMPUTE
 #undef RGW_XLOAD
 #undef RGW_XSTORE
 
-    /* every wave's tiles into LDS (the x buffers are free after the last barrier) */
-    float *out = (float *)lds;                         /* [rtw*16][MT] */
-    const unsigned int gr = rtw * 16u;
+    /* the waves' tiles into LDS ([W][16][MT], the x buffers are free after the last
+     * barrier), then each tile's P phases added in phase order into out [T*16][MT] */
+    float *part = (float *)lds;
+    const unsigned int gr = T * 16u;
 #pragma unroll
-    for (int j = 0; j < RT; ++j)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int t = 0; t < MT / 16; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                unsigned int row = (wave * (unsigned int)RT + (unsigned int)j) * 16u + 4u * g + (unsigned int)i;
-                out[row * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
-            }
+        for (int i = 0; i < 4; ++i)
+            part[(wave * 16u + 4u * g + (unsigned int)i) * MT + (unsigned int)t * 16u + r] = acc[t][i];
     __syncthreads();
+    float *out = part + W * 16 * MT;
+    if (P == 1) {
+        out = part;
+    } else {
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
+            const unsigned int j = idx / (16u * MT), rest = idx % (16u * MT);
+            float sum = part[(j * P) * 16u * MT + rest];
+#pragma unroll
+            for (int p = 1; p < P; ++p) sum += part[((j * P) + (unsigned int)p) * 16u * MT + rest];
+            out[idx] = sum;
+        }
+        __syncthreads();
+    }
     if (a.splits > 1u) {
         float *mine = a.partial
             + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
         for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
         return;
     }
-    rg_epilogue<MT, NT>(a, out, group, rtw, mrows, list);
+    rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
 }
 
 /* Add the split partials in split order, then the epilogue. One workgroup per 16-row tile
@@ -901,19 +898,24 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     }
     if (mt > 16u) {
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
-        /* 8 waves x 1 tile per workgroup, x through LDS in chunks. A product with at least
-         * 192 workgroups (the gate/up pair, the head) runs unsplit: no partials and no
-         * second launch. Fewer split k towards 256 workgroups while a split keeps a whole
-         * chunk; their partials are added by aotx_rgemv_reduce. */
+        /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
+         * tiles (gate/up, head), 2 x 4 for few (QKV, O, down), measured best at the 8B
+         * shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
+         * no second launch) unless they have fewer than 192 workgroups and a long k (down):
+         * those split k towards 256 workgroups while a split keeps a whole chunk, and
+         * aotx_rgemv_reduce adds the partials. */
         a->wide = 1u;
-        a->rt = 8u;                                    /* waves (one tile each) per workgroup */
+        a->rt = tiles >= 1536u ? 8u : 2u;
+        if (tw.rt == 8u || tw.rt == 4u || tw.rt == 2u) a->rt = tw.rt;
+        a->pd = 8u / a->rt;                            /* phases */
+        const unsigned int kc = a->pd == 4u ? 8u : 4u;
         if (epi == AOTX_EPI_SWIGLU)
             a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + a->rt / 2u - 1u) / (a->rt / 2u);
         else a->groups = (tiles + a->rt - 1u) / a->rt;
         const unsigned int wtarget = tw.target != 0u ? tw.target : 256u;
         unsigned int s = 1u;
-        if (a->groups < 192u)
-            while (a->groups * s < wtarget && a->qn / (s + 1u) >= (unsigned int)RGW_KC) s += 1u;
+        if (a->groups < 192u && a->qn > 32u)
+            while (a->groups * s < wtarget && a->qn / (s + 1u) >= kc) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
@@ -975,15 +977,21 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
     }
     if (a.wide) {
         unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
-        size_t xb = 2u * 32u * RGW_XS * 2u;
-        size_t ob = (size_t)a.rt * 16u * 32u * 4u;
-        const size_t lds = xb > ob ? xb : ob;
         const dim3 grid(a.groups * a.splits, ey);
         if (a.xmode != AOTX_X_F16) {
             fprintf(stderr, "aotx: the wide-batch product takes fp16 x only\n");
             exit(1);
         }
-        hipLaunchKernelGGL((aotx_rgemv_wide<32, 1, 8, 2>), grid, dim3(512), lds, s, a);
+        if (a.rt == 2u) {
+            const size_t xb = 2u * 32u * (8u * 128u + 8u) * 2u;
+            hipLaunchKernelGGL((aotx_rgemv_wide<2, 4, 8, 1>), grid, dim3(512), xb, s, a);
+        } else if (a.rt == 4u) {
+            const size_t xb = 2u * 32u * (4u * 128u + 8u) * 2u;
+            hipLaunchKernelGGL((aotx_rgemv_wide<4, 2, 4, 1>), grid, dim3(512), xb, s, a);
+        } else {
+            const size_t xb = 2u * 32u * (4u * 128u + 8u) * 2u;
+            hipLaunchKernelGGL((aotx_rgemv_wide<8, 1, 4, 2>), grid, dim3(512), xb, s, a);
+        }
         AOTX_LAUNCH_CHECK();
         if (a.splits > 1u) {
             hipLaunchKernelGGL((aotx_rgemv_reduce<32>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
