@@ -11,11 +11,13 @@ unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
 size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned int splits,
                          unsigned int group, unsigned int head_dim);
 /* q/out fp16 [tokens][heads][d]; m_dev = device token count (or null); partial = the
- * caller's chunk buffer (or null for the library scratch). */
+ * caller's chunk buffer and count its [tokens * kv_heads] arrival counters, zeroed once
+ * at allocation and left at zero by every launch (either null for the library scratch). */
 int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsigned int *pos,
                        const unsigned int *agent, const unsigned int *m_dev,
                        unsigned int tokens, unsigned int heads, unsigned int kv_heads,
                        unsigned int head_dim, unsigned int layer, unsigned int layers,
-                       unsigned int max_context, float *partial, hipStream_t stream);
+                       unsigned int max_context, float *partial, unsigned int *count,
+                       hipStream_t stream);
 
 #endif

@@ -16,8 +16,9 @@
  *     softmax per block in base 2 (scores carry log2(e) / sqrt(d)), fp32 accumulation;
  *   - the waves' (max, mass, sum) are merged in wave order through LDS. At small batches
  *     the context is split over workgroups (flash-decoding) so that the launch still
- *     covers the GPU, and a merge kernel adds the chunks of a (token, KV head) in chunk
- *     order, so the result does not depend on timing.
+ *     covers the GPU; the last chunk of a (token, KV head) to finish adds all of its
+ *     chunks in chunk order, so the result does not depend on timing and no second
+ *     launch is needed.
  */
 #include "aotx_internal.h"
 
@@ -44,11 +45,12 @@ struct aotx_attn_args {
     aotx_kvl_shape shape;
     aotx_state *state;
     float *partial;               /* [tokens*kv_heads][splits][G*(d+2)] */
+    unsigned int *count;          /* [tokens*kv_heads] chunk arrivals, zero between launches */
 };
 
 #define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
 #define ATTN_MAX_SPLITS 32u
-#define ATTN_TARGET_GROUPS 256u
+#define ATTN_TARGET_GROUPS 192u
 
 /* A kernel-constant word (the device token count) read through the scalar cache. */
 static __device__ __forceinline__ unsigned int aotx_attn_scalar(const unsigned int *p)
@@ -61,6 +63,16 @@ static __device__ __forceinline__ unsigned int aotx_attn_scalar(const unsigned i
 static __device__ __forceinline__ float aotx_exp2(float x)
 {
     return __builtin_amdgcn_exp2f(x);
+}
+
+/* Chunk partials cross workgroups on different XCDs: device-scope stores and loads. */
+static __device__ __forceinline__ void aotx_attn_put(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+static __device__ __forceinline__ float aotx_attn_get(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Chunk length of a token with n positions under S splits (whole 64-position units). */
@@ -270,60 +282,56 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
             float back = msum > 0.0f ? 1.0f / msum : 0.0f;
             a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
         } else {
-            mine[j * (D + 2) + 2 + e] = osum;
+            aotx_attn_put(mine + j * (D + 2) + 2 + e, osum);
             if (e == 0u) {
-                mine[j * (D + 2)] = top;
-                mine[j * (D + 2) + 1] = msum;
+                aotx_attn_put(mine + j * (D + 2), top);
+                aotx_attn_put(mine + j * (D + 2) + 1, msum);
             }
         }
     }
-}
-
-/* Merge the chunks of every (token, KV head) that was split, in chunk order:
- * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). One workgroup
- * per (token, KV head, query head), one thread per output column; every thread issues all
- * of its loads (each chunk's maximum, mass and sum) at once and forms the chunk weights
- * itself, so the merge is one round trip to memory with no LDS and no barrier. */
-template <int D, int G>
-__global__ __launch_bounds__(D) void aotx_attend_merge(aotx_attn_args a)
-{
-    unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
-    if (tokens > a.tokens) tokens = a.tokens;
-    const unsigned int unit = blockIdx.x;
-    const unsigned int j = blockIdx.y;
-    const unsigned int e = threadIdx.x;
-    const unsigned int kh = unit % a.kv_heads;
-    const unsigned int t = unit / a.kv_heads;
-    if (t >= tokens) return;
-    const unsigned int S = a.splits;
-    const unsigned int n = a.pos[t] + 1u;
-    const unsigned int chunk = aotx_attn_chunk(n, S);
-    const unsigned int st = (n + chunk - 1u) / chunk;
-    if (st <= 1u) return;
-    const unsigned int stride = G * (D + 2);
-    const float *all = a.partial + (unsigned long long)unit * S * stride + j * (D + 2);
-    float mc[ATTN_MAX_SPLITS], lc[ATTN_MAX_SPLITS], oc[ATTN_MAX_SPLITS];
-#pragma unroll
-    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) {
-        const bool live = c < st;
-        mc[c] = live ? all[c * stride] : -INFINITY;
-        lc[c] = live ? all[c * stride + 1u] : 0.0f;
-        oc[c] = live ? all[c * stride + 2u + e] : 0.0f;
+    if (st == 1u) return;
+    /* The last chunk of the (token, KV head) to finish merges all of them, in chunk order:
+     * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). Partials
+     * are written and read as device-scope accesses (through to the point where all XCDs
+     * meet, past the per-XCD L2), and every one of this workgroup's writes has completed
+     * before its arrival is counted, so no cache write-back or invalidation is needed. The
+     * last arrival puts the counter back to zero for the next launch. */
+    __shared__ unsigned int last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        last = atomicAdd(a.count + unit, 1u) == st - 1u ? 1u : 0u;
+        if (last != 0u) atomicExch(a.count + unit, 0u);
     }
-    float top = -INFINITY;
+    __syncthreads();
+    if (last == 0u) return;
+    const float *all = a.partial + (unsigned long long)unit * S * stride;
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += 64u * W) {
+        const unsigned int j = idx / D, e = idx - j * D;
+        const float *col = all + j * (D + 2);
+        float mc[ATTN_MAX_SPLITS], lc[ATTN_MAX_SPLITS], oc[ATTN_MAX_SPLITS];
 #pragma unroll
-    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) top = fmaxf(top, mc[c]);
-    float msum = 0.0f, osum = 0.0f;
-#pragma unroll
-    for (unsigned int c = 0; c < ATTN_MAX_SPLITS; ++c) {
-        if (c < st) {
-            const float f = mc[c] == -INFINITY ? 0.0f : aotx_exp2(mc[c] - top);
-            msum += lc[c] * f;
-            osum += oc[c] * f;
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
+            const bool live = cc < st;
+            mc[cc] = live ? aotx_attn_get(col + cc * stride) : -INFINITY;
+            lc[cc] = live ? aotx_attn_get(col + cc * stride + 1u) : 0.0f;
+            oc[cc] = live ? aotx_attn_get(col + cc * stride + 2u + e) : 0.0f;
         }
+        float top = -INFINITY;
+#pragma unroll
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) top = fmaxf(top, mc[cc]);
+        float msum = 0.0f, osum = 0.0f;
+#pragma unroll
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
+            if (cc < st) {
+                const float f = mc[cc] == -INFINITY ? 0.0f : aotx_exp2(mc[cc] - top);
+                msum += lc[cc] * f;
+                osum += oc[cc] * f;
+            }
+        }
+        const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
+        a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
     }
-    const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-    a.out[((unsigned long long)t * a.heads + kh * G + j) * D + e] = aotx_f2h(osum * back);
 }
 
 /* ---------------------------------------------------------------------------------------
@@ -360,7 +368,8 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
                        const unsigned int *agent, const unsigned int *m_dev,
                        unsigned int tokens, unsigned int heads, unsigned int kv_heads,
                        unsigned int head_dim, unsigned int layer, unsigned int layers,
-                       unsigned int max_context, float *partial, hipStream_t stream)
+                       unsigned int max_context, float *partial, unsigned int *count,
+                       hipStream_t stream)
 {
     if (tokens == 0u || kv_heads == 0u || heads % kv_heads != 0u) return 1;
     if (head_dim != 64u && head_dim != 128u) return 1;
@@ -385,15 +394,15 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
         ? partial
         : (float *)aotx_scratch(AOTX_SCRATCH_ATTN_PARTIAL,
                                 aotx_attn_scratch(tokens, kv_heads, a.splits, g, head_dim));
+    a.count = count != nullptr
+        ? count
+        : (unsigned int *)aotx_scratch(AOTX_SCRATCH_ATTN_COUNT,
+                                       (size_t)tokens * kv_heads * sizeof(unsigned int));
     dim3 grid(tokens * kv_heads * a.splits);
 #define AOTX_ATTN_GO(DD, GG)                                                               \
     do {                                                                                   \
         hipLaunchKernelGGL((aotx_attend_mma<DD, GG, 8>), grid, dim3(512), 0, stream, a);   \
         AOTX_LAUNCH_CHECK();                                                               \
-        if (a.splits > 1u) {                                                               \
-            hipLaunchKernelGGL((aotx_attend_merge<DD, GG>), dim3(tokens * kv_heads, GG),   \
-                               dim3(DD), 0, stream, a);                                    \
-        }                                                                                  \
     } while (0)
     if (head_dim == 128u) {
         if (g == 1u) AOTX_ATTN_GO(128, 1);
@@ -420,7 +429,7 @@ extern "C" int aotx_attend_paged(const void *q, const unsigned int *pos,
     if (q == nullptr || pos == nullptr || agent == nullptr || out == nullptr) return 1;
     return aotx_attend_launch((const unsigned short *)q, (unsigned short *)out, pos, agent,
                               nullptr, tokens, heads, kv_heads, head_dim, layer, layers,
-                              AOTX_SEQ_MAX_TOKENS, nullptr, aotx_stream(stream));
+                              AOTX_SEQ_MAX_TOKENS, nullptr, nullptr, aotx_stream(stream));
 }
 
 /* K/V rows into the pages (the page-write half of cuda/model/rope.cu:128-196). */

@@ -70,6 +70,7 @@ struct aotx_hold {
     float *gemv_partial;
     size_t gemv_partial_bytes;
     float *attn_partial;
+    unsigned int *attn_count;     /* chunk arrivals per (token, KV head), zero between launches */
     float *prob;
     unsigned int *ids;
     float *ey;
@@ -334,7 +335,8 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             aotx_launch_rope(r, T, s);
         }
         if (aotx_attend_launch(h->qh, h->att, h->pos, h->tagent, m_tokens, T, d->heads,
-                               d->kv_heads, hd, l, d->layers, max_context, h->attn_partial, s) != 0) {
+                               d->kv_heads, hd, l, d->layers, max_context, h->attn_partial,
+                               h->attn_count, s) != 0) {
             fprintf(stderr, "aotx: attention refused the shape\n");
             exit(1);
         }
@@ -592,6 +594,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
         if (need > ap) ap = need;
     }
     h->attn_partial = (float *)aotx_take(h, ap);
+    h->attn_count = (unsigned int *)aotx_take(h, (size_t)T * d->kv_heads * 4u);
     if (d->expert_count != 0u) {
         size_t slots = T * d->expert_used_count;
         h->prob = (float *)aotx_take(h, T * d->expert_count * 4u);

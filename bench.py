@@ -369,7 +369,7 @@ def main():
     }
     result["roofline"] = {
         "bound": "hbm",
-        "kernel": f"aotx_attend_kernel<128,4> (paged decode attention, batch {args.batch}, "
+        "kernel": f"aotx_attend_mma<128,4,8> (paged decode attention, batch {args.batch}, "
                   f"context {args.context}, 32/8 heads x 128)",
         "achieved": round(att_bytes / att_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(att_bytes / att_us / 1e3 / HBM_PEAK_GBS, 4),

@@ -225,3 +225,61 @@ def test_prefill_all_rows(torch, orc, tiny):
             assert rel_rms(lg[n - 1:n], want) < 1e-2
     finally:
         rt.close()
+
+
+def _device_model(torch, shape, seed):
+    """Weights synthesised on the device (the bytes build_host writes), copied back for the
+    oracle: host synthesis of 4096-wide tensors takes minutes."""
+    from aotx_amd.model import build_device
+    region_dev, lay = build_device(shape, seed=seed)
+    return region_dev, region_dev.cpu().numpy(), lay
+
+
+@pytest.mark.parametrize("rows", [32, 20])
+def test_8b_width_wide_batch_vs_oracle(torch, orc, rows):
+    """8B-width layer (d_model 4096, FFN 14336, 32/8 heads x 128) at 17..32 batch rows: the
+    QKV (rotary + page write), O and down (residual add + sums of squares) products take the
+    one-tile-per-workgroup wide kernel; a prompt pass of 4 tokens per slot, then a decode
+    step of one token per slot, logits vs the oracle."""
+    shape = Shape(layers=1, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
+                  vocab=1024)
+    region_dev, region, lay = _device_model(torch, shape, 5)
+    rt = Runtime(region_dev, lay.desc, max_tokens=128, pool_pages=256)
+    try:
+        ref = orc.Model(lay.desc, region, slots=rows, max_context=64, threads=8)
+        rng = np.random.default_rng(7)
+        ids = rng.integers(0, shape.vocab, 4 * rows).tolist()
+        offs = [4 * i for i in range(rows + 1)]
+        agents = list(range(rows))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        ids = rng.integers(0, shape.vocab, rows).tolist()
+        offs = list(range(rows + 1))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
+def test_8b_width_experts_wide_batch_vs_oracle(torch, orc):
+    """Routed experts at d_model 4096 with 24 rows: the expert down product (k = 4096) takes
+    the wide kernel through the expert row lists."""
+    shape = Shape(layers=1, hidden=4096, ffn=4096, heads=32, kv_heads=8, head_dim=128,
+                  vocab=1024, experts=4, used=2)
+    region_dev, region, lay = _device_model(torch, shape, 6)
+    rt = Runtime(region_dev, lay.desc, max_tokens=64, pool_pages=128)
+    try:
+        ref = orc.Model(lay.desc, region, slots=24, max_context=64, threads=8)
+        rng = np.random.default_rng(8)
+        ids = rng.integers(0, shape.vocab, 48).tolist()
+        offs = [2 * i for i in range(25)]
+        agents = list(range(24))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
