@@ -215,6 +215,10 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
         a.y = tmpl.y;
         a.ldy = tmpl.ldy;
         a.sumsq_out = tmpl.sumsq_out;
+        a.xg_out = tmpl.xg_out;
+        a.xg_w = tmpl.xg_w;
+        a.row_ss = tmpl.row_ss;
+        a.row_eps = tmpl.row_eps;
         a.qkv = tmpl.qkv;
         a.expert_stride = tmpl.expert_stride;
         a.list = tmpl.list;
@@ -250,6 +254,10 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     const unsigned int max_context = AOTX_SEQ_MAX_TOKENS;
     const bool fused_norm = T <= 16u;                /* x staged from the residual stream */
     const bool experts = d->expert_count != 0u;
+    /* wide batches of a dense model: the residual epilogue that ends each half also writes
+     * x = half(resid * w) for the next norm's weights w, and the next product multiplies its
+     * outputs by the rows' RMSNorm scale, so no norm kernel runs between them */
+    const bool scaled_x = !fused_norm && !experts;
 
     AOTX_CHECK(hipMemcpyAsync(h->step, h->pinned, sizeof(aotx_step), hipMemcpyHostToDevice, s));
     aotx_launch_rows(h->step, T, h->pos, h->tagent, h->last, s);
@@ -281,8 +289,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             x_in.sumsq = h->sumsq;
             x_in.eps = d->rms_eps;
         } else {
-            nrm.norm_w = attn_w;
-            aotx_launch_norm(nrm, T, s);
+            if (!scaled_x || l == 0u) {
+                nrm.norm_w = attn_w;
+                aotx_launch_norm(nrm, T, s);
+            } else {
+                x_in.row_ss = h->sumsq;          /* x = half(resid * attn_w) from the down product */
+                x_in.row_eps = d->rms_eps;
+            }
             x_in.xmode = AOTX_X_F16;
             x_in.x = h->x;
             x_in.ldx = d->hidden;
@@ -349,6 +362,10 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             t.y = h->resid;
             t.ldy = d->hidden;
             t.sumsq_out = h->sumsq;
+            if (scaled_x) {
+                t.xg_out = h->x;
+                t.xg_w = ffn_w;
+            }
             const void *o_w[1] = {RL->o};
             unsigned int o_rows[1] = {d->hidden};
             aotx_rproduct(h, o_w, o_rows, 1u, wide, AOTX_EPI_RESID, T, m_tokens, t);
@@ -411,11 +428,11 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
                 t.sumsq = h->sumsq;
                 t.eps = d->rms_eps;
             } else {
-                nrm.norm_w = ffn_w;
-                aotx_launch_norm(nrm, T, s);
                 t.xmode = AOTX_X_F16;
-                t.x = h->x;
+                t.x = h->x;                      /* half(resid * ffn_w) from the O product */
                 t.ldx = d->hidden;
+                t.row_ss = h->sumsq;
+                t.row_eps = d->rms_eps;
             }
             t.y = h->act;
             t.ldy = d->ffn;
@@ -430,6 +447,10 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             u.y = h->resid;
             u.ldy = d->hidden;
             u.sumsq_out = h->sumsq;
+            if (scaled_x && l + 1u < d->layers) {
+                u.xg_out = h->x;
+                u.xg_w = (const float *)aotx_tensor(d->layer[l + 1u].offset[AOTX_SLOT_ATTN_NORM]);
+            }
             const void *dn_w[1] = {RL->down};
             unsigned int dn_rows[1] = {d->hidden};
             aotx_rproduct(h, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_RESID, T, m_tokens, u);

@@ -67,7 +67,13 @@ struct aotx_rgemv_args {
     void *y;
     unsigned int ldy;
     float *partial;               /* splits > 1: [groups][splits][rt*16][MT] */
-    float *sumsq_out;             /* AOTX_EPI_RESID: [rows][n/64] sums of squares */
+    float *sumsq_out;             /* AOTX_EPI_RESID: [rows][n/16] sums of squares */
+    unsigned short *xg_out;       /* AOTX_EPI_RESID, optional: fp16 resid * xg_w, [rows][n] */
+    const float *xg_w;            /* the next norm's weights [n] */
+    const float *row_ss;          /* optional (wide batches, direct rows): the rows' partial
+                                     sums of squares [rows][k/16]; outputs are multiplied by
+                                     rsqrt(sum / k + eps) (the RMSNorm scale of x) */
+    float row_eps;
     aotx_qkv_epi qkv;
     /* routed experts (grid.y): as aotx_gemv_args */
     unsigned long long expert_stride;

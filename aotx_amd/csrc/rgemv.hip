@@ -193,12 +193,17 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             const unsigned int j = rest % rt, mm = rest / rt;
             const unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
             const bool row_ok = idx < total && mm < mrows && v0 < a.n;
+            const bool col_ok = row_ok && v0 + rr < a.n;
+            /* the next norm's weight is read alongside the residual, not after it */
+            const float gw = a.xg_out != nullptr && col_ok ? a.xg_w[v0 + rr] : 0.0f;
             float v = 0.0f;
-            if (row_ok && v0 + rr < a.n) {
+            if (col_ok) {
                 float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
                 v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : *p) + out[(j * 16u + rr) * MT + mm];
                 *p = v;
             }
+            if (a.xg_out != nullptr && col_ok)
+                a.xg_out[(unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
             float sq = v * v;
             sq += __shfl_xor(sq, 1, 64);
             sq += __shfl_xor(sq, 2, 64);
@@ -282,6 +287,43 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
         }
     }
 #undef RG_YROW
+}
+
+/* The RMSNorm scale of batch rows given as unscaled x (a.row_ss): out[row][mm] *= rsqrt(
+ * sum_i row_ss[m0 + mm][i] / k + eps), 16 threads per batch row adding its k/16 partial
+ * sums in a fixed order. rs is MT floats of LDS; ends with a barrier. */
+template <int MT, int NT>
+static __device__ __forceinline__ void rg_row_scale(const aotx_rgemv_args &a, float *out,
+                                                    unsigned int gr, unsigned int mrows, float *rs)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned int nss = (a.k + 15u) / 16u;
+    for (unsigned int base = 0; base < (unsigned int)MT * 16u; base += NT) {
+        const unsigned int mm = (base + tid) >> 4, l = tid & 15u;
+        float sum = 0.0f;
+        if (mm < mrows) {
+            /* 16 loads in flight at a time, added in index order */
+            const float *ss = a.row_ss + (unsigned long long)(a.m0 + mm) * nss;
+            for (unsigned int i0 = l; i0 < nss; i0 += 256u) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const unsigned int i = i0 + 16u * (unsigned int)u;
+                    v[u] = i < nss ? ss[i] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) sum += v[u];
+            }
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 8, 64);
+        if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
+    }
+    __syncthreads();
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
+    __syncthreads();
 }
 
 /* Eight fp16 values x = half(scale * r * w) of the fused norm (cuda/model/norm.cu:49-77),
@@ -797,6 +839,10 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
         return;
     }
+    if (a.row_ss != nullptr) {
+        __shared__ float rs[MT];
+        rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
+    }
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
 }
 
@@ -838,6 +884,10 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args 
         out[idx] = sum;
     }
     __syncthreads();
+    if (a.row_ss != nullptr) {
+        __shared__ float rs[MT];
+        rg_row_scale<MT, RG_THREADS>(a, out, nt * 16u, mrows, rs);
+    }
     /* the slab as a workgroup of its own: one tile (or one gate/up pair) */
     rg_epilogue<MT, RG_THREADS>(a, out, pair ? group * slabs + sl : group * a.rt + sl, nt, mrows, list);
 }
@@ -974,6 +1024,10 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
     aotx_rgemv_args a = a0;
     if (a.splits > 1u && a.partial == nullptr) {
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
+    }
+    if (a.row_ss != nullptr && (!a.wide || a.list != nullptr || a.xrow != nullptr)) {
+        fprintf(stderr, "aotx: the row-scaled product takes wide batches of direct rows only\n");
+        exit(1);
     }
     if (a.wide) {
         unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
