@@ -47,6 +47,7 @@ struct aotx_rgemv_args {
     unsigned int rt;              /* 16-row tiles per workgroup */
     unsigned int wide;            /* 1: the tile-split wide-batch kernel (fp16 x only) */
     unsigned int pd;              /* quads loaded ahead per wave (narrow kernel) */
+    unsigned int nw;              /* waves per workgroup (narrow kernel: 4 or 8) */
     unsigned int groups;          /* workgroups along n */
     unsigned int splits;          /* workgroups along k */
     unsigned int qps;             /* quads per split */

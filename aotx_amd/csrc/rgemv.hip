@@ -368,10 +368,12 @@ static __device__ __forceinline__ rg_u4 rg_x_piece(const aotx_rgemv_args &a, uns
 }
 
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
- * loaded ahead per wave. */
-template <int MT, int RT, int PD>
-__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
+ * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
+ * few tiles, so that each wave's share of the dequantisation is short). */
+template <int MT, int RT, int PD, int NW>
+__global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
 {
+    constexpr unsigned int NT = 64u * NW;
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const unsigned int tid = threadIdx.x;
     const unsigned int lane = tid & 63u;
@@ -397,9 +399,9 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     __shared__ unsigned int xsrc[MT];              /* source row of each batch row */
     __shared__ float xscale[MT];                   /* its RMSNorm scale (AOTX_X_NORM) */
 
-    /* ---- per-wave k quarter ---- */
+    /* ---- per-wave share of the k range ---- */
     const unsigned int nq = q1 - q0;
-    const unsigned int per = (nq + 3u) / 4u;
+    const unsigned int per = (nq + NW - 1u) / NW;
     const unsigned int wq0 = q0 + wave * per < q1 ? q0 + wave * per : q1;
     const unsigned int wq1 = wq0 + per < q1 ? wq0 + per : q1;
     const unsigned int r = lane & 15u, g = lane >> 4;
@@ -492,11 +494,11 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
     __shared__ float rres[RT * 16 * MT];               /* the epilogue's residual values */
     rg_u4 pre[RG_PRE][4];
     float ssp[16];
-    float rold[RT];
+    float rold[(RT * 16 * MT + 64 * NW - 1) / (64 * NW)];
     if (direct) {
 #pragma unroll
         for (int i = 0; i < RG_PRE; ++i) {
-            const unsigned int idx = tid + (unsigned int)i * RG_THREADS;
+            const unsigned int idx = tid + (unsigned int)i * NT;
             const unsigned int mm = idx / pieces, p = idx - mm * pieces;
             const unsigned int kk = kbeg + p * 8u;
             pre[i][0] = pre[i][1] = pre[i][2] = pre[i][3] = (rg_u4){0u, 0u, 0u, 0u};
@@ -521,14 +523,15 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
             }
         }
     }
+    constexpr unsigned int RPT = (RT * 16u * MT + NT - 1u) / NT;   /* residual values per thread */
     if (resid_pre) {
 #pragma unroll
-        for (int it = 0; it < RT; ++it) {
-            const unsigned int idx = tid + (unsigned int)it * RG_THREADS;
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
             const unsigned int rr = idx & 15u, rest = idx >> 4;
             const unsigned int j = rest % RT, mm = rest / RT;
             const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
-            rold[it] = mm < cap && v0 + rr < a.n
+            rold[it] = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n
                 ? ((const float *)a.y)[(unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr] : 0.0f;
         }
     }
@@ -574,17 +577,17 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
         }
         if (resid_pre) {
 #pragma unroll
-            for (int it = 0; it < RT; ++it) {
-                const unsigned int idx = tid + (unsigned int)it * RG_THREADS;
+            for (int it = 0; it < (int)RPT; ++it) {
+                const unsigned int idx = tid + (unsigned int)it * NT;
                 const unsigned int rr = idx & 15u, rest = idx >> 4;
-                rres[((rest % RT) * 16u + rr) * MT + rest / RT] = rold[it];
+                if (idx < RT * 16u * MT) rres[((rest % RT) * 16u + rr) * MT + rest / RT] = rold[it];
             }
         }
         rg_sync_lds();
         const unsigned int total = mrows * pieces;
 #pragma unroll
         for (int i = 0; i < RG_PRE; ++i) {
-            const unsigned int idx = tid + (unsigned int)i * RG_THREADS;
+            const unsigned int idx = tid + (unsigned int)i * NT;
             if (idx < total) {
                 const unsigned int mm = idx / pieces, p = idx - mm * pieces;
                 const unsigned int kk = kbeg + p * 8u;
@@ -597,7 +600,7 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
                 *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
             }
         }
-        for (unsigned int idx = tid + RG_PRE * RG_THREADS; idx < total; idx += RG_THREADS) {
+        for (unsigned int idx = tid + RG_PRE * NT; idx < total; idx += NT) {
             const unsigned int mm = idx / pieces, p = idx - mm * pieces;
             *(rg_u4 *)(xl + mm * xs + p * 8u) = rg_x_piece(a, xsrc[mm], kbeg + p * 8u,
                                                           norm ? xscale[mm] : 0.0f);
@@ -623,9 +626,9 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
 #undef RG_LOAD
 #undef RG_COMPUTE
 
-    /* ---- add the 4 waves' accumulators in wave order ---- */
+    /* ---- add the NW waves' accumulators in wave order ---- */
     __syncthreads();
-    float *part = (float *)lds;                      /* [4][RT*16][MT] */
+    float *part = (float *)lds;                      /* [NW][RT*16][MT] */
     const unsigned int gr = RT * 16u;
 #pragma unroll
     for (int j = 0; j < RT; ++j)
@@ -637,18 +640,21 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv(aotx_rgemv_args a)
                 part[(wave * gr + row) * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
             }
     __syncthreads();
-    float *out = part + 4u * gr * MT;
-    for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) {
-        out[idx] = part[idx] + part[gr * MT + idx] + part[2u * gr * MT + idx] + part[3u * gr * MT + idx];
+    float *out = part + NW * gr * MT;
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
+        float sum = part[idx];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * gr * MT + idx];
+        out[idx] = sum;
     }
     __syncthreads();
     if (a.splits > 1u) {
         float *mine = a.partial
             + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
-        for (unsigned int idx = tid; idx < gr * MT; idx += RG_THREADS) mine[idx] = out[idx];
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
         return;
     }
-    rg_epilogue<MT, RG_THREADS>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
+    rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
 }
 
 /* Wide batches (17..32 rows of fp16 x): a workgroup owns T 16-row tiles; its W = T * P
@@ -897,7 +903,7 @@ __global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args 
 static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
 {
     size_t x = (size_t)a.m * (a.qps * 128u + 8u) * 2u;
-    size_t red = (size_t)5u * a.rt * 16u * mt * 4u;
+    size_t red = (size_t)(a.nw + 1u) * a.rt * 16u * mt * 4u;
     return x > red ? x : red;
 }
 
@@ -917,6 +923,17 @@ static const aotx_rgemv_tune &aotx_rgemv_tuning()
         return v;
     }();
     return t;
+}
+
+/* Workgroup count up to which the narrow product runs 8 waves per workgroup
+ * (AOTX_RGEMV_NW8 overrides it for measurement sweeps). */
+static unsigned int tune_nw_limit()
+{
+    static const unsigned int v = [] {
+        const char *e = getenv("AOTX_RGEMV_NW8");
+        return e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 256u;
+    }();
+    return v;
 }
 
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
@@ -995,6 +1012,9 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     while (a->groups * s < target && (a->qn + s) / (s + 1u) >= minq) s += 1u;
     a->qps = (a->qn + s - 1u) / s;
     a->splits = (a->qn + a->qps - 1u) / a->qps;
+    /* 8 waves per workgroup while the launch has few workgroups (each wave then has half
+     * the quads to dequantise after its data arrives), 4 otherwise */
+    a->nw = a->groups * a->splits <= tune_nw_limit() ? 8u : 4u;
     return 0;
 }
 
@@ -1009,8 +1029,12 @@ static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
 {
     unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
     size_t lds = aotx_rgemv_lds(a, MT);
-    hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD>), dim3(a.groups * a.splits, ey), dim3(RG_THREADS),
-                       lds, s, a);
+    if (a.nw == 8u)
+        hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8>), dim3(a.groups * a.splits, ey), dim3(512),
+                           lds, s, a);
+    else
+        hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4>), dim3(a.groups * a.splits, ey), dim3(256),
+                           lds, s, a);
     AOTX_LAUNCH_CHECK();
     if (a.splits > 1u) {
         hipLaunchKernelGGL((aotx_rgemv_reduce<MT>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
