@@ -144,6 +144,66 @@ def attention_rate(torch, L, slots, context, heads, kvh, hd, layers):
     return us, algo
 
 
+def attention_ragged(torch, L, batch=32, lo=512, hi=8192, heads=32, kvh=8, hd=128, layers=4,
+                     seed=3):
+    """paged decode attention over `batch` sequences with context lengths
+    uniform in [lo, hi] (seeded), fp16 N(0, 1) keys/values, one query token per sequence at
+    its last position. Pages are handed out one at a time to the sequences in a seeded random
+    order, so a sequence's pages are a random selection of the pool's physical pages. The KV
+    layout holds `layers` layers (the launches rotate over them, so no launch finds the
+    previous one's bytes in the last-level cache). Returns (us per launch, algorithmic bytes
+    per launch, the context lengths)."""
+    import numpy as np
+    import aotx_amd as A
+    from aotx_amd.model import layout_pages
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(lo, hi + 1, batch)
+    need = [layout_pages(int(c) + 1, layers, kvh, hd) for c in ctx]
+    kvm = A.KvMap()
+    kvm.limit = int(sum(need)) + 8
+    A.check(L.aotx_kv_open(ctypes.byref(kvm)), "aotx_kv_open")
+    try:
+        order = np.repeat(np.arange(batch), need)
+        rng.shuffle(order)
+        for i, sl in enumerate(order):
+            if L.aotx_kv_request(int(sl), 1) != 1:
+                raise RuntimeError("page request refused")
+            if i % 64 == 63:
+                L.aotx_kv_serve(ctypes.byref(kvm), None)
+        L.aotx_kv_serve(ctypes.byref(kvm), None)
+        n = int(ctx.sum())
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        pos = torch.cat([torch.arange(int(c), dtype=torch.int32) for c in ctx]).cuda()
+        ag = torch.cat([torch.full((int(c),), i, dtype=torch.int32)
+                        for i, c in enumerate(ctx)]).cuda()
+        for layer in range(layers):
+            k = torch.randn(n, kvh * hd, device="cuda", generator=g).half()
+            v = torch.randn(n, kvh * hd, device="cuda", generator=g).half()
+            A.check(L.aotx_kv_write(A.ptr(k), A.ptr(v), A.ptr(pos), A.ptr(ag), n, kvh, hd, layer,
+                                    layers, None), "aotx_kv_write")
+            del k, v
+        torch.cuda.synchronize()
+        q = torch.randn(batch, heads, hd, device="cuda", generator=g).half()
+        out = torch.empty_like(q)
+        qpos = torch.tensor([int(c) - 1 for c in ctx], dtype=torch.int32, device="cuda")
+        qag = torch.arange(batch, dtype=torch.int32, device="cuda")
+        turn = [0]
+
+        def launch(st):
+            layer = turn[0] % layers
+            turn[0] += 1
+            A.check(L.aotx_attend_paged(A.ptr(q), A.ptr(qpos), A.ptr(qag), batch, heads, kvh, hd,
+                                        layer, layers, A.ptr(out), ctypes.c_void_p(st.cuda_stream)),
+                    "aotx_attend_paged")
+
+        us = graph_time(torch, launch)
+        algo = n * kvh * hd * 2 * 2 + 2 * q.numel() * 2
+    finally:
+        L.aotx_kv_close(ctypes.byref(kvm))
+    return us, algo, ctx
+
+
 def seat_context(torch, rt, slots, context, reserve, layers, kvh, hd):
     """Request pages for `context + reserve` positions per slot, write random fp16 K/V for
     positions [0, context) of every layer, and seat each slot at `context`."""
@@ -271,6 +331,40 @@ def traffic_run(args):
                       "copy_bytes": src.numel()}))
 
 
+def moe_run(args):
+    """BASELINE config 5 (`--moe`): Mixtral-shape routed-expert decoder (32 layers, d_model
+    4096, 8 experts of FFN 14336, top-2, vocab 32000), 64 slots at 4096-token paged KV, one
+    token per slot per step, greedy. Prints one JSON line with tokens/s and the step's
+    fraction of the HBM roofline (every expert is touched at 128 routed rows per layer)."""
+    import torch
+    import aotx_amd as A
+    from aotx_amd.model import MIXTRAL, Runtime, build_device, layout_pages
+    torch.cuda.init()
+    shape, batch, context = MIXTRAL, 64, 4096
+    t0 = time.perf_counter()
+    region, lay = build_device(shape, seed=0x5EED)
+    log(f"moe: weights {region.numel() / 1e9:.2f} GB built in {time.perf_counter() - t0:.1f}s")
+    reserve = args.warmup * 3 + args.steps * 3 + 8
+    per_slot = layout_pages(context + reserve, shape.layers, shape.kv_heads, shape.head_dim)
+    slots = list(range(batch))
+    rt = Runtime(region, lay.desc, max_tokens=batch, pool_pages=per_slot * batch + 8)
+    seat_context(torch, rt, slots, context, reserve, shape.layers, shape.kv_heads, shape.head_dim)
+    log(f"moe: seated {batch} x {context} in {time.perf_counter() - t0:.1f}s")
+    tps, ms = decode(torch, rt, slots, args.steps, args.warmup, A.neutral_how())
+    rt.close()
+    wbytes = region.numel()
+    ctx_mid = context + args.warmup + args.steps // 2
+    kv_tok = 2 * shape.kv_heads * shape.head_dim * 2 * shape.layers
+    step_bytes = wbytes + batch * (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
+    out = {"metric": "Mixtral-shape MoE decode tokens/s (BASELINE config 5)",
+           "value": round(tps, 2), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+           "steps": args.steps, "warmup": args.warmup, "batch": batch, "context": context,
+           "weights_gb": round(wbytes / 1e9, 3), "step_gb": round(step_bytes / 1e9, 3),
+           "step_roofline_frac": round(step_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+           "data": "synthetic (seeded N(0,0.02) Q8_0 weights; random fp16 KV; greedy ids)"}
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +374,8 @@ def main():
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--moe", action="store_true",
+                    help="BASELINE config 5 only: the Mixtral-shape routed-expert decoder")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the roofline kernel and a calibration copy (counter passes)")
     args = ap.parse_args()
@@ -291,6 +387,9 @@ def main():
 
     if args.traffic:
         traffic_run(args)
+        return
+    if args.moe:
+        moe_run(args)
         return
 
     import torch
@@ -382,6 +481,16 @@ def main():
             "frac": round(dom["repacked_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_launch": dom["bytes"], "us_per_launch": dom["repacked_us"]}
     rt.close()
+
+    # ragged contexts over permuted pages
+    r_us, r_bytes, r_ctx = attention_ragged(torch, L)
+    log(f"bench: attention 32 x U[512, 8192] (mean {r_ctx.mean():.0f}): {r_us:.2f} us, "
+        f"{r_bytes / r_us / 1e3:.1f} GB/s")
+    result["paged_attention_ragged"] = {
+        "kernel": "aotx_attend_mma<128,4,8>", "batch": 32, "context": "U[512, 8192] seeded",
+        "context_sum": int(r_ctx.sum()), "us_per_launch": round(r_us, 2),
+        "bytes_per_launch": int(r_bytes), "achieved": round(r_bytes / r_us / 1e3, 1),
+        "unit": "GB/s", "frac": round(r_bytes / r_us / 1e3 / HBM_PEAK_GBS, 4)}
 
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
