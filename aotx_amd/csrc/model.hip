@@ -35,6 +35,7 @@
 unsigned long long aotx_mem_weights_bytes(void);
 
 #define AOTX_BUCKETS 10u   /* 1, 2, 4, ..., 512 */
+#define AOTX_GEMV_COUNTS 65536u   /* split arrival counters: experts x product groups */
 
 /* Repacked (Q8R) copies of one layer's matrices; the library owns them. */
 struct aotx_rlayer {
@@ -69,6 +70,7 @@ struct aotx_hold {
     unsigned int *pos, *tagent, *last;
     float *gemv_partial;
     size_t gemv_partial_bytes;
+    unsigned int *gemv_count;     /* split arrivals per product group, zero between launches */
     float *attn_partial;
     unsigned int *attn_count;     /* chunk arrivals per (token, KV head), zero between launches */
     float *prob;
@@ -233,6 +235,12 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
                 exit(1);
             }
             a.partial = h->gemv_partial;
+            const unsigned int e = a.expert_stride != 0ull ? a.experts : 1u;
+            if (e * a.groups > AOTX_GEMV_COUNTS) {
+                fprintf(stderr, "aotx: split counters exceed the planned buffer\n");
+                exit(1);
+            }
+            a.count = h->gemv_count;
         }
         aotx_rgemv_launch(a, h->stream);
     }
@@ -608,6 +616,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     }
     h->gemv_partial_bytes = gp + 4096u;
     h->gemv_partial = (float *)aotx_take(h, h->gemv_partial_bytes);
+    h->gemv_count = (unsigned int *)aotx_take(h, AOTX_GEMV_COUNTS * sizeof(unsigned int));
     size_t ap = 0u;
     for (unsigned int t = 1u; t <= cap; t <<= 1) {
         unsigned int sp = aotx_attn_splits(t, d->kv_heads, AOTX_SEQ_MAX_TOKENS);

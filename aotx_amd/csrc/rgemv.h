@@ -68,6 +68,7 @@ struct aotx_rgemv_args {
     void *y;
     unsigned int ldy;
     float *partial;               /* splits > 1: [groups][splits][rt*16][MT] */
+    unsigned int *count;          /* splits > 1: [experts][groups] arrivals, zero between launches */
     float *sumsq_out;             /* AOTX_EPI_RESID: [rows][n/16] sums of squares */
     unsigned short *xg_out;       /* AOTX_EPI_RESID, optional: fp16 resid * xg_w, [rows][n] */
     const float *xg_w;            /* the next norm's weights [n] */

@@ -4,17 +4,18 @@
  * fp32 accumulation in v_mfma_f32_16x16x32_f16; reference: cuda/model/gemv.cuh:33-195,
  * cuda/model/gemm.cuh:55-189), arranged so that the weight stream never touches LDS and no
  * wave waits on another inside the k loop:
- *   - a workgroup owns rt 16-row tiles and a k range; its 4 waves take contiguous quarters
- *     of the k range, each for all rt tiles, and stream their weights with two 16-byte
+ *   - a workgroup owns rt 16-row tiles and a k range; its 4 (or 8) waves take contiguous
+ *     shares of the k range, each for all rt tiles, and stream their weights with two 16-byte
  *     loads per lane per tile per 128 k (the repacked layout puts a lane's 32 quants of one
  *     block next to each other), `pd` quads ahead of the MFMAs;
  *   - the batch rows of x for the workgroup's k range sit in LDS, staged once at the start
  *     (from fp16 x, or computed there from the residual stream: x = half(rsqrt(ss/h + eps)
  *     * resid * w), the reference's RMSNorm rounding of cuda/model/norm.cu:49-77, so the
  *     norm costs no kernel of its own);
- *   - the 4 waves' accumulators are added in wave order through LDS at the end; with k
- *     split over workgroups the partial tiles go to memory and a second kernel adds them in
- *     split order. Results do not depend on timing.
+ *   - the waves' accumulators are added in wave order through LDS at the end; with k split
+ *     over workgroups the partial tiles go to memory and the last split of the group to
+ *     finish (an arrival counter) adds them in split order and applies the epilogue, so
+ *     there is no second launch. Results do not depend on timing.
  *   - epilogues as gemv.hip, plus the residual add that also leaves the sums of squares of
  *     every 16 rows for the next norm.
  */
@@ -29,7 +30,6 @@ typedef _Float16 rg_h2 __attribute__((ext_vector_type(2)));
 typedef float rg_f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int rg_u4 __attribute__((ext_vector_type(4)));
 
-#define RG_THREADS 256
 
 /* A kernel-constant word read through the scalar cache (counted by lgkmcnt, so waiting for
  * it does not wait for the vector loads issued before it). Only for memory no kernel of
@@ -367,6 +367,52 @@ static __device__ __forceinline__ rg_u4 rg_x_piece(const aotx_rgemv_args &a, uns
     return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
 }
 
+/* Split partials cross workgroups on different XCDs: device-scope stores and loads (past
+ * the per-XCD L2, so no cache write-back or invalidation is needed). */
+static __device__ __forceinline__ void rg_put(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+static __device__ __forceinline__ float rg_get(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* k split over workgroups: publish this split's sums out[0, n); the last split of the
+ * product group to arrive adds all splits in split order (its own from LDS) into out and
+ * returns true; the others return false. All of this workgroup's stores have completed
+ * before its arrival is counted; the last arrival puts the counter back to zero. `last` is
+ * one word of LDS. */
+template <int NT>
+static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, float *out,
+                                                      unsigned int n, unsigned int expert,
+                                                      unsigned int group, unsigned int split,
+                                                      unsigned int *last)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned long long tile = (unsigned long long)expert * a.groups + group;
+    float *base = a.partial + tile * a.splits * n;
+    for (unsigned int idx = tid; idx < n; idx += NT) rg_put(base + (unsigned long long)split * n + idx, out[idx]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0u) {
+        const unsigned int arrived = atomicAdd(a.count + tile, 1u);
+        *last = arrived == a.splits - 1u ? 1u : 0u;
+        if (*last != 0u) atomicExch(a.count + tile, 0u);
+    }
+    __syncthreads();
+    if (*last == 0u) return false;
+    for (unsigned int idx = tid; idx < n; idx += NT) {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (unsigned int sp = 0; sp < a.splits; ++sp)
+            sum += sp == split ? out[idx] : rg_get(base + (unsigned long long)sp * n + idx);
+        out[idx] = sum;
+    }
+    __syncthreads();
+    return true;
+}
+
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
  * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
  * few tiles, so that each wave's share of the dequantisation is short). */
@@ -649,10 +695,8 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
     }
     __syncthreads();
     if (a.splits > 1u) {
-        float *mine = a.partial
-            + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
-        for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
-        return;
+        __shared__ unsigned int last;
+        if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
     rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
 }
@@ -663,8 +707,8 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
  * the MFMAs); the P waves of a tile take its quads of each chunk in turn (phase p: chunk
  * quads p, p + P, ...), so every wave streams its weights one quad ahead of the MFMAs
  * and all waves read the same x chunk. At the end the P phase sums of a tile are added in
- * phase order through LDS and the workgroup applies the epilogue, or with k split over
- * workgroups writes its partial tiles for aotx_rgemv_reduce. More phases put more waves
+ * phase order through LDS and the workgroup applies the epilogue (with k split over
+ * workgroups, the last split to finish adds the splits first). More phases put more waves
  * on the same tiles (more loads in flight per CU) at the price of more x staging. */
 template <int T, int P, int KC, int PDQ>
 __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
@@ -840,62 +884,14 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         __syncthreads();
     }
     if (a.splits > 1u) {
-        float *mine = a.partial
-            + (((unsigned long long)expert * a.groups + group) * a.splits + split) * gr * MT;
-        for (unsigned int idx = tid; idx < gr * MT; idx += NT) mine[idx] = out[idx];
-        return;
+        __shared__ unsigned int last;
+        if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
     if (a.row_ss != nullptr) {
         __shared__ float rs[MT];
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
     }
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
-}
-
-/* Add the split partials in split order, then the epilogue. One workgroup per 16-row tile
- * of a product group (per gate/up tile pair for the gated unit), so the adds of a launch
- * spread over many CUs and every thread's split loads are independent. */
-template <int MT>
-__global__ __launch_bounds__(RG_THREADS) void aotx_rgemv_reduce(aotx_rgemv_args a)
-{
-    __shared__ float out[32 * MT];
-    const unsigned int expert = blockIdx.y;
-    const unsigned int *list = nullptr;
-    unsigned int mrows = a.m;
-    if (a.expert_stride != 0ull) {
-        unsigned int total = rg_scalar(a.list_count + expert);
-        mrows = total > a.m0 ? total - a.m0 : 0u;
-        list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
-    } else if (a.m_dev != nullptr) {
-        unsigned int total = rg_scalar(a.m_dev);
-        mrows = total > a.m0 ? total - a.m0 : 0u;
-    }
-    if (mrows > a.m) mrows = a.m;
-    if (mrows > (unsigned int)MT) mrows = MT;
-    if (mrows == 0u) return;
-    const bool pair = a.epi == AOTX_EPI_SWIGLU;
-    const unsigned int slabs = pair ? a.rt / 2u : a.rt;
-    const unsigned int group = blockIdx.x / slabs;
-    const unsigned int sl = blockIdx.x % slabs;
-    const unsigned int nt = pair ? 2u : 1u;
-    const unsigned int gr = a.rt * 16u;
-    const float *all = a.partial
-        + ((unsigned long long)expert * a.groups + group) * a.splits * gr * MT;
-    for (unsigned int idx = threadIdx.x; idx < nt * 16u * MT; idx += RG_THREADS) {
-        unsigned int tile = idx / (16u * MT) == 0u ? sl : sl + slabs;
-        unsigned int at = tile * 16u * MT + idx % (16u * MT);
-        float sum = 0.0f;
-#pragma unroll 8
-        for (unsigned int sp = 0; sp < a.splits; ++sp) sum += all[(unsigned long long)sp * gr * MT + at];
-        out[idx] = sum;
-    }
-    __syncthreads();
-    if (a.row_ss != nullptr) {
-        __shared__ float rs[MT];
-        rg_row_scale<MT, RG_THREADS>(a, out, nt * 16u, mrows, rs);
-    }
-    /* the slab as a workgroup of its own: one tile (or one gate/up pair) */
-    rg_epilogue<MT, RG_THREADS>(a, out, pair ? group * slabs + sl : group * a.rt + sl, nt, mrows, list);
 }
 
 /* ---- host ---------------------------------------------------------------------------- */
@@ -969,8 +965,8 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
          * tiles (gate/up, head), 2 x 4 for few (QKV, O, down), measured best at the 8B
          * shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
          * no second launch) unless they have fewer than 192 workgroups and a long k (down):
-         * those split k towards 256 workgroups while a split keeps a whole chunk, and
-         * aotx_rgemv_reduce adds the partials. */
+         * those split k towards 256 workgroups while a split keeps a whole chunk, and the
+         * last split of a group to finish adds the partials. */
         a->wide = 1u;
         a->rt = tiles >= 1536u ? 8u : 2u;
         if (tw.rt == 8u || tw.rt == 4u || tw.rt == 2u) a->rt = tw.rt;
@@ -1036,11 +1032,6 @@ static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
         hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4>), dim3(a.groups * a.splits, ey), dim3(256),
                            lds, s, a);
     AOTX_LAUNCH_CHECK();
-    if (a.splits > 1u) {
-        hipLaunchKernelGGL((aotx_rgemv_reduce<MT>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
-                           dim3(RG_THREADS), 0, s, a);
-        AOTX_LAUNCH_CHECK();
-    }
 }
 
 void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
@@ -1048,6 +1039,10 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
     aotx_rgemv_args a = a0;
     if (a.splits > 1u && a.partial == nullptr) {
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
+    }
+    if (a.splits > 1u && a.count == nullptr) {
+        const size_t e = a.expert_stride != 0ull ? a.experts : 1u;
+        a.count = (unsigned int *)aotx_scratch(AOTX_SCRATCH_GEMV_COUNT, e * a.groups * sizeof(unsigned int));
     }
     if (a.row_ss != nullptr && (!a.wide || a.list != nullptr || a.xrow != nullptr)) {
         fprintf(stderr, "aotx: the row-scaled product takes wide batches of direct rows only\n");
@@ -1071,11 +1066,6 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             hipLaunchKernelGGL((aotx_rgemv_wide<8, 1, 4, 2>), grid, dim3(512), xb, s, a);
         }
         AOTX_LAUNCH_CHECK();
-        if (a.splits > 1u) {
-            hipLaunchKernelGGL((aotx_rgemv_reduce<32>), dim3(a.groups * (a.epi == AOTX_EPI_SWIGLU ? a.rt / 2u : a.rt), ey),
-                               dim3(RG_THREADS), 0, s, a);
-            AOTX_LAUNCH_CHECK();
-        }
         return;
     }
     if (a.rt == 1u) {
