@@ -962,13 +962,13 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     if (mt > 16u) {
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
         /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
-         * tiles (gate/up, head), 2 x 4 for few (QKV, O, down), measured best at the 8B
-         * shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
+         * tiles (gate/up pair, head), 4 x 2 for a 14336-row matrix, 2 x 4 for few (QKV, O,
+         * down), measured best at the 8B shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
          * no second launch) unless they have fewer than 192 workgroups and a long k (down):
          * those split k towards 256 workgroups while a split keeps a whole chunk, and the
          * last split of a group to finish adds the partials. */
         a->wide = 1u;
-        a->rt = tiles >= 1536u ? 8u : 2u;
+        a->rt = tiles >= 1536u ? 8u : (tiles >= 768u ? 4u : 2u);
         if (tw.rt == 8u || tw.rt == 4u || tw.rt == 2u) a->rt = tw.rt;
         a->pd = 8u / a->rt;                            /* phases */
         const unsigned int kc = a->pd == 4u ? 8u : 4u;
