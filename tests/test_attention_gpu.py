@@ -86,6 +86,58 @@ def test_attend_vs_oracle(torch, lib, orc, heads, kvh, d, layers, layer):
         lib.aotx_kv_close(ctypes.byref(m))
 
 
+def test_attend_config3_ragged_permuted(torch, lib, orc):
+    """BASELINE config 3 shape: 32 sequences, contexts uniform in [512, 8192], 32/8 heads x
+    128, pages handed out one at a time in a seeded random slot order (each sequence gets a
+    random selection of the pool's physical pages). One workgroup takes a whole sequence
+    here (up to 8192 positions); page decisions bit-exact, outputs vs the oracle."""
+    heads, kvh, d, layers, layer = 32, 8, 128, 2, 1
+    rng = np.random.default_rng(33)
+    slots = list(range(32))
+    contexts = [int(c) for c in rng.integers(512, 8193, len(slots))]
+    need = {s: layout_pages(n, layers, kvh, d) for s, n in zip(slots, contexts)}
+    pool = sum(need.values()) + 4
+    m = _open_pool(lib, pool)
+    try:
+        policy = KvPolicy(pool)
+        order = np.repeat(np.array(slots), [need[s] for s in slots])
+        rng.shuffle(order)
+        for i, s in enumerate(order):
+            assert lib.aotx_kv_request(int(s), 1) == 1
+            policy.request(int(s), 1)
+            if i % 64 == 63:
+                lib.aotx_kv_serve(ctypes.byref(m), None)
+                policy.serve()
+        lib.aotx_kv_serve(ctypes.byref(m), None)
+        policy.serve()
+        table = aotx_amd.KvTable()
+        lib.aotx_kv_table_read(ctypes.byref(table))
+        for s in slots:
+            got = [(table.page[s][i] - m.range) // aotx_amd.AOTX_KV_PAGE_BYTES for i in range(table.count[s])]
+            assert got == policy.page[s]
+        keys, vals = _fill(torch, lib, slots, contexts, layers, layer, kvh, d, rng)
+        q = rng.normal(0, 1, (len(slots), heads, d)).astype(np.float16)
+        pos = np.array([n - 1 for n in contexts], dtype=np.uint32)
+        ag = np.array(slots, dtype=np.uint32)
+        out = torch.zeros(len(slots) * heads * d, dtype=torch.float16, device="cuda")
+        lib.aotx_model_forget()
+        assert lib.aotx_attend_paged(p(dev(q, torch)), p(dev(pos, torch)), p(dev(ag, torch)),
+                                     len(slots), heads, kvh, d, layer, layers, p(out), None) == 0
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(len(slots), heads, d).astype(np.float32)
+        g = heads // kvh
+        for i, s in enumerate(slots):
+            for hh in range(0, heads, 3):
+                kk = keys[s][:, hh // g, :].astype(np.float32)
+                vv = vals[s][:, hh // g, :].astype(np.float32)
+                want = orc.attend_one(q[i, hh].astype(np.float32), kk, vv, contexts[i] - 1)
+                err = np.abs(got[i, hh] - want).max()
+                assert err < 4e-3, (i, hh, contexts[i], err)
+        assert lib.aotx_model_faulted() == 0
+    finally:
+        lib.aotx_kv_close(ctypes.byref(m))
+
+
 def test_attend_missing_page_counts_fault(torch, lib):
     m = _open_pool(lib, 8)
     try:
