@@ -66,7 +66,7 @@ struct aotx_hold {
     unsigned short *sel;
     float *qkv;                   /* fp32 QKV rows of the general path */
     float *logits;                /* [max_rows][vocab] */
-    unsigned int *pick_best;      /* [max_rows][16][2] largest logit per slice */
+    unsigned int *pick_best;      /* the sampler's buffer (aotx_pick_scratch) */
     unsigned int *pos, *tagent, *last;
     float *gemv_partial;
     size_t gemv_partial_bytes;
@@ -537,7 +537,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     h->sel = (unsigned short *)aotx_take(h, R * d->hidden * 2u);
     h->qkv = (float *)aotx_take(h, T * (wide + 2u * narrow) * 4u);
     h->logits = (float *)aotx_take(h, R * d->vocab * 4u);
-    h->pick_best = (unsigned int *)aotx_take(h, aotx_pick_scratch(R));
+    h->pick_best = (unsigned int *)aotx_take(h, aotx_pick_scratch(R, d->vocab));
     h->pos = (unsigned int *)aotx_take(h, T * 4u);
     h->tagent = (unsigned int *)aotx_take(h, T * 4u);
     h->last = (unsigned int *)aotx_take(h, AOTX_SLOTS * 4u);

@@ -10,7 +10,9 @@ void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
                       unsigned int top_k, float top_p, float temperature,
                       unsigned long long seed, int *token, unsigned int *draw,
                       const aotx_model_run *run, unsigned int *best, hipStream_t s);
-/* Bytes of the per-row candidate buffer (`best`) of aotx_launch_pick. */
-size_t aotx_pick_scratch(unsigned int rows);
+/* Bytes of the sampler's buffer (`best`) for `rows` rows of `vocab` logits: the slices'
+ * largest logits, the first-pass bucket counts (zeroed once at allocation, left at zero by
+ * every call) and the rows' exponentials. */
+size_t aotx_pick_scratch(unsigned int rows, unsigned int vocab);
 
 #endif

@@ -28,6 +28,7 @@
 #define PICK_BUCKETS 256u
 #define PICK_PASSES 2u
 #define PICK_CHUNKS 16u   /* workgroups per row of the largest-logit search */
+#define PICK_EXP_WGS 32u  /* workgroups per row of the exponentials and first histogram */
 
 #pragma clang fp contract(off)
 
@@ -90,6 +91,8 @@ struct aotx_pick_args {
     aotx_state *state;
     const aotx_model_run *run;    /* when set, every per-call value comes from here */
     unsigned int *best;           /* [rows][PICK_CHUNKS][2]: each chunk's (value bits, token) */
+    unsigned int *hist;           /* [rows][PICK_BUCKETS] first-pass counts, zero between calls */
+    float *ex;                    /* [rows][vocab] exp(v - top) */
 };
 
 /* (v, i) ranks ahead of (bv, bi) in the reference's largest-logit search: a larger value;
@@ -99,6 +102,31 @@ static __device__ __forceinline__ bool aotx_pick_ahead(float v, unsigned int i, 
                                                        unsigned int bi)
 {
     return v > bv || (v == bv && ((i & 255u) < (bi & 255u) || ((i & 255u) == (bi & 255u) && i < bi)));
+}
+
+/* The row's largest logit from the slices of aotx_argmax_kernel (reference order). */
+static __device__ __forceinline__ void aotx_pick_top(const aotx_pick_args &a, unsigned int r,
+                                                     float &best, unsigned int &at)
+{
+    const unsigned int *cand = a.best + (unsigned long long)r * PICK_CHUNKS * 2u;
+    best = -INFINITY;
+    at = 0u;
+    for (unsigned int c = 0u; c < PICK_CHUNKS; ++c) {
+        float v = __uint_as_float(cand[2u * c]);
+        unsigned int i = cand[2u * c + 1u];
+        if (aotx_pick_ahead(v, i, best, at)) {
+            best = v;
+            at = i;
+        }
+    }
+}
+
+/* The row's sampling settings (a per-row `how` overrides the call's). */
+static __device__ __forceinline__ float aotx_pick_warmth(const aotx_pick_args &a, unsigned int r)
+{
+    const aotx_model_how *how = a.run ? a.run->how : a.how;
+    if (how != nullptr) return how[r].temperature;
+    return a.run ? a.run->temperature : a.temperature;
 }
 
 /* The largest logit of each of PICK_CHUNKS slices of a row (grid: chunks x rows). The
@@ -157,6 +185,48 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_argmax_kernel(aotx_pick_arg
     }
 }
 
+/* exp(v - top) of every logit of a sampled row (stored for the pick's ordered sums) and
+ * the first pass of the cut search: the 256-bucket histogram over [top - 42, top], added
+ * into the row's counts (integer counts: their order does not matter). Grid: PICK_EXP_WGS
+ * x rows; rows at temperature 0 do nothing. */
+__global__ __launch_bounds__(PICK_THREADS) void aotx_pick_exp_kernel(aotx_pick_args a)
+{
+    __shared__ unsigned int bucket[PICK_BUCKETS];
+    const unsigned int tid = threadIdx.x;
+    const unsigned int r = blockIdx.y;
+    const aotx_model_run *run = a.run;
+    unsigned int rows = run ? run->rows : (a.rows_dev ? *a.rows_dev : a.rows);
+    int *token_out = run ? run->token : a.token;
+    if (r >= rows || token_out == nullptr) return;
+    if (run && run->select != AOTX_MODEL_ROWS_LAST) return;
+    if (aotx_pick_warmth(a, r) <= 0.0f) return;
+    float top;
+    unsigned int at;
+    aotx_pick_top(a, r, top, at);
+    for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS) bucket[i] = 0u;
+    __syncthreads();
+    const float *row = a.logits + (unsigned long long)r * a.ld;
+    float *ex = a.ex + (unsigned long long)r * a.vocab;
+    const float lo = -AOTX_MODEL_PICK_SPAN, hi = 0.0f, band = hi - lo;
+    const unsigned int span = (a.vocab + PICK_EXP_WGS - 1u) / PICK_EXP_WGS;
+    const unsigned int b0 = blockIdx.x * span;
+    const unsigned int b1 = b0 + span < a.vocab ? b0 + span : a.vocab;
+#pragma unroll 8
+    for (unsigned int i = b0 + tid; i < b1; i += PICK_THREADS) {
+        const float scaled = row[i] - top;
+        ex[i] = expf(scaled);
+        if (scaled >= lo && scaled <= hi) {
+            unsigned int b = (unsigned int)((scaled - lo) * (float)PICK_BUCKETS / band);
+            if (b >= PICK_BUCKETS) b = PICK_BUCKETS - 1u;
+            atomicAdd(&bucket[b], 1u);
+        }
+    }
+    __syncthreads();
+    unsigned int *h = a.hist + (unsigned long long)r * PICK_BUCKETS;
+    for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS)
+        if (bucket[i] != 0u) atomicAdd(h + i, bucket[i]);
+}
+
 __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args a)
 {
     __shared__ float part[PICK_THREADS];
@@ -164,8 +234,9 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
     __shared__ unsigned int bucket[PICK_BUCKETS];
     __shared__ float value[AOTX_MODEL_PICK_MAX];
     __shared__ unsigned int index[AOTX_MODEL_PICK_MAX];
+    __shared__ float t_min[AOTX_MODEL_PICK_MAX], t_mass[AOTX_MODEL_PICK_MAX], t_heat[AOTX_MODEL_PICK_MAX];
     __shared__ float s_top, s_sum, s_cut, s_lo, s_hi;
-    __shared__ unsigned int s_more, s_count, s_position;
+    __shared__ unsigned int s_more, s_position, s_slot;
 
     const unsigned int tid = threadIdx.x;
     const unsigned int r = blockIdx.x;
@@ -196,17 +267,9 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
 
     /* largest logit and its place, from the slices of aotx_argmax_kernel */
     if (tid == 0u) {
-        const unsigned int *cand = a.best + (unsigned long long)r * PICK_CHUNKS * 2u;
-        float best = -INFINITY;
-        unsigned int at = 0u;
-        for (unsigned int c = 0u; c < PICK_CHUNKS; ++c) {
-            float v = __uint_as_float(cand[2u * c]);
-            unsigned int i = cand[2u * c + 1u];
-            if (aotx_pick_ahead(v, i, best, at)) {
-                best = v;
-                at = i;
-            }
-        }
+        float best;
+        unsigned int at;
+        aotx_pick_top(a, r, best, at);
         s_top = best;
         mark[0] = at;
         s_position = atomicAdd(&a.state->draw[agent], 1u);
@@ -220,35 +283,71 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
         return;
     }
 
-    /* bucket search for the cut */
+    /* the row sum of exp(v - top) in the reference's order (thread t: tokens t, t + 256,
+     * ...; then thread 0 over the threads), from the stored exponentials */
+    const float *ex = a.ex + (unsigned long long)r * vocab;
+    float row_total = 0.0f;
+#pragma unroll 64
+    for (unsigned int i = tid; i < vocab; i += PICK_THREADS) row_total += ex[i];
+    part[tid] = row_total;
+    /* the first pass's counts, handed back to zero for the next call */
+    unsigned int *h = a.hist + (unsigned long long)r * PICK_BUCKETS;
+    for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS) {
+        bucket[i] = h[i];
+        h[i] = 0u;
+    }
+    __syncthreads();
+
+    /* bucket search for the cut: pass 0 counted by aotx_pick_exp_kernel, later passes
+     * here over the narrowed band */
     float lo = -AOTX_MODEL_PICK_SPAN;
     float hi = 0.0f;
     for (unsigned int pass = 0u; pass < PICK_PASSES; ++pass) {
-        for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS) bucket[i] = 0u;
-        __syncthreads();
         float band = hi - lo;
-        float row_total = 0.0f;
-#pragma unroll 8
-        for (unsigned int i = tid; i < vocab; i += PICK_THREADS) {
-            float scaled = row[i] - top;
-            if (pass == 0u) row_total += expf(scaled);
-            if (scaled >= lo && scaled <= hi) {
-                unsigned int b = (unsigned int)((scaled - lo) * (float)PICK_BUCKETS / band);
-                if (b >= PICK_BUCKETS) b = PICK_BUCKETS - 1u;
-                atomicAdd(&bucket[b], 1u);
+        if (pass != 0u) {
+            for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS) bucket[i] = 0u;
+            __syncthreads();
+            /* counts: any order, so 16-byte loads where the row allows */
+            const bool aligned = ((unsigned long long)row & 15ull) == 0ull;
+            const unsigned int body = aligned ? vocab / 4u * 4u : 0u;
+            if (aligned) {
+                const float4 *row4 = (const float4 *)row;
+#pragma unroll 16
+                for (unsigned int i4 = tid; i4 < vocab / 4u; i4 += PICK_THREADS) {
+                    const float4 f = row4[i4];
+                    const float fs[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float scaled = fs[e] - top;
+                        if (scaled >= lo && scaled <= hi) {
+                            unsigned int b = (unsigned int)((scaled - lo) * (float)PICK_BUCKETS / band);
+                            if (b >= PICK_BUCKETS) b = PICK_BUCKETS - 1u;
+                            atomicAdd(&bucket[b], 1u);
+                        }
+                    }
+                }
             }
+            for (unsigned int i = body + tid; i < vocab; i += PICK_THREADS) {
+                float scaled = row[i] - top;
+                if (scaled >= lo && scaled <= hi) {
+                    unsigned int b = (unsigned int)((scaled - lo) * (float)PICK_BUCKETS / band);
+                    if (b >= PICK_BUCKETS) b = PICK_BUCKETS - 1u;
+                    atomicAdd(&bucket[b], 1u);
+                }
+            }
+            __syncthreads();
         }
-        part[tid] = row_total;
-        __syncthreads();
         if (tid == 0u) {
             if (pass == 0u) {
                 float sum = 0.0f;
+#pragma unroll 16
                 for (unsigned int i = 0u; i < PICK_THREADS; ++i) sum += part[i];
                 s_sum = sum;
             }
             unsigned int held = 0u;
             s_more = 0u;
             s_cut = lo;
+#pragma unroll 8
             for (unsigned int b = PICK_BUCKETS; b != 0u; --b) {
                 if (held + bucket[b - 1u] > AOTX_MODEL_PICK_MAX) {
                     s_cut = lo + band * (float)b / (float)PICK_BUCKETS;
@@ -269,34 +368,74 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
         __syncthreads();
     }
 
-    /* candidates at or above the cut: each thread counts those of its contiguous run of
-     * tokens, and a prefix over the threads places them in token order. */
+    /* candidates at or above the cut. The sort below orders them by (value, id), a total
+     * order, so while they fit the 256 places their order of placement does not matter:
+     * one coalesced pass gives each the next free place (an LDS counter). Only when more
+     * pass the cut (logits equal to within the finest band, where the reference keeps
+     * whichever arrive first) are the 256 lowest token ids kept instead: each thread takes
+     * a contiguous run of tokens and a prefix over the threads places them in token order. */
     const float cut = s_cut;
-    const unsigned int per = (vocab + PICK_THREADS - 1u) / PICK_THREADS;
-    const unsigned int first = tid * per;
-    const unsigned int after = first + per < vocab ? first + per : vocab;
-    unsigned int mine = 0u;
-#pragma unroll 8
-    for (unsigned int i = first; i < after; ++i) {
-        if (row[i] - top >= cut) mine += 1u;
-    }
-    mark[tid] = mine;
+    if (tid == 0u) s_slot = 0u;
     __syncthreads();
-    if (tid == 0u) {
-        unsigned int run = 0u;
-        for (unsigned int i = 0u; i < PICK_THREADS; ++i) {
-            unsigned int c = mark[i];
-            mark[i] = run;
-            run += c;
-        }
-        s_count = run;
-    }
-    __syncthreads();
-    /* Place the candidates in token order; when more than 256 pass the cut (logits equal
-     * to within the finest band, where the reference keeps whichever arrive first), the
-     * 256 lowest token ids are kept. The list is then sorted by value. */
-    unsigned int count = s_count;
     {
+        /* one coalesced pass: every candidate takes the next place while places remain */
+        const unsigned int v4 = vocab / 4u;
+        const float4 *row4 = (const float4 *)row;
+        const bool aligned = ((unsigned long long)row & 15ull) == 0ull;
+        const unsigned int body = aligned ? v4 * 4u : 0u;
+        if (aligned) {
+#pragma unroll 16
+            for (unsigned int i4 = tid; i4 < v4; i4 += PICK_THREADS) {
+                const float4 f = row4[i4];
+                const float fs[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float scaled = fs[e] - top;
+                    if (scaled >= cut) {
+                        const unsigned int slot = atomicAdd(&s_slot, 1u);
+                        if (slot < AOTX_MODEL_PICK_MAX) {
+                            value[slot] = scaled;
+                            index[slot] = i4 * 4u + (unsigned int)e;
+                        }
+                    }
+                }
+            }
+        }
+        for (unsigned int i = body + tid; i < vocab; i += PICK_THREADS) {
+            const float scaled = row[i] - top;
+            if (scaled >= cut) {
+                const unsigned int slot = atomicAdd(&s_slot, 1u);
+                if (slot < AOTX_MODEL_PICK_MAX) {
+                    value[slot] = scaled;
+                    index[slot] = i;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    unsigned int count = s_slot;
+    if (count <= AOTX_MODEL_PICK_MAX) {
+        /* all placed */
+    } else {
+        const unsigned int per = (vocab + PICK_THREADS - 1u) / PICK_THREADS;
+        const unsigned int first = tid * per;
+        const unsigned int after = first + per < vocab ? first + per : vocab;
+        unsigned int run_mine = 0u;
+        for (unsigned int i = first; i < after; ++i) {
+            if (row[i] - top >= cut) run_mine += 1u;
+        }
+        __syncthreads();
+        mark[tid] = run_mine;
+        __syncthreads();
+        if (tid == 0u) {
+            unsigned int run = 0u;
+            for (unsigned int i = 0u; i < PICK_THREADS; ++i) {
+                unsigned int c = mark[i];
+                mark[i] = run;
+                run += c;
+            }
+        }
+        __syncthreads();
         unsigned int slot = mark[tid];
         for (unsigned int i = first; i < after; ++i) {
             float scaled = row[i] - top;
@@ -308,8 +447,8 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
                 slot += 1u;
             }
         }
+        count = AOTX_MODEL_PICK_MAX;
     }
-    if (count > AOTX_MODEL_PICK_MAX) count = AOTX_MODEL_PICK_MAX;
     for (unsigned int i = tid; i < AOTX_MODEL_PICK_MAX; i += PICK_THREADS) {
         if (i >= count) {
             value[i] = -INFINITY;
@@ -340,13 +479,26 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
             __syncthreads();
         }
     }
+    /* the per-candidate terms of the serial loops below, each the same expression as
+     * there, computed by all threads; thread 0 then adds them in candidate order */
+    const float heat = warmth;
+    {
+        const float v0 = value[0];
+        const float total = s_sum;
+        for (unsigned int i = tid; i < AOTX_MODEL_PICK_MAX; i += PICK_THREADS) {
+            t_min[i] = expf(value[i] - v0);
+            t_mass[i] = expf(value[i]) / total;
+            t_heat[i] = expf((value[i] - v0) / heat);
+        }
+    }
+    __syncthreads();
     if (tid != 0u) return;
 
     unsigned int keep = (want_k == 0u || want_k > count) ? count : want_k;
     if (min_p > 0.0f && min_p <= 1.0f) {
         unsigned int min_keep = 1u;
         for (unsigned int i = 1u; i < keep; ++i) {
-            if (expf(value[i] - value[0]) < min_p) break;
+            if (t_min[i] < min_p) break;
             min_keep = i + 1u;
         }
         keep = min_keep;
@@ -354,30 +506,32 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
     float limit = (want_p <= 0.0f || want_p > 1.0f) ? 1.0f : want_p;
     float mass = 0.0f;
     unsigned int taken = 0u;
+#pragma unroll 8
     for (unsigned int i = 0u; i < keep; ++i) {
-        mass += expf(value[i]) / s_sum;
+        mass += t_mass[i];
         taken = i + 1u;
         if (mass >= limit) break;
     }
-    float heat = warmth;
     float heat_total = 0.0f;
-    for (unsigned int i = 0u; i < taken; ++i) heat_total += expf((value[i] - value[0]) / heat);
+#pragma unroll 8
+    for (unsigned int i = 0u; i < taken; ++i) heat_total += t_heat[i];
     aotx_u32x4 word = aotx_philox_dev(position, 0u, 0u, agent, (unsigned int)stream,
                                       (unsigned int)(stream >> 32));
     float pick = (float)(word.x >> 8) * (1.0f / 16777216.0f) * heat_total;
     float walk = 0.0f;
     unsigned int chosen = index[0];
     for (unsigned int i = 0u; i < taken; ++i) {
-        walk += expf((value[i] - value[0]) / heat);
+        walk += t_heat[i];
         chosen = index[i];
         if (walk >= pick) break;
     }
     token_out[r] = (int)chosen;
 }
 
-size_t aotx_pick_scratch(unsigned int rows)
+size_t aotx_pick_scratch(unsigned int rows, unsigned int vocab)
 {
-    return (size_t)rows * PICK_CHUNKS * 2u * sizeof(unsigned int);
+    return (size_t)rows * (PICK_CHUNKS * 2u + PICK_BUCKETS) * sizeof(unsigned int)
+         + (size_t)rows * vocab * sizeof(float);
 }
 
 void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
@@ -404,7 +558,11 @@ void aotx_launch_pick(const float *logits, unsigned int ld, unsigned int vocab,
     a.state = aotx_state_device();
     a.run = run;
     a.best = best;
+    a.hist = best + (size_t)rows * PICK_CHUNKS * 2u;
+    a.ex = (float *)(a.hist + (size_t)rows * PICK_BUCKETS);
     hipLaunchKernelGGL(aotx_argmax_kernel, dim3(PICK_CHUNKS, rows), dim3(PICK_THREADS), 0, s, a);
+    AOTX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(aotx_pick_exp_kernel, dim3(PICK_EXP_WGS, rows), dim3(PICK_THREADS), 0, s, a);
     AOTX_LAUNCH_CHECK();
     hipLaunchKernelGGL(aotx_pick_kernel, dim3(rows), dim3(PICK_THREADS), 0, s, a);
     AOTX_LAUNCH_CHECK();
@@ -417,7 +575,7 @@ extern "C" int aotx_pick(const float *logits, unsigned int rows, unsigned int vo
 {
     if (logits == nullptr || agent == nullptr || token == nullptr || rows == 0u || vocab == 0u)
         return 1;
-    unsigned int *best = (unsigned int *)aotx_scratch(AOTX_SCRATCH_PICK, aotx_pick_scratch(rows));
+    unsigned int *best = (unsigned int *)aotx_scratch(AOTX_SCRATCH_PICK, aotx_pick_scratch(rows, vocab));
     aotx_launch_pick(logits, vocab, vocab, nullptr, rows, agent, how, top_k, top_p,
                      temperature, seed, token, draw, nullptr, best, aotx_stream(stream));
     return 0;
