@@ -250,6 +250,7 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
 
 static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br)
 {
+    (void)sel_all;    /* the head's rows are selected on the device from the call block */
     const aotx_model_desc *d = &h->desc;
     hipStream_t s = h->stream;
     const unsigned int T = 1u << bt;                 /* token capacity of this bucket */
@@ -468,15 +469,10 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     {
         aotx_rgemv_args t;
         memset(&t, 0, sizeof t);
+        /* the selected rows normalised once by a norm kernel: the head has thousands of
+         * workgroups, and staging the norm in each costs more than the launch */
         const float *out_w = (const float *)aotx_tensor(d->output_norm);
-        if (R <= 16u) {
-            t.xmode = AOTX_X_NORM;
-            t.resid = h->resid;
-            t.norm_w = out_w;
-            t.sumsq = h->sumsq;
-            t.eps = d->rms_eps;
-            t.xrow = sel_all ? nullptr : h->last;
-        } else {
+        {
             aotx_norm_args on = nrm;
             on.norm_w = out_w;
             on.x = nullptr;
