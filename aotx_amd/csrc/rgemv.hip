@@ -582,8 +582,11 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
         }
     }
 
+    /* with one tile per workgroup only the first buffer goes out before the staging, so
+     * every workgroup's x requests queue behind less of the grid's weight stream (measured
+     * faster for every one-tile shape; a gate/up pair keeps both buffers ahead) */
     RG_LOAD(0, wq0);
-    RG_LOAD(1, wq0 + PD);
+    if (RT > 1) RG_LOAD(1, wq0 + PD);
     if (a.expert_stride == 0ull && a.m_dev != nullptr) {
         unsigned int total = rg_scalar(a.m_dev);
         mrows = total > a.m0 ? total - a.m0 : 0u;
@@ -654,8 +657,8 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
         rg_sync_lds();
     }
 
-    /* both load buffers were filled before the staging; each is refilled right after its
-     * quads are computed, two steps ahead */
+    /* each buffer is refilled right after its quads are computed, two steps ahead */
+    if (RT == 1) RG_LOAD(1, wq0 + PD);
     if (wq0 < wq1) {
         unsigned int q = wq0;
         for (;;) {
