@@ -987,10 +987,13 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         return 0;
     }
     /* rows per workgroup: 4 tiles share the staged x of 9-16 batch rows; fewer rows take
-     * one tile (measured best at every 8B shape), gate/up pairs two. */
+     * one tile (measured best at every 8B shape), the gated unit two gate/up pairs. */
     const aotx_rgemv_tune &tune = aotx_rgemv_tuning();
     unsigned int rt = mt > 8u ? 4u : 1u;
     if (tune.rt != 0u) rt = tune.rt;
+    /* the gated unit takes two gate/up pairs per workgroup: its 448 workgroups are resident
+     * at once (896 single pairs ran in two rounds) */
+    if (epi == AOTX_EPI_SWIGLU && tune.rt == 0u) rt = 4u;
     if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
     a->rt = rt;
     a->pd = rt == 1u ? 4u : (rt == 2u ? 2u : 1u);
