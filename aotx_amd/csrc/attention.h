@@ -10,6 +10,15 @@ unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
 /* Bytes of the chunk partials of such a launch. */
 size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned int splits,
                          unsigned int group, unsigned int head_dim);
+struct aotx_attn_args;
+/* The arguments of a launch over these operands (the layer chain runs them as a stage);
+ * 1 when the shape is refused. */
+int aotx_attend_plan(aotx_attn_args *args, const unsigned short *q, unsigned short *out,
+                     const unsigned int *pos, const unsigned int *agent,
+                     const unsigned int *m_dev, unsigned int tokens, unsigned int heads,
+                     unsigned int kv_heads, unsigned int head_dim, unsigned int layer,
+                     unsigned int layers, unsigned int max_context, float *partial,
+                     unsigned int *count);
 /* q/out fp16 [tokens][heads][d]; m_dev = device token count (or null); partial = the
  * caller's chunk buffer and count its [tokens * kv_heads] arrival counters, zeroed once
  * at allocation and left at zero by every launch (either null for the library scratch). */

@@ -1,0 +1,330 @@
+/* Device code of paged decode attention (attention.hip): the per-workgroup body, shared
+ * by the standalone kernel and the layer chain (chain.hip).
+ */
+#ifndef AOTX_ATTENTION_DEV_H
+#define AOTX_ATTENTION_DEV_H
+
+#include "aotx_internal.h"
+#include "coherent.h"
+
+typedef unsigned int aotx_u4a __attribute__((ext_vector_type(4)));
+typedef _Float16 aotx_h4a __attribute__((ext_vector_type(4)));
+typedef _Float16 aotx_h8a __attribute__((ext_vector_type(8)));
+typedef float aotx_f4a __attribute__((ext_vector_type(4)));
+
+struct aotx_attn_args {
+    const unsigned short *q;      /* fp16 [tokens][heads][d] */
+    unsigned short *out;          /* fp16 [tokens][heads][d] */
+    const unsigned int *pos;      /* [tokens] */
+    const unsigned int *agent;    /* [tokens] */
+    const unsigned int *m_dev;    /* device token count, or null */
+    unsigned int tokens;
+    unsigned int heads;
+    unsigned int kv_heads;
+    unsigned int layer;
+    unsigned int splits;          /* chunks per (token, KV head) at most */
+    unsigned int chunk_max;       /* the largest context planned for */
+    aotx_kvl_shape shape;
+    aotx_state *state;
+    float *partial;               /* [tokens*kv_heads][splits][G*(d+2)] */
+    unsigned int *count;          /* [tokens*kv_heads] chunk arrivals, zero between launches */
+};
+
+#define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
+#define ATTN_MAX_SPLITS 32u
+#define ATTN_TARGET_GROUPS 192u
+
+/* A kernel-constant word (the device token count) read through the scalar cache. */
+static __device__ __forceinline__ unsigned int aotx_attn_scalar(const unsigned int *p)
+{
+    return *(const __attribute__((address_space(4))) unsigned int *)p;
+}
+
+/* 2^x with the hardware v_exp_f32: exp2(-inf) = 0, results below 2^-126 flush to 0 (weights
+ * that small do not change an fp32 sum of weights of order one). */
+static __device__ __forceinline__ float aotx_exp2(float x)
+{
+    return __builtin_amdgcn_exp2f(x);
+}
+
+/* Chunk partials cross workgroups on different XCDs: device-scope stores and loads. */
+static __device__ __forceinline__ void aotx_attn_put(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+static __device__ __forceinline__ float aotx_attn_get(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Chunk length of a token with n positions under S splits (whole 64-position units). */
+static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, unsigned int S)
+{
+    unsigned int chunk = (n + S - 1u) / S;
+    return (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
+}
+
+/* One workgroup = W waves = one (token, KV head, context chunk); each wave takes a
+ * contiguous run of 16-position layout blocks. Per wave and block, on the matrix cores:
+ *   - scores S[pos][head] = K . q^T: one v_mfma_f32_16x16x32_f16 per 32 of d, keys as the A
+ *     operand straight from memory (lane (r, g) holds row r, d 32kk + 8g..+7), the query
+ *     heads of the KV head as the B columns (heads past G are zero);
+ *   - the score layout (lane (r, g): head r, positions 4g..4g+3) is the A-operand layout of
+ *     v_mfma_f32_16x16x16_f16, so the probabilities feed P . V as fp16 (the mass adds the
+ *     same rounded probabilities, so numerator and denominator agree);
+ *   - the values need positions along k: the wave writes its block (row-major, rows padded
+ *     against bank conflicts) to a private LDS slot and reads 16-bit columns back;
+ *   - online softmax in base 2 per head with a max over the 4 lane groups of the head.
+ * The output accumulators hold heads 4g..4g+3 x 16 d columns per lane and PV step. */
+template <int D, int G, int W, bool CH, class Wait>
+static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a, unsigned int bx,
+                                                        Wait &wait)
+{
+    static_assert(G <= 16, "one MFMA tile of query heads");
+    constexpr int KK = D / 32;          /* score MFMA steps */
+    constexpr int VP = D / 32;          /* 16-byte value pieces per lane per block */
+    constexpr int NS = D / 16;          /* P.V MFMAs (16 d columns each) */
+    constexpr int VS = D + 8;           /* LDS row stride of a value block (halves) */
+    __shared__ float wm[W][G], wl[W][G];
+    __shared__ float wo[W][G][D];
+    __shared__ __attribute__((aligned(16))) unsigned short vl[W][16 * VS];
+
+    const unsigned int lane = threadIdx.x & 63u;
+    const unsigned int wave = threadIdx.x >> 6;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+    unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
+    if (tokens > a.tokens) tokens = a.tokens;
+    const unsigned int S = a.splits;
+    const unsigned int c = bx % S;
+    const unsigned int rest = bx / S;
+    const unsigned int kh = rest % a.kv_heads;
+    const unsigned int t = rest / a.kv_heads;
+    if (t >= tokens) return;
+    const unsigned int n = a.pos[t] + 1u;
+    const unsigned int chunk = aotx_attn_chunk(n, S);
+    const unsigned int st = (n + chunk - 1u) / chunk;
+    if (c >= st) return;
+    const unsigned int p0 = c * chunk;
+    const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
+    const unsigned int nblk = (p1 - p0 + 15u) / 16u;
+    const unsigned int per = (nblk + W - 1u) / W;
+    const unsigned int b0 = p0 / 16u + wave * per;
+    unsigned int b1 = b0 + per;
+    if (b1 > (p1 + 15u) / 16u) b1 = (p1 + 15u) / 16u;
+    const unsigned int agent = a.agent[t];
+    const aotx_kv_table *kv = &a.state->kv;
+    const float scale = 1.4426950408889634f / sqrtf((float)D);
+
+    wait();
+    aotx_h8a qb[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        aotx_u4a w = {0u, 0u, 0u, 0u};
+        if (r < (unsigned int)G)
+            w = co_load4<CH>(a.q + ((unsigned long long)t * a.heads + kh * G + r) * D
+                             + 32 * kk + 8 * g);
+        qb[kk] = __builtin_bit_cast(aotx_h8a, w);
+    }
+    float mrun = -INFINITY, lrun = 0.0f;     /* head r of this lane */
+    aotx_f4a o[NS];
+#pragma unroll
+    for (int cc = 0; cc < NS; ++cc) o[cc] = (aotx_f4a){0.0f, 0.0f, 0.0f, 0.0f};
+    int missing = 0;
+    const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + r) * D + 8u * g) * 2u;
+    const unsigned int vbyte = ((a.kv_heads + kh) * AOTX_KVL_BLOCK * D + lane * 8u) * 2u;
+    unsigned short *vw = vl[wave];
+
+    aotx_u4a kr[2][KK], vr[2][VP];
+    /* in a chain the newest position's keys and values were written by an earlier stage of
+     * the same launch: every block is read with device-scope loads (sc1) */
+    constexpr int CPOL = CH ? 16 : 0;
+    bool absent[2];
+    unsigned long long pages = 0ull;
+    unsigned int wbase = b0;
+#define MMA_WINDOW(B0)                                                                      \
+    do {                                                                                    \
+        wbase = (B0);                                                                       \
+        unsigned int bl = wbase + lane;                                                     \
+        pages = bl < b1 ? (unsigned long long)aotx_kvl_block(a.shape, kv, agent, a.layer, bl * 16u) \
+                        : 0ull;                                                             \
+    } while (0)
+#define MMA_LOAD(BUF, B)                                                                    \
+    do {                                                                                    \
+        if ((B) - wbase >= 64u) MMA_WINDOW(B);                                              \
+        unsigned long long pb = __shfl(pages, (int)((B) - wbase), 64);                     \
+        pb = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb >> 32)) << 32) \
+           | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb); \
+        absent[BUF] = pb == 0ull;                                                           \
+        __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
+            (void *)pb, (short)0, absent[BUF] ? 0 : (int)a.shape.block_bytes, 0x00020000);  \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            kr[BUF][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + kk * 64, 0, CPOL); \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u)                                      \
+            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * 1024, 0, CPOL); \
+    } while (0)
+
+#define MMA_COMPUTE(BUF, B)                                                                 \
+    do {                                                                                    \
+        if (absent[BUF]) missing = 1;                                                       \
+        aotx_f4a sc = {0.0f, 0.0f, 0.0f, 0.0f};                                             \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                    \
+                __builtin_bit_cast(aotx_h8a, kr[BUF][kk]), qb[kk], sc, 0, 0, 0);             \
+        /* the block's values into this wave's LDS slot (row-major, padded rows) */         \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u) {                                    \
+            const unsigned int piece = (unsigned int)u * 64u + lane;                        \
+            *(aotx_u4a *)(vw + (piece / (D / 8)) * VS + (piece % (D / 8)) * 8u) = vr[BUF][u]; \
+        }                                                                                   \
+        float pr[4];                                                                        \
+        float mb = -INFINITY;                                                               \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
+            const bool ok = p >= p0 && p < p1 && !absent[BUF];                              \
+            pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
+            mb = fmaxf(mb, pr[i]);                                                          \
+        }                                                                                   \
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
+        const float mnew = fmaxf(mrun, mb);                                                 \
+        const float shift = aotx_exp2(mrun - mnew);        /* 0 from -inf */                \
+        mrun = mnew;                                                                        \
+        aotx_h4a pa;                                                                        \
+        float mass = 0.0f;                                                                  \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const _Float16 ph = (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
+            pa[i] = ph;                                                                     \
+            mass += (float)ph;                                                              \
+        }                                                                                   \
+        lrun = lrun * shift + mass;                                                         \
+        /* the accumulators of heads 4g + i take those heads' shifts */                     \
+        if (__any(shift != 1.0f)) {                                                         \
+            float sh[4];                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) sh[i] = __shfl(shift, (int)(4u * g) + i, 64); \
+            _Pragma("unroll") for (int cc = 0; cc < NS; ++cc)                               \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
+        }                                                                                   \
+        _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
+            const unsigned short *col = vw + (4u * g) * VS + 16u * (unsigned int)cc + r;    \
+            aotx_h4a vb;                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                   \
+                vb[i] = __builtin_bit_cast(_Float16, col[(unsigned int)i * VS]);            \
+            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[cc], 0, 0, 0);          \
+        }                                                                                   \
+    } while (0)
+
+    if (b0 < b1) {
+        unsigned int b = b0;
+        MMA_WINDOW(b0);
+        MMA_LOAD(0, b);
+        for (;;) {
+            if (b + 1u < b1) MMA_LOAD(1, b + 1u);
+            MMA_COMPUTE(0, b);
+            b += 1u;
+            if (b >= b1) break;
+            if (b + 1u < b1) MMA_LOAD(0, b + 1u);
+            MMA_COMPUTE(1, b);
+            b += 1u;
+            if (b >= b1) break;
+        }
+    }
+#undef MMA_WINDOW
+#undef MMA_LOAD
+#undef MMA_COMPUTE
+
+    /* a head's mass over its 4 lane groups */
+    lrun += __shfl_xor(lrun, 16, 64);
+    lrun += __shfl_xor(lrun, 32, 64);
+    missing = __any(missing);
+    if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
+    if (g == 0u && r < (unsigned int)G) {
+        wm[wave][r] = missing ? -INFINITY : mrun;
+        wl[wave][r] = missing ? 0.0f : lrun;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned int head = 4u * g + (unsigned int)i;
+        if (head < (unsigned int)G) {
+#pragma unroll
+            for (int cc = 0; cc < NS; ++cc) wo[wave][head][16 * cc + r] = missing ? 0.0f : o[cc][i];
+        }
+    }
+    __syncthreads();
+    /* merge the W waves in wave order */
+    const unsigned int unit = t * a.kv_heads + kh;
+    const unsigned int stride = G * (D + 2);
+    float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D / 2); idx += 64u * W) {
+        const unsigned int j = idx / (D / 2), e = 2u * (idx - j * (D / 2));
+        float top = wm[0][j];
+#pragma unroll
+        for (int w = 1; w < W; ++w) top = fmaxf(top, wm[w][j]);
+        float msum = 0.0f, osum[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            float f = (wm[w][j] == -INFINITY) ? 0.0f : exp2f(wm[w][j] - top);
+            msum += wl[w][j] * f;
+            osum[0] += wo[w][j][e] * f;
+            osum[1] += wo[w][j][e + 1u] * f;
+        }
+        if (st == 1u) {
+            float back = msum > 0.0f ? 1.0f / msum : 0.0f;
+            co_store2h<CH>(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+                           aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
+        } else {
+            aotx_attn_put(mine + j * (D + 2) + 2 + e, osum[0]);
+            aotx_attn_put(mine + j * (D + 2) + 3 + e, osum[1]);
+            if (e == 0u) {
+                aotx_attn_put(mine + j * (D + 2), top);
+                aotx_attn_put(mine + j * (D + 2) + 1, msum);
+            }
+        }
+    }
+    if (st == 1u) return;
+    /* The last chunk of the (token, KV head) to finish merges all of them, in chunk order:
+     * M = max m_c, out = half(sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M)). Partials
+     * are written and read as device-scope accesses (through to the point where all XCDs
+     * meet, past the per-XCD L2), and every one of this workgroup's writes has completed
+     * before its arrival is counted, so no cache write-back or invalidation is needed. The
+     * last arrival puts the counter back to zero for the next launch. */
+    __shared__ unsigned int last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        last = atomicAdd(a.count + unit, 1u) == st - 1u ? 1u : 0u;
+        if (last != 0u) atomicExch(a.count + unit, 0u);
+    }
+    __syncthreads();
+    if (last == 0u) return;
+    const float *all = a.partial + (unsigned long long)unit * S * stride;
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D / 2); idx += 64u * W) {
+        const unsigned int j = idx / (D / 2), e = 2u * (idx - j * (D / 2));
+        const float *col = all + j * (D + 2);
+        float mc[ATTN_MAX_SPLITS], lc[ATTN_MAX_SPLITS], oc[ATTN_MAX_SPLITS], od[ATTN_MAX_SPLITS];
+#pragma unroll
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
+            const bool live = cc < st;
+            mc[cc] = live ? aotx_attn_get(col + cc * stride) : -INFINITY;
+            lc[cc] = live ? aotx_attn_get(col + cc * stride + 1u) : 0.0f;
+            oc[cc] = live ? aotx_attn_get(col + cc * stride + 2u + e) : 0.0f;
+            od[cc] = live ? aotx_attn_get(col + cc * stride + 3u + e) : 0.0f;
+        }
+        float top = -INFINITY;
+#pragma unroll
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) top = fmaxf(top, mc[cc]);
+        float msum = 0.0f, osum[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
+            if (cc < st) {
+                const float f = mc[cc] == -INFINITY ? 0.0f : aotx_exp2(mc[cc] - top);
+                msum += lc[cc] * f;
+                osum[0] += oc[cc] * f;
+                osum[1] += od[cc] * f;
+            }
+        }
+        const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
+        co_store2h<CH>(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+                       aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
+    }
+}
+
+#endif

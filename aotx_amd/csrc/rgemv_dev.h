@@ -1,0 +1,969 @@
+/* Device code of the streaming Q8 product (rgemv.hip): operand helpers, epilogues and
+ * the narrow-batch body, shared by the standalone kernels and the layer chain (chain.hip).
+ */
+#ifndef AOTX_RGEMV_DEV_H
+#define AOTX_RGEMV_DEV_H
+
+#include "coherent.h"
+#include "rgemv.h"
+
+typedef _Float16 rg_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 rg_h2 __attribute__((ext_vector_type(2)));
+typedef float rg_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int rg_u4 __attribute__((ext_vector_type(4)));
+
+
+/* A kernel-constant word read through the scalar cache (counted by lgkmcnt, so waiting for
+ * it does not wait for the vector loads issued before it). Only for memory no kernel of
+ * the same launch writes. */
+static __device__ __forceinline__ unsigned int rg_scalar(const unsigned int *p)
+{
+    return *(const __attribute__((address_space(4))) unsigned int *)p;
+}
+
+/* Workgroup barrier that waits for this wave's LDS operations only: global loads already
+ * in flight (the weight stream) stay in flight across it. */
+static __device__ __forceinline__ void rg_sync_lds()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+/* ---- product ------------------------------------------------------------------------ */
+
+static __device__ __forceinline__ void rg_dequant4(unsigned int w, rg_h2 s2, unsigned int &lo,
+                                                   unsigned int &hi)
+{
+    unsigned int u = w ^ 0x80808080u;
+    unsigned int a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    unsigned int b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const rg_h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(unsigned int, (__builtin_bit_cast(rg_h2, a) - bias) * s2);
+    hi = __builtin_bit_cast(unsigned int, (__builtin_bit_cast(rg_h2, b) - bias) * s2);
+}
+
+/* The segment holding output row v, and the first row of that segment. Written as sums
+ * of one-sided selects, never a select between two fields: the compiler turns the latter
+ * into one load from a computed offset, which keeps a copy of the arguments (the layer
+ * chain makes one) in scratch memory instead of registers. */
+static __device__ __forceinline__ unsigned int rg_seg(const aotx_rgemv_args &a, unsigned int v,
+                                                      unsigned int &begin)
+{
+    const bool past0 = a.nseg > 1u && v >= a.seg_end[0];
+    const bool past1 = a.nseg > 2u && v >= a.seg_end[1];     /* implies past0 */
+    begin = (past0 ? a.seg_end[0] : 0u) + (past1 ? a.seg_end[1] - a.seg_end[0] : 0u);
+    return (past0 ? 1u : 0u) + (past1 ? 1u : 0u);
+}
+static __device__ __forceinline__ unsigned int rg_seg_end(const aotx_rgemv_args &a, unsigned int seg)
+{
+    return a.seg_end[0] + (seg >= 1u ? a.seg_end[1] - a.seg_end[0] : 0u)
+         + (seg >= 2u ? a.seg_end[2] - a.seg_end[1] : 0u);
+}
+static __device__ __forceinline__ const unsigned char *rg_seg_w(const aotx_rgemv_args &a, unsigned int seg)
+{
+    const unsigned long long w0 = (unsigned long long)a.w[0], w1 = (unsigned long long)a.w[1],
+                             w2 = (unsigned long long)a.w[2];
+    const unsigned long long p = w0 + (seg >= 1u ? w1 - w0 : 0ull) + (seg >= 2u ? w2 - w1 : 0ull);
+    /* weights are global memory: global (not flat) loads */
+    return (const unsigned char *)(const __attribute__((address_space(1))) unsigned char *)p;
+}
+
+/* Weight tile j of a workgroup: Q8R base of its 16 rows, and whether it exists. */
+static __device__ __forceinline__ const unsigned char *rg_tile(const aotx_rgemv_args &a,
+                                                               unsigned int group, unsigned int j,
+                                                               unsigned int rt, unsigned int expert,
+                                                               unsigned int &quant_off_unused)
+{
+    (void)quant_off_unused;
+    unsigned int seg, tile;  /* tile index inside its segment's tensor */
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        seg = j < half ? 0u : 1u;
+        tile = group * half + (j < half ? j : j - half);
+    } else {
+        unsigned int v0 = (group * rt + j) * 16u;
+        unsigned int begin;
+        seg = rg_seg(a, v0, begin);
+        tile = (v0 - begin) / 16u;
+        unsigned int seg_tiles = (rg_seg_end(a, seg) - begin + 15u) / 16u;
+        if (tile >= seg_tiles) tile = seg_tiles - 1u;   /* past the last row: discarded */
+    }
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int seg_tiles = (a.n + 15u) / 16u;
+        if (tile >= seg_tiles) tile = seg_tiles - 1u;
+    }
+    return rg_seg_w(a, seg) + (unsigned long long)expert * a.expert_stride
+         + (unsigned long long)tile * a.qn * 2048ull;
+}
+
+/* Scale plane of the same tile: the quant plane of the whole tensor comes first. */
+static __device__ __forceinline__ const unsigned short *rg_scales(const aotx_rgemv_args &a,
+                                                                  unsigned int group, unsigned int j,
+                                                                  unsigned int rt, unsigned int expert)
+{
+    unsigned int seg, tile, seg_rows;
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        seg = j < half ? 0u : 1u;
+        tile = group * half + (j < half ? j : j - half);
+        seg_rows = a.n;
+    } else {
+        unsigned int v0 = (group * rt + j) * 16u;
+        unsigned int begin;
+        seg = rg_seg(a, v0, begin);
+        tile = (v0 - begin) / 16u;
+        seg_rows = rg_seg_end(a, seg) - begin;
+    }
+    unsigned long long tiles = (seg_rows + 15u) / 16u;
+    if (tile >= tiles) tile = (unsigned int)tiles - 1u;
+    const unsigned char *base = rg_seg_w(a, seg) + (unsigned long long)expert * a.expert_stride;
+    return (const unsigned short *)(base + tiles * a.qn * 2048ull)
+         + (unsigned long long)tile * a.qn * 64ull;
+}
+
+/* The virtual output row of row rr of tile j (SWIGLU: the gate/up row index). */
+static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a, unsigned int group,
+                                                       unsigned int j, unsigned int rr, unsigned int rt)
+{
+    if (a.epi == AOTX_EPI_SWIGLU) {
+        unsigned int half = rt / 2u;
+        return (group * half + (j < half ? j : j - half)) * 16u + rr;
+    }
+    return (group * rt + j) * 16u + rr;
+}
+
+/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. CH: the
+ * results are read by later stages of the same launch (device-scope stores; the F16 and
+ * plain residual forms are not used there). */
+template <int MT, int NT, bool CH = false>
+static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
+                                                   unsigned int group, unsigned int rt,
+                                                   unsigned int mrows, const unsigned int *list,
+                                                   const float *rpre = nullptr)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned int gr = rt * 16u;
+#define RG_YROW(mm) (list != nullptr ? list[(mm)] : a.m0 + (mm))
+    if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr) {
+        /* one thread per output: 16 consecutive threads hold the 16 rows of one tile for
+         * one row of x, add them into the residual stream, and leave the tile's sum of
+         * squares for the next norm with a 16-lane shuffle sum */
+        const unsigned int total = rt * 16u * MT;          /* a multiple of 16 */
+        for (unsigned int base = 0; base < total; base += NT) {
+            const unsigned int idx = base + tid;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % rt, mm = rest / rt;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, rt);
+            const bool row_ok = idx < total && mm < mrows && v0 < a.n;
+            const bool col_ok = row_ok && v0 + rr < a.n;
+            /* the next norm's weight is read alongside the residual, not after it */
+            const float gw = a.xg_out != nullptr && col_ok ? a.xg_w[v0 + rr] : 0.0f;
+            float v = 0.0f;
+            if (col_ok) {
+                float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
+                v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : co_loadf<CH>(p))
+                  + out[(j * 16u + rr) * MT + mm];
+                co_storef<CH>(p, v);
+            }
+            if (a.xg_out != nullptr && col_ok)
+                a.xg_out[(unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
+            float sq = v * v;
+            sq += __shfl_xor(sq, 1, 64);
+            sq += __shfl_xor(sq, 2, 64);
+            sq += __shfl_xor(sq, 4, 64);
+            sq += __shfl_xor(sq, 8, 64);
+            if (row_ok && rr == 0u)
+                co_storef<CH>(a.sumsq_out + (unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
+        }
+    } else if (a.epi == AOTX_EPI_F32 || a.epi == AOTX_EPI_F16 || a.epi == AOTX_EPI_RESID) {
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
+            unsigned int row = idx % gr, mm = idx / gr;
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            float val = out[row * MT + mm];
+            unsigned long long at = (unsigned long long)RG_YROW(mm) * a.ldy + v;
+            if (a.epi == AOTX_EPI_F32) co_storef<CH>((float *)a.y + at, val);
+            else if (a.epi == AOTX_EPI_F16) ((unsigned short *)a.y)[at] = aotx_f2h(val);
+            else ((float *)a.y)[at] += val;
+        }
+    } else if (a.epi == AOTX_EPI_SWIGLU) {
+        /* a thread takes two adjacent units (one 32-bit store; n and ldy are even) */
+        const unsigned int half = rt / 2u;
+        for (unsigned int idx = tid; idx < half * 8u * MT; idx += NT) {
+            unsigned int row = 2u * (idx % (half * 8u)), mm = idx / (half * 8u);
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            unsigned int h[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                float gate = out[(row + e) * MT + mm];
+                float up = out[(row + e + half * 16u) * MT + mm];
+                float unit = gate / (1.0f + expf(-gate));
+                h[e] = aotx_f2h(unit * up);
+            }
+            unsigned short *dst = (unsigned short *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v;
+            if (v + 1u < a.n) co_store2h<CH>(dst, h[0], h[1]);
+            else dst[0] = (unsigned short)h[0];            /* odd n (never in a chain) */
+        }
+    } else if (a.epi == AOTX_EPI_QKV) {
+        const aotx_qkv_epi &e = a.qkv;
+        const unsigned int d = e.head_dim;
+        const float step = powf(e.theta, -2.0f / (float)d);
+        for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += NT) {
+            unsigned int pr = idx % (gr / 2u), mm = idx / (gr / 2u);
+            unsigned int row = 2u * pr;
+            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+            if (mm >= mrows || v >= a.n) continue;
+            unsigned int begin;
+            const unsigned int sg = rg_seg(a, v, begin);
+            unsigned int local = v - begin;
+            unsigned int t = a.m0 + mm;
+            float a0 = out[row * MT + mm];
+            float a1 = out[(row + 1u) * MT + mm];
+            unsigned int head = local / d;
+            unsigned int dim = local - head * d;
+            unsigned int position = e.pos[t];
+            if (sg == 0u) {
+                float angle = (float)position * powf(step, (float)(dim >> 1));
+                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                unsigned short *dst = e.qh + (unsigned long long)t * e.heads * d + local;
+                co_store2h<CH>(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
+                continue;
+            }
+            unsigned char *blk = aotx_kvl_block(e.shape, &e.state->kv, e.agent[t], e.layer, position);
+            if (blk == nullptr) {
+                if (dim == 0u && sg == 1u) atomicAdd(&e.state->faults, 1u);
+                continue;
+            }
+            unsigned int krow = (sg == 1u ? head : e.kv_heads + head) * AOTX_KVL_BLOCK
+                              + position % AOTX_KVL_BLOCK;
+            unsigned short *dst = (unsigned short *)blk + (unsigned long long)krow * d + dim;
+            if (sg == 1u) {
+                float angle = (float)position * powf(step, (float)(dim >> 1));
+                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                co_store2h<CH>(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
+            } else {
+                co_store2h<CH>(dst, aotx_f2h(a0), aotx_f2h(a1));
+            }
+        }
+    }
+#undef RG_YROW
+}
+
+/* The RMSNorm scale of batch rows given as unscaled x (a.row_ss): out[row][mm] *= rsqrt(
+ * sum_i row_ss[m0 + mm][i] / k + eps), 16 threads per batch row adding its k/16 partial
+ * sums in a fixed order. rs is MT floats of LDS; ends with a barrier. */
+template <int MT, int NT>
+static __device__ __forceinline__ void rg_row_scale(const aotx_rgemv_args &a, float *out,
+                                                    unsigned int gr, unsigned int mrows, float *rs)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned int nss = (a.k + 15u) / 16u;
+    for (unsigned int base = 0; base < (unsigned int)MT * 16u; base += NT) {
+        const unsigned int mm = (base + tid) >> 4, l = tid & 15u;
+        float sum = 0.0f;
+        if (mm < mrows) {
+            /* 16 loads in flight at a time, added in index order */
+            const float *ss = a.row_ss + (unsigned long long)(a.m0 + mm) * nss;
+            for (unsigned int i0 = l; i0 < nss; i0 += 256u) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const unsigned int i = i0 + 16u * (unsigned int)u;
+                    v[u] = i < nss ? ss[i] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) sum += v[u];
+            }
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 8, 64);
+        if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
+    }
+    __syncthreads();
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
+    __syncthreads();
+}
+
+/* Eight fp16 values x = half(scale * r * w) of the fused norm (cuda/model/norm.cu:49-77),
+ * from the residual and norm-weight words already loaded. */
+static __device__ __forceinline__ rg_u4 rg_norm_piece(rg_u4 r0, rg_u4 r1, rg_u4 w0, rg_u4 w1,
+                                                      float scale)
+{
+    unsigned int rw[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    unsigned int ww[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+    unsigned int h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        h[e] = aotx_f2h(scale * __builtin_bit_cast(float, rw[e]) * __builtin_bit_cast(float, ww[e]));
+    return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
+/* Eight values of row `src` of x from k = kk (fp16 x, or the fused norm of the residual
+ * stream when scale != 0 is given for AOTX_X_NORM); k past a.k gives zeros. */
+template <bool CH>
+static __device__ __forceinline__ rg_u4 rg_x_piece(const aotx_rgemv_args &a, unsigned int src,
+                                                   unsigned int kk, float scale)
+{
+    if (a.xmode == AOTX_X_NORM) {
+        const float *rrow = a.resid + (unsigned long long)src * a.k;
+        if (kk + 8u <= a.k)
+            return rg_norm_piece(co_load4<CH>(rrow + kk), co_load4<CH>(rrow + kk + 4u),
+                                 *(const rg_u4 *)(a.norm_w + kk), *(const rg_u4 *)(a.norm_w + kk + 4u),
+                                 scale);
+        unsigned int h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            unsigned int kc = kk + (unsigned int)e;
+            h[e] = kc < a.k ? aotx_f2h(scale * co_loadf<CH>(rrow + kc) * a.norm_w[kc]) : 0u;
+        }
+        return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    if (kk + 8u <= a.k) return co_load4<CH>(a.x + (unsigned long long)src * a.ldx + kk);
+    unsigned int h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        h[e] = kk + (unsigned int)e < a.k ? a.x[(unsigned long long)src * a.ldx + kk + e] : 0u;
+    return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
+/* Split partials cross workgroups on different XCDs: device-scope stores and loads (past
+ * the per-XCD L2, so no cache write-back or invalidation is needed). */
+static __device__ __forceinline__ void rg_put(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+static __device__ __forceinline__ float rg_get(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* k split over workgroups: publish this split's sums out[0, n); the last split of the
+ * product group to arrive adds all splits in split order (its own from LDS) into out and
+ * returns true; the others return false. All of this workgroup's stores have completed
+ * before its arrival is counted; the last arrival puts the counter back to zero. `last` is
+ * one word of LDS. */
+template <int NT>
+static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, float *out,
+                                                      unsigned int n, unsigned int expert,
+                                                      unsigned int group, unsigned int split,
+                                                      unsigned int *last)
+{
+    const unsigned int tid = threadIdx.x;
+    const unsigned long long tile = (unsigned long long)expert * a.groups + group;
+    float *base = a.partial + tile * a.splits * n;
+    for (unsigned int idx = tid; idx < n; idx += NT) rg_put(base + (unsigned long long)split * n + idx, out[idx]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0u) {
+        const unsigned int arrived = atomicAdd(a.count + tile, 1u);
+        *last = arrived == a.splits - 1u ? 1u : 0u;
+        if (*last != 0u) atomicExch(a.count + tile, 0u);
+    }
+    __syncthreads();
+    if (*last == 0u) return false;
+    for (unsigned int idx = tid; idx < n; idx += NT) {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (unsigned int sp = 0; sp < a.splits; ++sp)
+            sum += sp == split ? out[idx] : rg_get(base + (unsigned long long)sp * n + idx);
+        out[idx] = sum;
+    }
+    __syncthreads();
+    return true;
+}
+
+/* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
+ * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
+ * few tiles, so that each wave's share of the dequantisation is short). */
+template <int MT, int RT, int PD, int NW, bool CH, class Wait>
+static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsigned int bx,
+                                                 unsigned int expert, unsigned char *lds,
+                                                 Wait &wait)
+{
+    constexpr unsigned int NT = 64u * NW;
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
+    const unsigned int *list = nullptr;
+    unsigned int mrows = a.m;
+    if (a.expert_stride != 0ull) {
+        /* an expert no row chose streams nothing */
+        unsigned int total = rg_scalar(a.list_count + expert);
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+        list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
+        if (mrows == 0u) return;
+    }
+
+    const unsigned int group = bx / a.splits;
+    const unsigned int split = bx % a.splits;
+    const unsigned int q0 = split * a.qps;
+    const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
+    const unsigned int kr = a.qps * 128u;          /* LDS k capacity */
+    const unsigned int xs = kr + 8u;               /* LDS x row stride (halves) */
+    unsigned short *xl = (unsigned short *)lds;
+    __shared__ unsigned int xsrc[MT];              /* source row of each batch row */
+    __shared__ float xscale[MT];                   /* its RMSNorm scale (AOTX_X_NORM) */
+
+    /* ---- per-wave share of the k range ---- */
+    const unsigned int nq = q1 - q0;
+    const unsigned int per = (nq + NW - 1u) / NW;
+    const unsigned int wq0 = q0 + wave * per < q1 ? q0 + wave * per : q1;
+    const unsigned int wq1 = wq0 + per < q1 ? wq0 + per : q1;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+
+    const unsigned char *qb[RT];
+    const unsigned short *sb[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        unsigned int dummy = 0u;
+        qb[j] = rg_tile(a, group, (unsigned int)j, RT, expert, dummy) + lane * 16u;
+        sb[j] = rg_scales(a, group, (unsigned int)j, RT, expert) + lane;
+    }
+
+    rg_f4 acc[RT][MT / 16];
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    rg_u4 wa[2][PD][RT][2];
+    unsigned int ws[2][PD][RT];    /* one 32-bit register per scale: no packing waits */
+
+    /* loads past the wave's range repeat its last quad (a cache hit), so every load can be
+     * issued unconditionally: no register copies that would wait for them */
+    const unsigned int qlast = wq0 < wq1 ? wq1 - 1u : q0;
+#define RG_LOAD(BUF, QS)                                                                 \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = (QS) + (unsigned int)qi;                                   \
+            if (qq > qlast) qq = qlast;                                                  \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
+                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
+                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+    /* Branch-free: a quad past the wave's range reads the last quad's x and has its scale
+     * forced to zero (it adds nothing); a batch column past mrows reads row 0 of x (its
+     * results are never written). */
+#define RG_COMPUTE(BUF, QS)                                                              \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            const unsigned int qq = (QS) + (unsigned int)qi;                             \
+            const unsigned int qx = qq > qlast ? qlast : qq;                             \
+            const unsigned short *xq = xl + (qx - q0) * 128u + 32u * g;                  \
+            rg_h8 B[MT / 16][4];                                                         \
+            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
+                const unsigned int mm = (unsigned int)t * 16u + r;                       \
+                const unsigned int mr = mm < mrows ? mm : 0u;                            \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
+                    B[t][s] = *(const rg_h8 *)(xq + mr * xs + 8u * s);                   \
+            }                                                                            \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const unsigned int sbits = qq < wq1 ? ws[BUF][qi][j] : 0u;               \
+                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
+                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
+                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
+                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
+                    unsigned int d0, d1, d2, d3;                                         \
+                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
+                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
+                    rg_u4 av = {d0, d1, d2, d3};                                         \
+                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
+                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
+                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
+                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
+                }                                                                        \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+
+    /* ---- loads that do not depend on the weights go out first. With direct rows (batch
+     * row i is row m0 + i: no expert list, no row map) that is the first RG_PRE staging
+     * rounds of x (or of the residual and norm weights, plus the sums of squares, for the
+     * fused norm) and the residual values the epilogue adds to, for every row the pass
+     * may hold. vmcnt counts in issue order, so these must precede the weight stream to
+     * be waited for without it. ---- */
+    constexpr int RG_PRE = 2;
+    const bool direct = list == nullptr && a.xrow == nullptr;
+    /* in a chain (CH) x is the product of an earlier stage of the same launch: it is
+     * loaded before the weights only once this workgroup has seen that stage complete */
+    const bool early = direct && (!CH || wait.seen);
+    const bool norm = a.xmode == AOTX_X_NORM;
+    const bool resid_pre = early && a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
+    const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
+    const unsigned int kbeg = q0 * 128u;
+    const unsigned int pieces = (q1 - q0) * 16u;       /* 16-byte pieces (8 values) per row */
+    const unsigned int nss = (a.k + 15u) / 16u;
+    __shared__ float rres[RT * 16 * MT];               /* the epilogue's residual values */
+    rg_u4 pre[RG_PRE][4];
+    float ssp[16];
+    float rold[(RT * 16 * MT + 64 * NW - 1) / (64 * NW)];
+    if (early) {
+#pragma unroll
+        for (int i = 0; i < RG_PRE; ++i) {
+            const unsigned int idx = tid + (unsigned int)i * NT;
+            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            const unsigned int kk = kbeg + p * 8u;
+            pre[i][0] = pre[i][1] = pre[i][2] = pre[i][3] = (rg_u4){0u, 0u, 0u, 0u};
+            if (mm < cap && kk + 8u <= a.k) {
+                if (norm) {
+                    const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
+                    pre[i][0] = co_load4<CH>(rrow);
+                    pre[i][1] = co_load4<CH>(rrow + 4);
+                    pre[i][2] = *(const rg_u4 *)(a.norm_w + kk);
+                    pre[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
+                } else {
+                    pre[i][0] = co_load4<CH>(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
+                }
+            }
+        }
+        if (norm) {
+            const unsigned int mm = tid >> 4, l = tid & 15u;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const unsigned int at = l + 16u * (unsigned int)i;
+                ssp[i] = mm < cap && at < nss ? co_loadf<CH>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
+            }
+        }
+    }
+    constexpr unsigned int RPT = (RT * 16u * MT + NT - 1u) / NT;   /* residual values per thread */
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % RT, mm = rest / RT;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
+            rold[it] = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n
+                ? co_loadf<CH>((const float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr) : 0.0f;
+        }
+    }
+
+    /* with one tile per workgroup only the first buffer goes out before the staging, so
+     * every workgroup's x requests queue behind less of the grid's weight stream (measured
+     * faster for every one-tile shape; a gate/up pair keeps both buffers ahead) */
+    /* (a chain item that still has to wait issues both, so that they load while it waits) */
+    const bool both_first = RT > 1 || (CH && !early);
+    RG_LOAD(0, wq0);
+    if (both_first) RG_LOAD(1, wq0 + PD);
+    if (a.expert_stride == 0ull && a.m_dev != nullptr) {
+        unsigned int total = rg_scalar(a.m_dev);
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+    if (mrows == 0u) return;
+    if (!early) wait();
+
+    /* ---- stage the batch rows of x for [q0, q1) ---- */
+    {
+        /* sources, and norm scales (16 threads per row add its partial sums of squares) */
+        {
+            const unsigned int mm = tid >> 4, l = tid & 15u;
+            unsigned int src = a.m0 + mm;
+            if (!direct && mm < mrows)
+                src = list != nullptr ? list[mm] / a.xrow_div : a.xrow[a.m0 + mm];
+            if (l == 0u && mm < mrows) xsrc[mm] = src;
+            if (norm) {
+                float sum = 0.0f;
+                if (early) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) sum += ssp[i];
+                    if (mm < mrows)
+                        for (unsigned int i = l + 256u; i < nss; i += 16u)
+                            sum += co_loadf<CH>(a.sumsq + (unsigned long long)src * nss + i);
+                } else if (mm < mrows) {
+                    const float *ss = a.sumsq + (unsigned long long)src * nss;
+#pragma unroll 4
+                    for (unsigned int i = l; i < nss; i += 16u) sum += co_loadf<CH>(ss + i);
+                }
+                sum += __shfl_xor(sum, 1, 64);
+                sum += __shfl_xor(sum, 2, 64);
+                sum += __shfl_xor(sum, 4, 64);
+                sum += __shfl_xor(sum, 8, 64);
+                if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
+            }
+        }
+        if (resid_pre) {
+#pragma unroll
+            for (int it = 0; it < (int)RPT; ++it) {
+                const unsigned int idx = tid + (unsigned int)it * NT;
+                const unsigned int rr = idx & 15u, rest = idx >> 4;
+                if (idx < RT * 16u * MT) rres[((rest % RT) * 16u + rr) * MT + rest / RT] = rold[it];
+            }
+        }
+        rg_sync_lds();
+        const unsigned int total = mrows * pieces;
+#pragma unroll
+        for (int i = 0; i < RG_PRE; ++i) {
+            const unsigned int idx = tid + (unsigned int)i * NT;
+            if (idx < total) {
+                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                const unsigned int kk = kbeg + p * 8u;
+                rg_u4 v;
+                if (early && kk + 8u <= a.k)
+                    v = norm ? rg_norm_piece(pre[i][0], pre[i][1], pre[i][2], pre[i][3], xscale[mm])
+                             : pre[i][0];
+                else
+                    v = rg_x_piece<CH>(a, xsrc[mm], kk, norm ? xscale[mm] : 0.0f);
+                *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+            }
+        }
+        for (unsigned int idx = tid + RG_PRE * NT; idx < total; idx += NT) {
+            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            *(rg_u4 *)(xl + mm * xs + p * 8u) = rg_x_piece<CH>(a, xsrc[mm], kbeg + p * 8u,
+                                                              norm ? xscale[mm] : 0.0f);
+        }
+        rg_sync_lds();
+    }
+
+    /* each buffer is refilled right after its quads are computed, two steps ahead */
+    if (!both_first) RG_LOAD(1, wq0 + PD);
+    if (wq0 < wq1) {
+        unsigned int q = wq0;
+        for (;;) {
+            RG_COMPUTE(0, q);
+            q += PD;
+            if (q >= wq1) break;
+            RG_LOAD(0, q + PD);
+            RG_COMPUTE(1, q);
+            q += PD;
+            if (q >= wq1) break;
+            RG_LOAD(1, q + PD);
+        }
+    }
+#undef RG_LOAD
+#undef RG_COMPUTE
+
+    /* ---- add the NW waves' accumulators in wave order ---- */
+    __syncthreads();
+    float *part = (float *)lds;                      /* [NW][RT*16][MT] */
+    const unsigned int gr = RT * 16u;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < MT / 16; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                unsigned int row = (unsigned int)j * 16u + 4u * g + (unsigned int)i;
+                part[(wave * gr + row) * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
+            }
+    __syncthreads();
+    float *out = part + NW * gr * MT;
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
+        float sum = part[idx];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * gr * MT + idx];
+        out[idx] = sum;
+    }
+    __syncthreads();
+    if (a.splits > 1u) {
+        __shared__ unsigned int last;
+        if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
+    }
+    rg_epilogue<MT, NT, CH>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
+}
+
+
+/* Bytes of the staged x rows of a chain stage (the front of its dynamic LDS; the wave
+ * reduction area follows). */
+static __host__ __device__ __forceinline__ unsigned int rg_chain_xbytes(const aotx_rgemv_args &a)
+{
+    return (a.m * (a.qps * 128u + 8u) * 2u + 15u) / 16u * 16u;
+}
+
+/* One workgroup's share of a product stage of the layer chain: items it0, it0 + step, ...
+ * below `items` (item = group * splits + split, as for rg_narrow; direct batch rows,
+ * operands written by earlier stages of the same launch). Each wave's weight loads form
+ * one stream over all of its items, two chunks of PD quads ahead of the MFMAs, so the
+ * loads of the next item are in flight while this one is reduced and written; the staged
+ * x stays in LDS for every item of the same k range. The first item's loads are issued
+ * before the wait for the stage's inputs. Returns the number of items done. */
+template <int MT, int RT, int PD, int NW, class Wait>
+static __device__ __forceinline__ unsigned int rg_chain_stage(const aotx_rgemv_args &a,
+                                                              unsigned int it0, unsigned int step,
+                                                              unsigned int items,
+                                                              unsigned char *lds, Wait &wait)
+{
+    constexpr unsigned int NT = 64u * NW;
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+    if (it0 >= items) return 0u;
+    const unsigned int nitems = (items - it0 + step - 1u) / step;
+
+    unsigned int mrows = a.m;
+    if (a.m_dev != nullptr) {
+        const unsigned int total = rg_scalar(a.m_dev);
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > a.m) mrows = a.m;
+    if (mrows > (unsigned int)MT) mrows = MT;
+
+    const unsigned int xs = a.qps * 128u + 8u;     /* LDS x row stride (halves) */
+    unsigned short *xl = (unsigned short *)lds;
+    float *part = (float *)(lds + rg_chain_xbytes(a));   /* [NW][RT*16][MT] then out */
+    __shared__ float xscale[MT];
+    const bool norm = a.xmode == AOTX_X_NORM;
+
+    /* ---- the load stream: item lk, chunk lc ---- */
+    unsigned int lk = 0u, lc = 0u, lchunks = 0u, lq0 = 0u, llast = 0u;
+    const unsigned char *lqb[RT];
+    const unsigned short *lsb[RT];
+#define RGC_RANGE(K, WQ0, WQ1, Q0)                                                       \
+    do {                                                                                 \
+        const unsigned int it_ = it0 + (K) * step;                                       \
+        const unsigned int sp_ = it_ % a.splits;                                         \
+        (Q0) = sp_ * a.qps;                                                              \
+        const unsigned int q1_ = (Q0) + a.qps < a.qn ? (Q0) + a.qps : a.qn;              \
+        const unsigned int per_ = (q1_ - (Q0) + NW - 1u) / NW;                           \
+        (WQ0) = (Q0) + wave * per_ < q1_ ? (Q0) + wave * per_ : q1_;                     \
+        (WQ1) = (WQ0) + per_ < q1_ ? (WQ0) + per_ : q1_;                                 \
+    } while (0)
+    /* move the stream to the first item at or after lk in which this wave has quads */
+#define RGC_SEEK()                                                                       \
+    do {                                                                                 \
+        for (; lk < nitems; ++lk) {                                                      \
+            unsigned int w0_, w1_, q0_;                                                  \
+            RGC_RANGE(lk, w0_, w1_, q0_);                                                \
+            lchunks = ((w1_ - w0_ + PD - 1u) / PD + 1u) & ~1u;   /* even: see below */   \
+            if (lchunks == 0u) continue;                                                 \
+            lq0 = w0_;                                                                   \
+            llast = w1_ - 1u;                                                            \
+            const unsigned int grp_ = (it0 + lk * step) / a.splits;                      \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                unsigned int dummy_ = 0u;                                                \
+                lqb[j] = rg_tile(a, grp_, (unsigned int)j, RT, 0u, dummy_) + lane * 16u; \
+                lsb[j] = rg_scales(a, grp_, (unsigned int)j, RT, 0u) + lane;             \
+            }                                                                            \
+            break;                                                                       \
+        }                                                                                \
+    } while (0)
+
+    rg_u4 wa[2][PD][RT][2];
+    unsigned int ws[2][PD][RT];
+    /* Every call issues the same loads: past the end of the stream it repeats the last
+     * chunk (a cache hit, never computed). A load issued on one path only would make the
+     * compiler wait for all outstanding loads (vmcnt(0)) where the paths join, so each
+     * chunk would wait for the one issued after it. */
+#define RGC_LOAD(BUF)                                                                    \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            unsigned int qq = lq0 + lc * PD + (unsigned int)qi;                          \
+            if (qq > llast) qq = llast;                                                  \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const rg_u4 *src = (const rg_u4 *)(lqb[j] + (unsigned long long)qq * 2048ull); \
+                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
+                ws[BUF][qi][j] = lsb[j][(unsigned long long)qq * 64ull];                 \
+            }                                                                            \
+        }                                                                                \
+        if (lk < nitems && ++lc >= lchunks) {                                            \
+            lc = 0u;                                                                     \
+            ++lk;                                                                        \
+            RGC_SEEK();                                                                  \
+            if (lk >= nitems) lc = 0u;   /* repeat a chunk already read */               \
+        }                                                                                \
+    } while (0)
+
+    /* the stream starts on the first item (also for a wave with no quads in any item, so
+     * that its repeated loads read valid weights) */
+    {
+        unsigned int w0_, w1_, q0_;
+        RGC_RANGE(0u, w0_, w1_, q0_);
+        lq0 = q0_;
+        llast = q0_;
+        lchunks = 1u;
+        const unsigned int grp_ = it0 / a.splits;
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+            unsigned int dummy_ = 0u;
+            lqb[j] = rg_tile(a, grp_, (unsigned int)j, RT, 0u, dummy_) + lane * 16u;
+            lsb[j] = rg_scales(a, grp_, (unsigned int)j, RT, 0u) + lane;
+        }
+    }
+    RGC_SEEK();
+    if (lk >= nitems) lc = 0u;
+    RGC_LOAD(0);
+    RGC_LOAD(1);
+    wait();
+
+    unsigned int staged = 0xffffffffu;   /* the split whose x rows are in LDS */
+    for (unsigned int k = 0; k < nitems; ++k) {
+        const unsigned int it = it0 + k * step;
+        const unsigned int group = it / a.splits, split = it % a.splits;
+        unsigned int wq0, wq1, q0;
+        RGC_RANGE(k, wq0, wq1, q0);
+        const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
+
+        /* ---- stage the batch rows of x for [q0, q1) when the k range changes ---- */
+        if (split != staged) {
+            /* one round trip: the first pieces of x (or of the residual rows and norm
+             * weights) and the rows' partial sums of squares are all loaded before any is
+             * used */
+            staged = split;
+            const unsigned int pieces = (q1 - q0) * 16u;
+            const unsigned int total = mrows * pieces;
+            const unsigned int nss = (a.k + 15u) / 16u;
+            rg_u4 pr[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const unsigned int idx = tid + (unsigned int)i * NT;
+                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                const unsigned int kk = q0 * 128u + p * 8u;
+                pr[i][0] = pr[i][1] = pr[i][2] = pr[i][3] = (rg_u4){0u, 0u, 0u, 0u};
+                if (idx < total && kk + 8u <= a.k) {
+                    if (norm) {
+                        const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
+                        pr[i][0] = co_load4<true>(rrow);
+                        pr[i][1] = co_load4<true>(rrow + 4);
+                        pr[i][2] = *(const rg_u4 *)(a.norm_w + kk);
+                        pr[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
+                    } else {
+                        pr[i][0] = co_load4<true>(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
+                    }
+                }
+            }
+            if (norm) {
+                const unsigned int mm = tid >> 4, l = tid & 15u;
+                float ssp[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const unsigned int at = l + 16u * (unsigned int)i;
+                    ssp[i] = mm < mrows && at < nss
+                           ? co_loadf<true>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sum += ssp[i];
+                if (mm < mrows)
+                    for (unsigned int i = l + 256u; i < nss; i += 16u)
+                        sum += co_loadf<true>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + i);
+                sum += __shfl_xor(sum, 1, 64);
+                sum += __shfl_xor(sum, 2, 64);
+                sum += __shfl_xor(sum, 4, 64);
+                sum += __shfl_xor(sum, 8, 64);
+                if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
+                rg_sync_lds();
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const unsigned int idx = tid + (unsigned int)i * NT;
+                if (idx < total) {
+                    const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                    const unsigned int kk = q0 * 128u + p * 8u;
+                    rg_u4 v;
+                    if (kk + 8u <= a.k)
+                        v = norm ? rg_norm_piece(pr[i][0], pr[i][1], pr[i][2], pr[i][3], xscale[mm])
+                                 : pr[i][0];
+                    else
+                        v = rg_x_piece<true>(a, a.m0 + mm, kk, norm ? xscale[mm] : 0.0f);
+                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
+                }
+            }
+            for (unsigned int idx = tid + 2u * NT; idx < total; idx += NT) {
+                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
+                *(rg_u4 *)(xl + mm * xs + p * 8u) =
+                    rg_x_piece<true>(a, a.m0 + mm, q0 * 128u + p * 8u, norm ? xscale[mm] : 0.0f);
+            }
+            rg_sync_lds();
+        }
+
+        rg_f4 acc[RT][MT / 16];
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+#pragma unroll
+            for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+        const unsigned int qlast = wq0 < wq1 ? wq1 - 1u : q0;
+        /* an even number of chunks per item (an odd count takes one chunk of zero scales),
+         * so every item starts on buffer 0: with the buffer order fixed in the code the
+         * compiler's wait before each chunk covers that chunk's loads only */
+        const unsigned int chunks = ((wq1 - wq0 + PD - 1u) / PD + 1u) & ~1u;
+#define RGC_COMPUTE(BUF, QS)                                                             \
+    do {                                                                                 \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
+            const unsigned int qq = (QS) + (unsigned int)qi;                             \
+            const unsigned int qx = qq > qlast ? qlast : qq;                             \
+            const unsigned short *xq = xl + (qx - q0) * 128u + 32u * g;                  \
+            rg_h8 B[MT / 16][4];                                                         \
+            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
+                const unsigned int mm = (unsigned int)t * 16u + r;                       \
+                const unsigned int mr = mm < mrows ? mm : 0u;                            \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
+                    B[t][s] = *(const rg_h8 *)(xq + mr * xs + 8u * s);                   \
+            }                                                                            \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
+                const unsigned int sbits = qq < wq1 ? ws[BUF][qi][j] : 0u;               \
+                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
+                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
+                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
+                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
+                    unsigned int d0, d1, d2, d3;                                         \
+                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
+                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
+                    rg_u4 av = {d0, d1, d2, d3};                                         \
+                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
+                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
+                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
+                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
+                }                                                                        \
+            }                                                                            \
+        }                                                                                \
+    } while (0)
+        /* each buffer is refilled from the stream right after it is used */
+        for (unsigned int c = 0; c < chunks; c += 2u) {
+            RGC_COMPUTE(0, wq0 + c * PD);
+            RGC_LOAD(0);
+            RGC_COMPUTE(1, wq0 + (c + 1u) * PD);
+            RGC_LOAD(1);
+        }
+#undef RGC_COMPUTE
+
+        /* ---- add the NW waves' accumulators in wave order ---- */
+        const unsigned int gr = RT * 16u;
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+#pragma unroll
+            for (int t = 0; t < MT / 16; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    unsigned int row = (unsigned int)j * 16u + 4u * g + (unsigned int)i;
+                    part[(wave * gr + row) * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
+                }
+        rg_sync_lds();
+        float *out = part + NW * gr * MT;
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
+            float sum = part[idx];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * gr * MT + idx];
+            out[idx] = sum;
+        }
+        rg_sync_lds();
+        bool mine = true;
+        if (a.splits > 1u) {
+            __shared__ unsigned int last;
+            mine = rg_split_merge<NT>(a, out, gr * MT, 0u, group, split, &last);
+        }
+        if (mine) rg_epilogue<MT, NT, true>(a, out, group, RT, mrows, nullptr, nullptr);
+        __syncthreads();          /* out and part are rewritten by the next item */
+    }
+#undef RGC_RANGE
+#undef RGC_SEEK
+#undef RGC_LOAD
+    return nitems;
+}
+
+#endif
