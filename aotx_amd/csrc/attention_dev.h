@@ -212,16 +212,21 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         }                                                                                   \
     } while (0)
 
+    /* The next block's loads are issued on every step: past the wave's last block the page
+     * address is zero and the loads go through a zero-size resource (they return zeros
+     * and touch no memory; that buffer is never computed). With a load on one path only,
+     * the compiler's wait before a block's MFMAs would also cover part of the next block's
+     * loads. */
     if (b0 < b1) {
         unsigned int b = b0;
         MMA_WINDOW(b0);
         MMA_LOAD(0, b);
         for (;;) {
-            if (b + 1u < b1) MMA_LOAD(1, b + 1u);
+            MMA_LOAD(1, b + 1u);
             MMA_COMPUTE(0, b);
             b += 1u;
             if (b >= b1) break;
-            if (b + 1u < b1) MMA_LOAD(0, b + 1u);
+            MMA_LOAD(0, b + 1u);
             MMA_COMPUTE(1, b);
             b += 1u;
             if (b >= b1) break;
