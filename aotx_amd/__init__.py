@@ -122,6 +122,30 @@ class KvTable(ctypes.Structure):
 
 
 # name -> (restype, argtypes). Every symbol declared in include/aotx_hip.h.
+AOTX_TENSOR_NAME_BYTES = 128
+AOTX_TENSOR_DIMS = 4
+AOTX_DESC_WHOLE = 5
+AOTX_DESC_BUFFER = 48
+AOTX_DESC_MAX_BINDINGS = AOTX_DESC_WHOLE + AOTX_MODEL_MAX_LAYERS * AOTX_LAYER_TENSOR_SLOTS
+
+
+class TensorInfo(ctypes.Structure):
+    """include/aotx_modelfile.h aotx_tensor_info (modelfile.h:97-104)."""
+    _fields_ = [("name", ctypes.c_char * AOTX_TENSOR_NAME_BYTES), ("dim_count", u32),
+                ("type", u32), ("dims", u64 * AOTX_TENSOR_DIMS), ("offset", u64),
+                ("bytes", u64)]
+
+
+class StringArray(ctypes.Structure):
+    _fields_ = [("count", u64), ("bytes", ctypes.POINTER(ctypes.c_uint8)),
+                ("offsets", ctypes.POINTER(u64))]
+
+
+class ModelBinding(ctypes.Structure):
+    """include/aotx_modelfile.h aotx_model_binding (forward.cuh:290-294)."""
+    _fields_ = [("name", ctypes.c_char * AOTX_DESC_BUFFER), ("slot", u32), ("needed", u32)]
+
+
 PROTOTYPES = {
     "aotx_mem_weights_set": (i32, [u64, u64]),
     "aotx_mem_weights_base": (u64, []),
@@ -167,6 +191,33 @@ PROTOTYPES = {
     "aotx_synth_f16": (i32, [vp, u64, f32, u64, vp]),
     "aotx_synth_f16_host": (i32, [vp, u64, f32, u64, u32]),
     "aotx_version": (ctypes.c_char_p, []),
+    # GGUF model files (include/aotx_modelfile.h)
+    "aotx_modelfile_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+    "aotx_modelfile_close": (None, [vp]),
+    "aotx_modelfile_file_bytes": (u64, [vp]),
+    "aotx_modelfile_header_bytes": (u64, [vp]),
+    "aotx_modelfile_u32": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(u32)]),
+    "aotx_modelfile_u64": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(u64)]),
+    "aotx_modelfile_f32": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(f32)]),
+    "aotx_modelfile_string": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                    ctypes.POINTER(ctypes.c_size_t)]),
+    "aotx_modelfile_strings": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(StringArray)]),
+    "aotx_modelfile_i32s": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                  ctypes.POINTER(u64)]),
+    "aotx_modelfile_f32s": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                  ctypes.POINTER(u64)]),
+    "aotx_modelfile_bools": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p),
+                                   ctypes.POINTER(u64)]),
+    "aotx_modelfile_tensor_count": (u64, [vp]),
+    "aotx_modelfile_tensor": (i32, [vp, u64, ctypes.POINTER(TensorInfo)]),
+    "aotx_modelfile_find": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
+    "aotx_modelfile_data_bytes": (u64, [vp]),
+    "aotx_modelfile_read": (i32, [vp, u64, u64, vp]),
+    "aotx_model_desc_file": (i32, [vp, u32, ctypes.POINTER(ModelDesc), ctypes.POINTER(ModelBinding),
+                                   u32, ctypes.POINTER(u32), ctypes.c_char_p, ctypes.c_size_t]),
+    "aotx_model_place_bytes": (u64, [vp, ctypes.POINTER(ModelBinding), u32]),
+    "aotx_model_place": (i32, [vp, ctypes.POINTER(ModelDesc), ctypes.POINTER(ModelBinding), u32,
+                               ctypes.c_char_p, ctypes.c_size_t]),
 }
 
 _lib = None

@@ -22,13 +22,18 @@ FLAGS = [
 ]
 
 
+# host-only C++ (the model-file reader)
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
+
+
 def _sources():
-    return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(f for f in os.listdir(CSRC) if f.endswith(".hip") or f.endswith(".cpp"))
 
 
 def _compile(src):
-    obj = os.path.join(OUT_DIR, src.replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+    obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
+    flags = FLAGS if src.endswith(".hip") else HOST_FLAGS
+    cmd = [HIPCC] + flags + ["-c", os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(line for line in proc.stderr.splitlines()
                     if "packed-fp32-ops" not in line)

@@ -316,3 +316,34 @@ def test_8b_width_layer_chain_vs_oracle(torch, orc, monkeypatch):
         assert rt.faulted() == 0
     finally:
         rt.close()
+
+
+def test_gguf_file_through_place_and_step(torch, orc, tiny, tmp_path):
+    """The tiny model written as a GGUF file, read back by the library's reader, placed into
+    a new weights region (aotx_model_place) and run: the same logits, bit for bit, as the
+    region built directly (the same bytes through the same kernels), and within 1e-2 of the
+    oracle; a second slot decodes after it."""
+    from aotx_amd import gguf
+    region, lay = tiny
+    path = tmp_path / "tiny.gguf"
+    gguf.export(TINY, region, lay, path)
+    ids = list(range(30, 44))
+    direct = _runtime(torch, region, lay)
+    try:
+        _, _, want_dev = direct.step(ids, [0, 14], [5])
+        _, _, want_dev2 = direct.step([7], [0, 1], [5])
+    finally:
+        direct.close()
+    region_f, desc = gguf.load(path)
+    assert desc.token_embd != aotx_amd.AOTX_MODEL_ABSENT and desc.tied_output == 0
+    rt = Runtime(region_f, desc, max_tokens=32, pool_pages=64)
+    try:
+        _, _, got = rt.step(ids, [0, 14], [5])
+        _, _, got2 = rt.step([7], [0, 1], [5])
+        assert np.array_equal(got, want_dev) and np.array_equal(got2, want_dev2)
+        ref = orc.Model(lay.desc, region, slots=8, max_context=64)
+        assert rel_rms(got, ref.step(ids, [0, 14], [5])) < 1e-2
+        assert rel_rms(got2, ref.step([7], [0, 1], [5])) < 1e-2
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
