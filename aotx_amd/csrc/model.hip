@@ -207,8 +207,18 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
                           unsigned int nseg, unsigned int k, int epi, unsigned int cap,
                           const unsigned int *m_dev, const aotx_rgemv_args &tmpl)
 {
-    for (unsigned int m0 = 0; m0 < cap; m0 += 32u) {
-        unsigned int mt = cap - m0 < 32u ? cap - m0 : 32u;
+    /* 256 rows or more of a dense product: one GEMM pass (up to 512 rows; below 256 rows
+     * its few workgroups are slower than re-reading the weights per 32 rows); routed
+     * experts keep passes of 32 rows through their row lists */
+    static const bool gemm_on = [] {
+        const char *v = getenv("AOTX_GEMM");       /* 0: 32-row passes, for comparison */
+        return !(v != nullptr && v[0] == '0');
+    }();
+    const bool gemm = gemm_on && cap >= 256u && tmpl.expert_stride == 0ull && tmpl.list == nullptr
+                   && tmpl.xrow == nullptr && tmpl.xmode == AOTX_X_F16;
+    for (unsigned int m0 = 0, mt = 0; m0 < cap; m0 += mt) {
+        mt = gemm ? (cap - m0 < AOTX_RGEMM_ROWS ? cap - m0 : AOTX_RGEMM_ROWS)
+                  : (cap - m0 < 32u ? cap - m0 : 32u);
         aotx_rgemv_args a;
         if (aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt) != 0) {
             fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);

@@ -46,6 +46,7 @@ struct aotx_rgemv_args {
     unsigned int qn;              /* quads of k */
     unsigned int rt;              /* 16-row tiles per workgroup */
     unsigned int wide;            /* 1: the tile-split wide-batch kernel (fp16 x only) */
+    unsigned int gemm;            /* 1: the GEMM of 33..512 rows (fp16 x, direct rows) */
     unsigned int pd;              /* quads loaded ahead per wave (narrow kernel) */
     unsigned int nw;              /* waves per workgroup (narrow kernel: 4 or 8) */
     unsigned int groups;          /* workgroups along n */
@@ -86,7 +87,10 @@ struct aotx_rgemv_args {
     unsigned int experts;
 };
 
-/* Plan a product over Q8R tensors; rows per segment; returns 1 when refused. */
+/* Plan a product over Q8R tensors; rows per segment; returns 1 when refused. mt is the
+ * pass capacity: up to 16 rows take the streaming kernel, up to 32 the wide kernel, and
+ * up to AOTX_RGEMM_ROWS the GEMM. */
+#define AOTX_RGEMM_ROWS 512u
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                     unsigned int nseg, unsigned int k, int epi, unsigned int mt);
 /* Plan a product as a stage of the layer chain (chain.hip): one 16-row tile per item (a

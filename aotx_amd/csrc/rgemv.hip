@@ -269,6 +269,169 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
 }
 
+/* Many batch rows (prefill: 256..512 per pass): a GEMM. A workgroup takes 128 weight rows
+ * (8 tiles) by MB batch rows; its 8 waves are 2 (weight rows) x 4 (batch rows), each holding
+ * 4 tiles x MB/64 column blocks of accumulators, so each dequantised A fragment feeds MB/64
+ * MFMAs and each B fragment read from LDS feeds 4 tiles (dequantisation and x staging are
+ * VALU work that otherwise outweighs the MFMAs). Per 128-k quad: the next quad's x rows go
+ * to LDS through registers (requested before this quad's MFMAs, stored after them), and the
+ * weights are requested two quads ahead and dequantised in registers into the A operand,
+ * as in the streaming product. The results pass through LDS to the same epilogues. */
+#define RGM_MB 192
+template <int MB>
+__global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
+{
+    constexpr int RT = 8;                         /* weight tiles per workgroup */
+    constexpr int CB = MB / 64;                   /* column blocks per wave */
+    constexpr int NT = 512;
+    constexpr int XS = 128 + 8;                   /* LDS x row stride (halves) */
+    constexpr int PIECES = 16;                    /* 16-byte pieces of a row per quad */
+    constexpr int PPT = MB * PIECES / NT;         /* pieces per thread */
+    static_assert(MB * PIECES % NT == 0 && MB % 64 == 0, "whole pieces and blocks");
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
+    const unsigned int wn = wave & 1u, wm = wave >> 1;   /* 2 x 4 waves */
+    const unsigned int r = lane & 15u, g = lane >> 4;
+    const unsigned int group = blockIdx.x;
+
+    aotx_rgemv_args a = a0;
+    a.m0 = a0.m0 + blockIdx.y * (unsigned int)MB;
+    unsigned int total = a0.m;
+    if (a0.m_dev != nullptr) {
+        const unsigned int live = rg_scalar(a0.m_dev);
+        total = live < total ? live : total;
+    }
+    if (a.m0 >= total) return;
+    const unsigned int mrows = total - a.m0 < (unsigned int)MB ? total - a.m0 : (unsigned int)MB;
+
+    unsigned short *xl = (unsigned short *)lds;         /* [2][MB][XS] */
+    const unsigned char *qb[4];
+    const unsigned short *sb[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        unsigned int dummy = 0u;
+        qb[t] = rg_tile(a, group, wn * 4u + (unsigned int)t, RT, 0u, dummy) + lane * 16u;
+        sb[t] = rg_scales(a, group, wn * 4u + (unsigned int)t, RT, 0u) + lane;
+    }
+    rg_f4 acc[4][CB];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < CB; ++c) acc[t][c] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    /* a thread's x pieces keep their row and place from quad to quad: the row's address
+     * (a valid row for rows past mrows, whose pieces are stored as zeros) and the LDS
+     * offset are computed once */
+    /* piece i of a thread is row tid / 16 + 32 i, place tid % 16 */
+    constexpr unsigned int RSTEP = NT / PIECES;
+    const unsigned int xrow0 = tid / PIECES, xpc = tid % PIECES;
+    unsigned int xoff[PPT];                       /* element offsets from a.x */
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+        const unsigned int mm = xrow0 + (unsigned int)i * RSTEP;
+        xoff[i] = (a.m0 + (mm < mrows ? mm : 0u)) * a.ldx + xpc * 8u;
+    }
+
+    rg_u4 wa[2][4][2];
+    unsigned int ws[2][4];
+    const unsigned int qn = a.qn;
+    /* every call issues the same loads (a quad past k repeats the last: never computed) */
+#define RGM_WLOAD(BUF, Q)                                                                \
+    do {                                                                                 \
+        const unsigned int qq_ = (Q) < qn ? (Q) : qn - 1u;                               \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                  \
+            const rg_u4 *src = (const rg_u4 *)(qb[t] + (unsigned long long)qq_ * 2048ull); \
+            wa[BUF][t][0] = __builtin_nontemporal_load(src);                            \
+            wa[BUF][t][1] = __builtin_nontemporal_load(src + 64);                        \
+            ws[BUF][t] = sb[t][(unsigned long long)qq_ * 64ull];                         \
+        }                                                                                \
+    } while (0)
+    /* x pieces of quad Q (k is a whole number of quads: a quad past k repeats the last) */
+    rg_u4 xr[PPT];
+#define RGM_XLOAD(Q)                                                                     \
+    do {                                                                                 \
+        const unsigned int qx_ = ((Q) < qn ? (Q) : qn - 1u) * 128u;                      \
+        _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
+            xr[i] = *(const rg_u4 *)(a.x + xoff[i] + qx_);                               \
+    } while (0)
+#define RGM_XSTORE(Q)                                                                    \
+    do {                                                                                 \
+        unsigned short *xb_ = xl + ((Q) & 1u) * (unsigned int)(MB * XS) + xrow0 * XS + xpc * 8u; \
+        _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
+            *(rg_u4 *)(xb_ + (unsigned int)i * RSTEP * XS) =                             \
+                xrow0 + (unsigned int)i * RSTEP < mrows ? xr[i] : (rg_u4){0u, 0u, 0u, 0u}; \
+    } while (0)
+
+    /* Quad q is computed from LDS x buffer q & 1 and weight buffer q & 1. Its step first
+     * requests quad q + 1's x and quad q + 2's weights (x first: the store of x then waits
+     * for nothing issued after it), computes, and stores quad q + 1's x. */
+    RGM_XLOAD(0u);
+    RGM_WLOAD(0, 0u);
+    RGM_WLOAD(1, 1u);
+    RGM_XSTORE(0u);
+    rg_sync_lds();
+    for (unsigned int q = 0; q < qn; q += 2u) {
+#define RGM_STEP(BUF, QQ)                                                                \
+    do {                                                                                 \
+        const unsigned int qc_ = (QQ);                                                   \
+        RGM_XLOAD(qc_ + 1u);                                                             \
+        __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */ \
+        const unsigned short *xb = xl + (qc_ & 1u) * (unsigned int)(MB * XS);           \
+        const unsigned int sq_ = qc_ < qn ? 0xffffffffu : 0u;                            \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                  \
+            const unsigned int sbits = ws[BUF][t] & sq_;                                 \
+            rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));                 \
+            const rg_u4 q0v = wa[BUF][t][0], q1v = wa[BUF][t][1];                        \
+            unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                        \
+                                  q1v[0], q1v[1], q1v[2], q1v[3]};                       \
+            _Pragma("unroll") for (int s = 0; s < 4; ++s) {                              \
+                unsigned int d0, d1, d2, d3;                                             \
+                rg_dequant4(qd[2 * s], s2, d0, d1);                                      \
+                rg_dequant4(qd[2 * s + 1], s2, d2, d3);                                  \
+                rg_u4 av = {d0, d1, d2, d3};                                             \
+                rg_h8 A = __builtin_bit_cast(rg_h8, av);                                 \
+                _Pragma("unroll") for (int c = 0; c < CB; ++c) {                         \
+                    const rg_h8 B = *(const rg_h8 *)(xb + (wm * (16u * CB) + (unsigned int)c * 16u + r) * XS \
+                                                     + 32u * g + 8u * (unsigned int)s);  \
+                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[t][c], 0, 0, 0); \
+                }                                                                        \
+            }                                                                            \
+        }                                                                                \
+        __builtin_amdgcn_sched_barrier(0);     /* the MFMAs before the new loads */      \
+        RGM_WLOAD(BUF, qc_ + 2u);                                                        \
+        __builtin_amdgcn_sched_barrier(0);                                               \
+        RGM_XSTORE(qc_ + 1u);                                                            \
+        rg_sync_lds();                                                                   \
+    } while (0)
+        RGM_STEP(0, q);
+        RGM_STEP(1, q + 1u);
+#undef RGM_STEP
+    }
+#undef RGM_WLOAD
+#undef RGM_XLOAD
+#undef RGM_XSTORE
+
+    /* the tile results into LDS, out[(tile * 16 + row) * MB + batch row] (the x buffers
+     * are free after the last barrier), then the epilogue */
+    float *out = (float *)lds;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                out[((wn * 4u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i) * MB
+                    + wm * (16u * CB) + (unsigned int)c * 16u + r] = acc[t][c][i];
+    __syncthreads();
+    if (a.row_ss != nullptr) {
+        __shared__ float rs[MB];
+        rg_row_scale<MB, NT>(a, out, RT * 16u, mrows, rs);
+    }
+    rg_epilogue<MB, NT>(a, out, group, RT, mrows, nullptr);
+}
+
 /* ---- host ---------------------------------------------------------------------------- */
 
 static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
@@ -311,7 +474,8 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
                     unsigned int nseg, unsigned int k, int epi, unsigned int mt)
 {
     memset(a, 0, sizeof *a);
-    if (k == 0u || k % 32u != 0u || nseg == 0u || nseg > 3u || mt == 0u || mt > 32u) return 1;
+    if (k == 0u || k % 32u != 0u || nseg == 0u || nseg > 3u || mt == 0u || mt > AOTX_RGEMM_ROWS)
+        return 1;
     a->m = mt;
     a->k = k;
     a->qn = (unsigned int)aotx_q8r_quads(k);
@@ -333,6 +497,17 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     } else {
         a->n = total;
         tiles = (total + 15u) / 16u;
+    }
+    if (mt > 32u) {
+        /* 128 weight rows (8 tiles; SWIGLU: 4 gate/up pairs) by 128 batch rows per workgroup */
+        a->gemm = 1u;
+        a->rt = 8u;
+        a->nw = 8u;
+        a->groups = epi == AOTX_EPI_SWIGLU ? ((unsigned int)aotx_q8r_tiles(rows[0]) + 3u) / 4u
+                                           : (tiles + 7u) / 8u;
+        a->splits = 1u;
+        a->qps = a->qn;
+        return 0;
     }
     if (mt > 16u) {
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
@@ -445,6 +620,19 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         const size_t e = a.expert_stride != 0ull ? a.experts : 1u;
         a.count = (unsigned int *)aotx_scratch(AOTX_SCRATCH_GEMV_COUNT, e * a.groups * sizeof(unsigned int));
     }
+    if (a.gemm) {
+        if (a.xmode != AOTX_X_F16 || a.expert_stride != 0ull || a.list != nullptr
+            || a.xrow != nullptr || a.splits != 1u) {
+            fprintf(stderr, "aotx: the GEMM takes fp16 x of direct rows only\n");
+            exit(1);
+        }
+        const dim3 grid(a.groups, (a.m + RGM_MB - 1u) / RGM_MB);
+        const size_t x = 2u * RGM_MB * (128u + 8u) * 2u, res = 128u * RGM_MB * 4u;
+        const size_t lds = x > res ? x : res;
+        hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), grid, dim3(512), lds, s, a);
+        AOTX_LAUNCH_CHECK();
+        return;
+    }
     if (a.row_ss != nullptr && (!a.wide || a.list != nullptr || a.xrow != nullptr)) {
         fprintf(stderr, "aotx: the row-scaled product takes wide batches of direct rows only\n");
         exit(1);
@@ -504,8 +692,9 @@ static int aotx_q8r_gemv_any(const void *wr, unsigned int n, unsigned int k, con
     if (k == 0u || k % 32u != 0u || k % 8u != 0u) return 1;
     const void *ws[1] = {wr};
     unsigned int rows[1] = {n};
-    for (unsigned int m0 = 0; m0 < m; m0 += 32u) {
-        unsigned int mt = m - m0 < 32u ? m - m0 : 32u;
+    for (unsigned int m0 = 0, mt = 0; m0 < m; m0 += mt) {
+        /* more than 32 rows: GEMM passes of up to AOTX_RGEMM_ROWS */
+        mt = m - m0 > 32u ? (m - m0 < AOTX_RGEMM_ROWS ? m - m0 : AOTX_RGEMM_ROWS) : m - m0;
         aotx_rgemv_args a;
         if (aotx_rgemv_plan(&a, ws, rows, 1u, k, epi, mt) != 0) return 1;
         a.xmode = AOTX_X_F16;
