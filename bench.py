@@ -365,6 +365,37 @@ def moe_run(args):
     print(json.dumps(out))
 
 
+def prefill_run(args):
+    """`--prefill`: one prompt chunk of 128, 256 and 512 tokens of the 8B shape (a fresh
+    slot each time) through aotx_model_launch, whole step; best of 5 after a warm-up.
+    Prints one JSON line. AOTX_GEMM=0 in the environment times the 32-row passes instead
+    of the GEMM."""
+    import torch
+    from aotx_amd.model import LLAMA_8B, Runtime, build_device, layout_pages
+    torch.cuda.init()
+    shape = LLAMA_8B
+    region, lay = build_device(shape, seed=7)
+    per = layout_pages(512 + 16, shape.layers, shape.kv_heads, shape.head_dim)
+    rt = Runtime(region, lay.desc, max_tokens=512, pool_pages=per * 20 + 8)
+    rng = np.random.default_rng(0)
+    out, slot = {}, 0
+    for t in (128, 256, 512):
+        times = []
+        for _ in range(6):
+            ids = rng.integers(0, shape.vocab, t).tolist()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            rt.step(ids, [0, t], [slot])
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            slot += 1
+        best = min(times[1:])
+        out[str(t)] = {"ms": round(best * 1e3, 3), "tokens_per_s": round(t / best, 1)}
+    rt.close()
+    print(json.dumps({"metric": "prefill tokens/s (8B shape, one prompt chunk)",
+                      "gemm": os.environ.get("AOTX_GEMM", "1") != "0", "chunks": out}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -376,6 +407,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--moe", action="store_true",
                     help="BASELINE config 5 only: the Mixtral-shape routed-expert decoder")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time one prompt chunk of 128/256/512 tokens (8B shape) and exit")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the roofline kernel and a calibration copy (counter passes)")
     args = ap.parse_args()
@@ -390,6 +423,9 @@ def main():
         return
     if args.moe:
         moe_run(args)
+        return
+    if args.prefill:
+        prefill_run(args)
         return
 
     import torch
