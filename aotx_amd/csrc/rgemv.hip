@@ -269,30 +269,30 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
 }
 
-/* Many batch rows (prefill: 256..512 per pass): a GEMM. A workgroup takes 128 weight rows
- * (8 tiles) by MB batch rows; its 8 waves are 2 (weight rows) x 4 (batch rows), each holding
- * 4 tiles x MB/64 column blocks of accumulators, so each dequantised A fragment feeds MB/64
- * MFMAs and each B fragment read from LDS feeds 4 tiles (dequantisation and x staging are
- * VALU work that otherwise outweighs the MFMAs). Per 128-k quad: the next quad's x rows go
- * to LDS through registers (requested before this quad's MFMAs, stored after them), and the
- * weights are requested two quads ahead and dequantised in registers into the A operand,
- * as in the streaming product. The results pass through LDS to the same epilogues. */
-#define RGM_MB 192
+/* Many batch rows (prefill): a GEMM. A workgroup takes 256 weight rows (16 tiles; for
+ * SwiGLU 8 gate/up pairs) by MB batch rows. Each of its 8 waves owns 2 tiles over all MB
+ * rows (MB/16 column blocks of accumulators), so every weight is dequantised once per
+ * workgroup, each A fragment feeds MB/16 MFMAs, and each B fragment read from LDS feeds 2.
+ * Per 128-k quad: the next quad's x rows go to LDS through registers (requested before
+ * this quad's MFMAs, stored after them), and the weights are requested two quads ahead
+ * and dequantised in registers into the A operand, as in the streaming product. The
+ * results pass through LDS to the same epilogues. */
+#define RGM_MB 64
+#define RGM_RT 16
 template <int MB>
 __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
 {
-    constexpr int RT = 8;                         /* weight tiles per workgroup */
-    constexpr int CB = MB / 64;                   /* column blocks per wave */
+    constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
+    constexpr int CB = MB / 16;                   /* column blocks per wave */
     constexpr int NT = 512;
     constexpr int XS = 128 + 8;                   /* LDS x row stride (halves) */
     constexpr int PIECES = 16;                    /* 16-byte pieces of a row per quad */
     constexpr int PPT = MB * PIECES / NT;         /* pieces per thread */
-    static_assert(MB * PIECES % NT == 0 && MB % 64 == 0, "whole pieces and blocks");
+    static_assert(MB * PIECES % NT == 0 && MB % 16 == 0, "whole pieces and blocks");
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const unsigned int tid = threadIdx.x;
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
-    const unsigned int wn = wave & 1u, wm = wave >> 1;   /* 2 x 4 waves */
     const unsigned int r = lane & 15u, g = lane >> 4;
     const unsigned int group = blockIdx.x;
 
@@ -307,24 +307,22 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
     const unsigned int mrows = total - a.m0 < (unsigned int)MB ? total - a.m0 : (unsigned int)MB;
 
     unsigned short *xl = (unsigned short *)lds;         /* [2][MB][XS] */
-    const unsigned char *qb[4];
-    const unsigned short *sb[4];
+    const unsigned char *qb[2];
+    const unsigned short *sb[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 2; ++t) {
         unsigned int dummy = 0u;
-        qb[t] = rg_tile(a, group, wn * 4u + (unsigned int)t, RT, 0u, dummy) + lane * 16u;
-        sb[t] = rg_scales(a, group, wn * 4u + (unsigned int)t, RT, 0u) + lane;
+        qb[t] = rg_tile(a, group, wave * 2u + (unsigned int)t, RT, 0u, dummy) + lane * 16u;
+        sb[t] = rg_scales(a, group, wave * 2u + (unsigned int)t, RT, 0u) + lane;
     }
-    rg_f4 acc[4][CB];
+    rg_f4 acc[2][CB];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[t][c] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    /* a thread's x pieces keep their row and place from quad to quad: the row's address
-     * (a valid row for rows past mrows, whose pieces are stored as zeros) and the LDS
-     * offset are computed once */
-    /* piece i of a thread is row tid / 16 + 32 i, place tid % 16 */
+    /* piece i of a thread is row tid / 16 + 32 i, place tid % 16 (rows past mrows read a
+     * valid row and are stored as zeros) */
     constexpr unsigned int RSTEP = NT / PIECES;
     const unsigned int xrow0 = tid / PIECES, xpc = tid % PIECES;
     unsigned int xoff[PPT];                       /* element offsets from a.x */
@@ -334,14 +332,14 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
         xoff[i] = (a.m0 + (mm < mrows ? mm : 0u)) * a.ldx + xpc * 8u;
     }
 
-    rg_u4 wa[2][4][2];
-    unsigned int ws[2][4];
+    rg_u4 wa[2][2][2];
+    unsigned int ws[2][2];
     const unsigned int qn = a.qn;
     /* every call issues the same loads (a quad past k repeats the last: never computed) */
 #define RGM_WLOAD(BUF, Q)                                                                \
     do {                                                                                 \
         const unsigned int qq_ = (Q) < qn ? (Q) : qn - 1u;                               \
-        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                  \
+        _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                  \
             const rg_u4 *src = (const rg_u4 *)(qb[t] + (unsigned long long)qq_ * 2048ull); \
             wa[BUF][t][0] = __builtin_nontemporal_load(src);                            \
             wa[BUF][t][1] = __builtin_nontemporal_load(src + 64);                        \
@@ -380,7 +378,8 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
         __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */ \
         const unsigned short *xb = xl + (qc_ & 1u) * (unsigned int)(MB * XS);           \
         const unsigned int sq_ = qc_ < qn ? 0xffffffffu : 0u;                            \
-        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                  \
+        rg_h8 A[2][4];                                                                   \
+        _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                  \
             const unsigned int sbits = ws[BUF][t] & sq_;                                 \
             rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));                 \
             const rg_u4 q0v = wa[BUF][t][0], q1v = wa[BUF][t][1];                        \
@@ -391,14 +390,16 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
                 rg_dequant4(qd[2 * s], s2, d0, d1);                                      \
                 rg_dequant4(qd[2 * s + 1], s2, d2, d3);                                  \
                 rg_u4 av = {d0, d1, d2, d3};                                             \
-                rg_h8 A = __builtin_bit_cast(rg_h8, av);                                 \
-                _Pragma("unroll") for (int c = 0; c < CB; ++c) {                         \
-                    const rg_h8 B = *(const rg_h8 *)(xb + (wm * (16u * CB) + (unsigned int)c * 16u + r) * XS \
-                                                     + 32u * g + 8u * (unsigned int)s);  \
-                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[t][c], 0, 0, 0); \
-                }                                                                        \
+                A[t][s] = __builtin_bit_cast(rg_h8, av);                                 \
             }                                                                            \
         }                                                                                \
+        _Pragma("unroll") for (int c = 0; c < CB; ++c)                                   \
+            _Pragma("unroll") for (int s = 0; s < 4; ++s) {                              \
+                const rg_h8 B = *(const rg_h8 *)(xb + ((unsigned int)c * 16u + r) * XS    \
+                                                 + 32u * g + 8u * (unsigned int)s);      \
+                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][s], B, acc[0][c], 0, 0, 0); \
+                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][s], B, acc[1][c], 0, 0, 0); \
+            }                                                                            \
         __builtin_amdgcn_sched_barrier(0);     /* the MFMAs before the new loads */      \
         RGM_WLOAD(BUF, qc_ + 2u);                                                        \
         __builtin_amdgcn_sched_barrier(0);                                               \
@@ -417,13 +418,13 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
      * are free after the last barrier), then the epilogue */
     float *out = (float *)lds;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int c = 0; c < CB; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                out[((wn * 4u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i) * MB
-                    + wm * (16u * CB) + (unsigned int)c * 16u + r] = acc[t][c][i];
+                out[((wave * 2u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i) * MB
+                    + (unsigned int)c * 16u + r] = acc[t][c][i];
     __syncthreads();
     if (a.row_ss != nullptr) {
         __shared__ float rs[MB];
@@ -499,12 +500,12 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         tiles = (total + 15u) / 16u;
     }
     if (mt > 32u) {
-        /* 128 weight rows (8 tiles; SWIGLU: 4 gate/up pairs) by 128 batch rows per workgroup */
+        /* 256 weight rows (16 tiles; SWIGLU: 8 gate/up pairs) by 64 batch rows per workgroup */
         a->gemm = 1u;
-        a->rt = 8u;
+        a->rt = 16u;
         a->nw = 8u;
-        a->groups = epi == AOTX_EPI_SWIGLU ? ((unsigned int)aotx_q8r_tiles(rows[0]) + 3u) / 4u
-                                           : (tiles + 7u) / 8u;
+        a->groups = epi == AOTX_EPI_SWIGLU ? ((unsigned int)aotx_q8r_tiles(rows[0]) + 7u) / 8u
+                                           : (tiles + 15u) / 16u;
         a->splits = 1u;
         a->qps = a->qn;
         return 0;
@@ -627,7 +628,7 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             exit(1);
         }
         const dim3 grid(a.groups, (a.m + RGM_MB - 1u) / RGM_MB);
-        const size_t x = 2u * RGM_MB * (128u + 8u) * 2u, res = 128u * RGM_MB * 4u;
+        const size_t x = 2u * RGM_MB * (128u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
         const size_t lds = x > res ? x : res;
         hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), grid, dim3(512), lds, s, a);
         AOTX_LAUNCH_CHECK();
