@@ -7,9 +7,11 @@
  *   quads  Qn = ceil(k / 128)        (4 blocks of 32; blocks past k are zero)
  *   quants: [T][Qn][2 halves][64 lanes][16 B]  lane l = r + 16 g holds row 16t + r,
  *           block 4Q + g: quants 0..15 in the first half, 16..31 in the second, so each of a
- *           wave's two 16-byte loads reads 1 KB of contiguous bytes
+ *           wave's two 16-byte loads reads 1 KB of contiguous bytes; each quant is stored
+ *           as the byte q + 128 (q XOR 0x80), which the dequantisation uses as it is
  *   scales: [T][Qn][64 lanes] fp16   the scale of that block
- * A tensor is 34/32 bytes per weight plus the zero padding of the last tile and quad.
+ * A tensor is 34/32 bytes per weight plus the padding of the last tile and quad (q = 0,
+ * scale 0).
  */
 #ifndef AOTX_RGEMV_H
 #define AOTX_RGEMV_H

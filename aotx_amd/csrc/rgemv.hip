@@ -51,10 +51,10 @@ __global__ void aotx_q8r_repack_kernel(const unsigned char *src, unsigned int n,
         if (row < n && blk < blocks) {
             const unsigned char *b = src + row * row_bytes + blk * 34ull;
             *sd = (unsigned short)(b[0] | (b[1] << 8));
-            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = b[2 + j];
+            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = b[2 + j] ^ 0x80u;
         } else {
             *sd = 0u;
-            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = 0u;
+            for (int j = 0; j < 32; ++j) qd[(j >> 4) * 1024 + (j & 15)] = 0x80u;   /* q = 0 */
         }
     }
 }

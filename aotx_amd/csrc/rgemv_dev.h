@@ -30,10 +30,12 @@ static __device__ __forceinline__ void rg_sync_lds()
 
 /* ---- product ------------------------------------------------------------------------ */
 
-static __device__ __forceinline__ void rg_dequant4(unsigned int w, rg_h2 s2, unsigned int &lo,
+/* Four Q8R quants (stored as q + 128, one byte each) to half(q * scale): the byte under
+ * exponent bits 0x64 is the half 1024 + byte = 1152 + q, exact; minus 1152 is q, exact; the
+ * product with the scale rounds once. */
+static __device__ __forceinline__ void rg_dequant4(unsigned int u, rg_h2 s2, unsigned int &lo,
                                                    unsigned int &hi)
 {
-    unsigned int u = w ^ 0x80808080u;
     unsigned int a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
     unsigned int b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
     const rg_h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};

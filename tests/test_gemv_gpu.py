@@ -148,7 +148,8 @@ def test_repacked_gemv_benchmark_shapes(torch, lib, orc, n, k, m):
 
 def test_repack_layout(torch, lib):
     """Repacked bytes: lane l = r + 16 g of (tile t, quad q) holds row 16t + r, block 4q + g;
-    its quants 0..15 sit in the first 1 KB half of the (t, q) record, 16..31 in the second."""
+    its quants 0..15 sit in the first 1 KB half of the (t, q) record, 16..31 in the second,
+    each stored as q + 128 (the byte XOR 0x80); padding is q = 0 with scale 0."""
     n, k = 40, 384
     w = make(torch, lib, n, k, 3)
     wr = repack(torch, lib, w, n, k).cpu().numpy()
@@ -163,7 +164,7 @@ def test_repack_layout(torch, lib):
                 r, g = lane % 16, lane // 16
                 row, blk = 16 * t + r, 4 * q + g
                 if row < n and blk < k // 32:
-                    assert np.array_equal(quant[t, q, lane], src[row, blk, 2:])
+                    assert np.array_equal(quant[t, q, lane], src[row, blk, 2:] ^ 0x80)
                     assert scale[t, q, lane] == src[row, blk, :2].view(np.uint16)[0]
                 else:
-                    assert not quant[t, q, lane].any() and scale[t, q, lane] == 0
+                    assert (quant[t, q, lane] == 0x80).all() and scale[t, q, lane] == 0
