@@ -101,6 +101,28 @@ class ModelRun(ctypes.Structure):
     ]
 
 
+AOTX_MODEL_ROLES = 5
+AOTX_SEQ_TICK_BUDGET = 512
+AOTX_SEQ_STATE_FREE, AOTX_SEQ_STATE_PREFILL, AOTX_SEQ_STATE_DECODE, AOTX_SEQ_STATE_DONE = 0, 1, 2, 3
+
+
+class PlanSlot(ctypes.Structure):
+    """include/aotx_plan.h aotx_plan_slot (the reference's aotx_seq fields the plan reads)."""
+    _fields_ = [("state", u32), ("role", u32), ("prompt", u32), ("sampled", u32),
+                ("limit", u32), ("page_limit", u32), ("seed", u64), ("sample", ModelHow)]
+
+
+class PlanState(ctypes.Structure):
+    """include/aotx_plan.h aotx_plan_state (cuda/model/decode_state.cuh:35-55)."""
+    _fields_ = [
+        ("ids", i32 * AOTX_SEQ_TICK_BUDGET), ("offset", u32 * (AOTX_SLOTS + 1)),
+        ("agent", u32 * AOTX_SLOTS), ("how", ModelHow * AOTX_SLOTS), ("rows", u32 * AOTX_SLOTS),
+        ("first", u32 * AOTX_SLOTS), ("place", u32 * AOTX_SLOTS), ("asked", u32 * AOTX_SLOTS),
+        ("cursor", u32 * AOTX_MODEL_ROLES), ("seqs", u32), ("tokens", u32), ("waited", u32),
+        ("short_of", u32), ("steps", u64),
+    ]
+
+
 class KvEntry(ctypes.Structure):
     _fields_ = [("agent", u32), ("pages", u32)]
 
@@ -165,6 +187,9 @@ PROTOTYPES = {
     "aotx_model_probe": (i32, [u32, vp, vp, u32, vp, vp, vp, u32, vp, vp, u32]),
     "aotx_model_buffer": (u64, [u32, u32]),
     "aotx_model_seat": (i32, [u32, u32]),
+    # the tick plan (include/aotx_plan.h)
+    "aotx_decode_plan": (i32, [u32, vp, vp, u32, u32, u32, vp, vp]),
+    "aotx_model_kv_pages": (u32, [u32, u32]),
     "aotx_kv_open": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_reserve": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_serve": (i32, [ctypes.POINTER(KvMap), vp]),

@@ -91,6 +91,9 @@ static inline __host__ __device__ unsigned int aotx_kvl_pages(const aotx_kvl_sha
     return (blocks + s.blocks_page - 1u) / s.blocks_page;
 }
 
+/* The KV shape of a role with a model described (model.hip); 1 when it has none. */
+int aotx_role_kv_shape(unsigned int role, aotx_kvl_shape *out);
+
 /* First byte of the layout block holding (layer, position) of one slot, or null. */
 static inline __device__ unsigned char *aotx_kvl_block(const aotx_kvl_shape &s,
                                                        const aotx_kv_table *kv,

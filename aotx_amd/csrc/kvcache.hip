@@ -9,6 +9,7 @@
  * reference's, so every page-table decision is the same.
  */
 #include "aotx_internal.h"
+#include "kvcache_dev.h"
 
 #include <stddef.h>
 #include <string.h>
@@ -145,28 +146,6 @@ extern "C" void aotx_kv_close(aotx_kv_map *map)
     AOTX_CHECK(hipDeviceSynchronize());
     map->range = 0ull;
     map->free_count = 0u;
-}
-
-/* One request into the queue (cuda/kvcache/pages.cu:13-57). */
-static __device__ int aotx_kv_put(aotx_kv_table *kv, unsigned int agent, unsigned int pages)
-{
-    if (agent >= AOTX_SLOTS || pages > AOTX_KV_PAGES_EACH) {
-        atomicAdd(&kv->refused, 1u);
-        return 0;
-    }
-    unsigned int at = atomicAdd(&kv->made, 0u);
-    for (;;) {
-        if (at - atomicAdd(&kv->served, 0u) >= AOTX_KV_QUEUE_MAX) {
-            atomicAdd(&kv->refused, 1u);
-            return 0;
-        }
-        unsigned int was = atomicCAS(&kv->made, at, at + 1u);
-        if (was == at) break;
-        at = was;
-    }
-    kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].agent = agent;
-    kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].pages = pages;
-    return 1;
 }
 
 __global__ void aotx_kv_put_kernel(aotx_state *state, unsigned int agent, unsigned int pages,

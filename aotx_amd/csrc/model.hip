@@ -22,6 +22,7 @@
  * the same kernels eagerly).
  */
 #include "aotx_internal.h"
+#include "../../include/aotx_plan.h"
 #include "attention.h"
 #include "chain.h"
 #include "experts.h"
@@ -183,6 +184,21 @@ static int aotx_desc_ok(const aotx_model_desc *d)
         }
     }
     return 1;
+}
+
+int aotx_role_kv_shape(unsigned int role, aotx_kvl_shape *out)
+{
+    if (role >= AOTX_MODEL_ROLES || !aotx_holds[role].described) return 1;
+    const aotx_model_desc *d = &aotx_holds[role].desc;
+    *out = aotx_kvl_make(d->layers, d->kv_heads, d->head_dim);
+    return 0;
+}
+
+extern "C" unsigned int aotx_model_kv_pages(unsigned int role, unsigned int context)
+{
+    aotx_kvl_shape shape;
+    if (aotx_role_kv_shape(role, &shape) != 0) return 0u;
+    return aotx_kvl_pages(shape, context);
 }
 
 extern "C" int aotx_model_set_desc(unsigned int role, const aotx_model_desc *desc)

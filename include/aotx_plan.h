@@ -1,0 +1,84 @@
+/* The tick plan: the row packing that builds the batch of one decode step from the
+ * sequence slots (the reference's aotx_decode_plan, cuda/model/plan.cu:54-199, with the
+ * page check of cuda/model/decode_state.cuh:75-107).
+ *
+ * The reference's plan reads its slots from the device sequence store and its gates
+ * (ready, scheduler hold, journal replay, role rotation) from device globals. Here the
+ * caller hands the slot fields the packing reads as a device table and calls the plan
+ * only on ticks that run; the batch it writes (ids, offset, agent, how) is what
+ * aotx_model_sample / aotx_model_launch take, in device memory, with no host copy. */
+#ifndef AOTX_PLAN_H
+#define AOTX_PLAN_H
+
+#include "aotx_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AOTX_SEQ_TICK_BUDGET   512u   /* rows of one tick at most: cuda/model/decode.cuh:15 */
+
+/* Slot states: cuda/model/decode.cuh:19-22. */
+#define AOTX_SEQ_STATE_FREE    0u
+#define AOTX_SEQ_STATE_PREFILL 1u
+#define AOTX_SEQ_STATE_DECODE  2u
+#define AOTX_SEQ_STATE_DONE    3u
+
+/* The fields of a sequence slot the plan reads (the reference's aotx_seq: state, role,
+ * prompt, sampled, limit, page_limit, seed, sample; read at plan.cu:74-156). */
+typedef struct aotx_plan_slot {
+    unsigned int state;
+    unsigned int role;
+    unsigned int prompt;       /* prompt tokens of the list */
+    unsigned int sampled;      /* tokens sampled so far (the list holds prompt + sampled) */
+    unsigned int limit;        /* reply tokens at most: pages cover prompt + limit */
+    unsigned int page_limit;   /* pages the slot may hold (0: no limit) */
+    unsigned long long seed;
+    aotx_model_how sample;
+} aotx_plan_slot;
+
+/* The batch of one tick and the plan's marks (cuda/model/decode_state.cuh:35-55 without
+ * the multimodal input rows and the role/replay gates; asked is aotx_seq_asked,
+ * decode_state.cuh:67-70). Device memory, zeroed by the caller before the first tick. */
+typedef struct aotx_plan_state {
+    int ids[AOTX_SEQ_TICK_BUDGET];          /* the token of every row of the batch */
+    unsigned int offset[AOTX_SLOTS + 1u];   /* the first row of each sequence */
+    unsigned int agent[AOTX_SLOTS];         /* the slot of each sequence */
+    aotx_model_how how[AOTX_SLOTS];         /* the sample of each sequence (seed = slot seed) */
+    unsigned int rows[AOTX_SLOTS];          /* rows each slot gave this tick */
+    unsigned int first[AOTX_SLOTS];         /* the list position of the first of them */
+    unsigned int place[AOTX_SLOTS];         /* the slot's sequence, or AOTX_SLOTS */
+    unsigned int asked[AOTX_SLOTS];         /* pages each slot has asked the pool for */
+    unsigned int cursor[AOTX_MODEL_ROLES];  /* the rotating first slot of each role */
+    unsigned int seqs;                      /* sequences of this tick's batch */
+    unsigned int tokens;                    /* rows of this tick's batch */
+    unsigned int waited;                    /* prefill pieces that got no room, summed */
+    unsigned int short_of;                  /* slots that waited for pages, summed */
+    unsigned long long steps;               /* ticks that gave a batch of one row or more */
+} aotx_plan_state;
+
+/* Plan one tick of `role` (cuda/model/plan.cu:54-199): every slot of the role in state
+ * PREFILL or DECODE whose list (prompt + sampled) has tokens no page holds yet (the
+ * device's seen count) and whose pages cover prompt + limit takes part; a slot short of
+ * pages asks the pool (the device request queue, aotx_kv_serve answers it) and waits.
+ * Decode slots give one row each, first, in slot order from the role's cursor; prefill
+ * slots then take the rest of `budget` (at most AOTX_SEQ_TICK_BUDGET) in the same order,
+ * and the piece that crosses its end is cut. slots [AOTX_SLOTS], tokens [AOTX_SLOTS][stride]
+ * (each slot's list) and plan are device pointers; pool_pages is the pool's page count
+ * (the map's limit; a partly served request is asked again while pages are free).
+ * Returns 1 for a role with no model described or a bad argument. Asynchronous on the
+ * stream. */
+int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, const int *tokens,
+                     unsigned int stride, unsigned int budget, unsigned int pool_pages,
+                     aotx_plan_state *plan, void *stream);
+
+/* Pages a slot of `role` needs for a context of `context` positions (the reference's
+ * aotx_kvl_pages over the role's KV shape, cuda/model/kv_layout.cuh); 0 when the role has
+ * no model described. */
+unsigned int aotx_model_kv_pages(unsigned int role, unsigned int context);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

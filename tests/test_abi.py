@@ -11,6 +11,7 @@ import aotx_amd
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "aotx_hip.h")
+PLAN_HEADER = os.path.join(ROOT, "include", "aotx_plan.h")
 HEADERS = sorted(os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))
                  if f.endswith(".h"))
 
@@ -55,6 +56,8 @@ STRUCTS = {
     "aotx_model_run": aotx_amd.ModelRun,
     "aotx_kv_map": aotx_amd.KvMap,
     "aotx_kv_table": aotx_amd.KvTable,
+    "aotx_plan_slot": aotx_amd.PlanSlot,
+    "aotx_plan_state": aotx_amd.PlanState,
 }
 
 
@@ -65,8 +68,10 @@ def test_struct_layouts_match_c(tmp_path):
         "aotx_model_run": ["ids", "seed", "seqs", "select", "temperature", "how", "capture_count"],
         "aotx_kv_map": ["limit", "held", "free_count", "created"],
         "aotx_kv_table": ["count", "made", "served", "queue"],
+        "aotx_plan_slot": ["state", "page_limit", "seed", "sample"],
+        "aotx_plan_state": ["offset", "how", "place", "asked", "cursor", "seqs", "short_of", "steps"],
     }
-    src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void){']
+    src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', f'#include "{PLAN_HEADER}"', 'int main(void){']
     for name, fl in fields.items():
         src.append(f'printf("{name} %zu\\n", sizeof({name}));')
         for f in fl:
