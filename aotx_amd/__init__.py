@@ -123,6 +123,17 @@ class PlanState(ctypes.Structure):
     ]
 
 
+class TextSource(ctypes.Structure):
+    """include/aotx_text.h aotx_text_source (cuda/text/text.cuh:128-137); host arrays."""
+    _fields_ = [("token_bytes", vp), ("token_at", vp), ("tokens", u64), ("merge_bytes", vp),
+                ("merge_at", vp), ("merges", u64), ("token_type", vp), ("family", u32)]
+
+
+class TextStore(ctypes.Structure):
+    """include/aotx_text.h aotx_text_store (cuda/text/text.cuh:146-150)."""
+    _fields_ = [("block", vp * 8), ("blocks", u32), ("bytes", u64)]
+
+
 class KvEntry(ctypes.Structure):
     _fields_ = [("agent", u32), ("pages", u32)]
 
@@ -190,6 +201,13 @@ PROTOTYPES = {
     # the tick plan (include/aotx_plan.h)
     "aotx_decode_plan": (i32, [u32, vp, vp, u32, u32, u32, vp, vp]),
     "aotx_model_kv_pages": (u32, [u32, u32]),
+    # the tokenizer (include/aotx_text.h)
+    "aotx_text_family_find": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(u32)]),
+    "aotx_text_vocab_build": (i32, [ctypes.POINTER(TextSource), ctypes.POINTER(TextStore)]),
+    "aotx_text_vocab_release": (None, [ctypes.POINTER(TextStore)]),
+    "aotx_text_vocab_report": (i32, [ctypes.POINTER(u32)]),
+    "aotx_text_encode": (i32, [vp, vp, u32, vp, vp, vp]),
+    "aotx_text_detok": (i32, [vp, vp, u32, vp, u32, vp, vp]),
     "aotx_kv_open": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_reserve": (i32, [ctypes.POINTER(KvMap)]),
     "aotx_kv_serve": (i32, [ctypes.POINTER(KvMap), vp]),

@@ -1,0 +1,99 @@
+"""Byte-level BPE tokenizer restated in Python — TEST INFRASTRUCTURE ONLY.
+
+Follows the reference's cuda/text/: the byte map of cuda/text/text.cuh:256-290 (the GPT-2
+byte-to-code-point map), the split patterns whose alternatives cuda/text/pretok.cu:6-45
+states (written here as the published regular expressions of those families, run by the
+`regex` module), the merge step of cuda/text/bpe.cu (the pair of lowest merge rank first,
+the leftmost of equal ranks; with the family's whole rule a pre-token that is a token
+stays whole, cuda/text/families.h:18-23), and the detokenizer of cuda/text/detok.cu
+(byte-level code points give their byte, control tokens give nothing).
+"""
+import regex
+
+PATTERNS = {
+    "qwen2": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
+    "llama3": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
+    "gpt2": r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+|\s+(?!\S)|\s+",
+    "qwen35": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}\p{M}]?[\p{L}\p{M}]+|\p{N}| ?[^\s\p{L}\p{N}\p{M}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
+}
+# pattern row and whole rule of each family (cuda/text/families.h:10-43)
+FAMILY = {"qwen2": ("qwen2", False), "llama3": ("llama3", True), "llama-bpe": ("llama3", True),
+          "gpt-2": ("gpt2", False), "qwen35": ("qwen35", False)}
+
+
+def byte_point(b):
+    if 0x21 <= b <= 0x7E or 0xA1 <= b <= 0xAC or 0xAE <= b <= 0xFF:
+        return b
+    if b <= 0x20:
+        return 0x100 + b
+    if b <= 0xA0:
+        return 0x100 + 33 + (b - 0x7F)
+    return 0x100 + 67
+
+
+POINT_BYTE = {byte_point(b): b for b in range(256)}
+
+
+def byte_string(bs):
+    """The byte-level string of raw bytes."""
+    return "".join(chr(byte_point(b)) for b in bs)
+
+
+def pretokens(text, pattern):
+    """Pre-tokens of a str (consecutive, covering it)."""
+    return [m.group(0) for m in regex.finditer(PATTERNS[pattern], text)]
+
+
+class Vocab:
+    def __init__(self, tokens, merges, types=None, family="gpt-2"):
+        self.tokens = list(tokens)
+        self.id = {}
+        for i, t in enumerate(self.tokens):
+            self.id.setdefault(t, i)
+        self.rank = {}
+        for r, m in enumerate(merges):
+            sp = m.find(" ", 1)
+            if sp < 0:
+                continue
+            left, right = m[:sp], m[sp + 1:]
+            if left in self.id and right in self.id and left + right in self.id:
+                self.rank.setdefault((self.id[left], self.id[right]), (r, self.id[left + right]))
+        self.types = list(types) if types is not None else [1] * len(self.tokens)
+        self.pattern, self.whole = FAMILY[family]
+
+    def merge(self, piece_bytes):
+        s = byte_string(piece_bytes)
+        if self.whole and s in self.id:
+            return [self.id[s]]
+        sym = [self.id[ch] for ch in s]
+        while len(sym) > 1:
+            best = None
+            for i in range(len(sym) - 1):
+                got = self.rank.get((sym[i], sym[i + 1]))
+                if got is not None and (best is None or got[0] < best[0]):
+                    best = (got[0], i, got[1])
+            if best is None:
+                break
+            _, i, res = best
+            sym[i:i + 2] = [res]
+        return sym
+
+    def encode(self, data):
+        """Token ids of UTF-8 bytes."""
+        out = []
+        for piece in pretokens(data.decode("utf-8"), self.pattern):
+            out += self.merge(piece.encode("utf-8"))
+        return out
+
+    def decode(self, ids):
+        out = bytearray()
+        for i in ids:
+            if i >= len(self.tokens) or self.types[i] == 3:
+                continue
+            for ch in self.tokens[i]:
+                p = ord(ch)
+                if p in POINT_BYTE:
+                    out.append(POINT_BYTE[p])
+                else:
+                    out += ch.encode("utf-8")
+        return bytes(out)

@@ -12,6 +12,7 @@ import aotx_amd
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "aotx_hip.h")
 PLAN_HEADER = os.path.join(ROOT, "include", "aotx_plan.h")
+TEXT_HEADER = os.path.join(ROOT, "include", "aotx_text.h")
 HEADERS = sorted(os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))
                  if f.endswith(".h"))
 
@@ -58,6 +59,8 @@ STRUCTS = {
     "aotx_kv_table": aotx_amd.KvTable,
     "aotx_plan_slot": aotx_amd.PlanSlot,
     "aotx_plan_state": aotx_amd.PlanState,
+    "aotx_text_source": aotx_amd.TextSource,
+    "aotx_text_store": aotx_amd.TextStore,
 }
 
 
@@ -70,8 +73,10 @@ def test_struct_layouts_match_c(tmp_path):
         "aotx_kv_table": ["count", "made", "served", "queue"],
         "aotx_plan_slot": ["state", "page_limit", "seed", "sample"],
         "aotx_plan_state": ["offset", "how", "place", "asked", "cursor", "seqs", "short_of", "steps"],
+        "aotx_text_source": ["tokens", "merge_bytes", "merges", "token_type", "family"],
+        "aotx_text_store": ["blocks", "bytes"],
     }
-    src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', f'#include "{PLAN_HEADER}"', 'int main(void){']
+    src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', f'#include "{PLAN_HEADER}"', f'#include "{TEXT_HEADER}"', 'int main(void){']
     for name, fl in fields.items():
         src.append(f'printf("{name} %zu\\n", sizeof({name}));')
         for f in fl:

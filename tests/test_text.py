@@ -1,0 +1,79 @@
+"""The tokenizer's oracle (oracle/text.py) pinned against an independent BPE
+implementation (the `tokenizers` library) on a vocabulary it trained, and the family
+table of the library (no GPU)."""
+import random
+
+import pytest
+
+from oracle.text import FAMILY, PATTERNS, Vocab, pretokens
+from tests.text_util import hf_with, text, trained
+
+
+@pytest.fixture(scope="module")
+def bpe():
+    return trained()
+
+
+@pytest.mark.parametrize("family", ["gpt-2", "llama3", "qwen2", "qwen35"])
+def test_oracle_matches_tokenizers_library(bpe, family):
+    tokens, merges, _ = bpe
+    pattern, whole = FAMILY[family]
+    v = Vocab(tokens, merges, family=family)
+    hf = hf_with(PATTERNS[pattern], tokens, merges, whole)
+    rng = random.Random(11)
+    for _ in range(300):
+        s = text(rng, rng.randint(1, 40))
+        assert v.encode(s.encode()) == hf.encode(s).ids, repr(s)
+
+
+def test_gpt2_split_is_the_byte_level_pretokenizer(bpe):
+    """The gpt2 pattern here equals the library's own ByteLevel split."""
+    tokens, merges, hf = bpe
+    v = Vocab(tokens, merges, family="gpt-2")
+    rng = random.Random(12)
+    for _ in range(200):
+        s = text(rng, rng.randint(1, 40))
+        assert v.encode(s.encode()) == hf.encode(s).ids, repr(s)
+
+
+def test_pretokens_cover_text_and_known_splits():
+    rng = random.Random(13)
+    for pattern in PATTERNS:
+        for _ in range(100):
+            s = text(rng, 20)
+            assert "".join(pretokens(s, pattern)) == s
+    # numbers: llama3 groups of three from the left, qwen2 one by one, gpt2 one run
+    assert pretokens("x 1234567", "llama3") == ["x", " ", "123", "456", "7"]
+    assert pretokens("x 1234567", "qwen2") == ["x", " ", "1", "2", "3", "4", "5", "6", "7"]
+    assert pretokens("x 1234567", "gpt2") == ["x", " 1234567"]
+    # contractions: any case for llama3, small letters only for gpt2
+    assert pretokens("IT'S", "llama3") == ["IT", "'S"]
+    assert pretokens("IT'S", "gpt2") == ["IT", "'", "S"]
+    # a space run gives back its last space to a following word; newlines end a run
+    assert pretokens("a   b", "gpt2") == ["a", "  ", " b"]
+    assert pretokens("a \n\n b", "llama3") == ["a", " \n\n", " b"]
+
+
+def test_decode_round_trip_and_control(bpe):
+    tokens, merges, _ = bpe
+    types = [1] * len(tokens)
+    v = Vocab(tokens, merges, types, family="llama3")
+    rng = random.Random(14)
+    for _ in range(100):
+        b = text(rng, 30).encode()
+        assert v.decode(v.encode(b)) == b
+    ids = v.encode(b"hello world")
+    types[ids[0]] = 3
+    v2 = Vocab(tokens, merges, types, family="llama3")
+    assert v2.decode(ids) == v.decode(ids[1:])
+
+
+def test_family_table(lib):
+    import ctypes
+    row = ctypes.c_uint32()
+    names = ["qwen2", "deepseek-r1-qwen", "kormo", "f2llmv2", "llama3", "llama-v3", "llama-bpe",
+             "falcon3", "falcon-h1", "pixtral", "midm-2.0", "lfm2", "jina-v5-nano", "gpt-2", "mpt",
+             "olmo", "jais", "trillion", "granite-docling", "qwen35"]
+    for i, n in enumerate(names):
+        assert lib.aotx_text_family_find(n.encode(), len(n), ctypes.byref(row)) == 0 and row.value == i
+    assert lib.aotx_text_family_find(b"nope", 4, ctypes.byref(row)) == 1

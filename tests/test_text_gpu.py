@@ -1,0 +1,124 @@
+"""The tokenizer on the GPU (aotx_text_encode / aotx_text_detok) against its oracle, on a
+vocabulary trained by the `tokenizers` library, for four split families."""
+import ctypes
+import random
+
+import numpy as np
+import pytest
+
+import aotx_amd
+from aotx_amd import TextSource, TextStore
+from oracle.text import Vocab
+from tests.text_util import text, trained
+
+pytestmark = pytest.mark.gpu
+
+ROWS = {"qwen2": 0, "llama3": 4, "gpt-2": 13, "qwen35": 19}
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+    return torch
+
+
+@pytest.fixture(scope="module")
+def bpe():
+    return trained()
+
+
+def _runs(strings):
+    data = [s.encode("utf-8") for s in strings]
+    at = np.zeros(len(data) + 1, dtype=np.uint64)
+    at[1:] = np.cumsum([len(d) for d in data])
+    return np.frombuffer(b"".join(data), dtype=np.uint8).copy(), at
+
+
+class Built:
+    """The library's vocabulary built from tokens/merges/types for a family."""
+
+    def __init__(self, lib, tokens, merges, types, family):
+        self.lib = lib
+        self.keep = []
+        tb, ta = _runs(tokens)
+        mb, ma = _runs(merges)
+        ty = np.asarray(types, dtype=np.int32)
+        self.keep += [tb, ta, mb, ma, ty]
+        src = TextSource()
+        src.token_bytes, src.token_at, src.tokens = tb.ctypes.data, ta.ctypes.data, len(tokens)
+        src.merge_bytes, src.merge_at, src.merges = mb.ctypes.data, ma.ctypes.data, len(merges)
+        src.token_type = ty.ctypes.data
+        src.family = ROWS[family]
+        self.store = TextStore()
+        assert lib.aotx_text_vocab_build(ctypes.byref(src), ctypes.byref(self.store)) == 0
+
+    def close(self):
+        self.lib.aotx_text_vocab_release(ctypes.byref(self.store))
+
+
+def _encode(torch, lib, strings):
+    data, at = _runs(strings)
+    d = torch.from_numpy(data if len(data) else np.zeros(1, np.uint8)).cuda()
+    a = torch.from_numpy(at.view(np.int64)).cuda()
+    ids = torch.zeros(max(int(at[-1]), 1), dtype=torch.int32, device="cuda")
+    cnt = torch.zeros(len(strings), dtype=torch.int32, device="cuda")
+    assert lib.aotx_text_encode(d.data_ptr(), a.data_ptr(), len(strings), ids.data_ptr(),
+                                cnt.data_ptr(), None) == 0
+    ids, cnt = ids.cpu().numpy(), cnt.cpu().numpy()
+    return [list(ids[int(at[i]):int(at[i]) + int(cnt[i])]) for i in range(len(strings))]
+
+
+def _detok(torch, lib, seqs, limit=4096):
+    at = np.zeros(len(seqs) + 1, dtype=np.uint64)
+    at[1:] = np.cumsum([len(s) for s in seqs])
+    flat = np.asarray([x for s in seqs for x in s] or [0], dtype=np.int32)
+    ids = torch.from_numpy(flat).cuda()
+    a = torch.from_numpy(at.view(np.int64)).cuda()
+    out = torch.zeros(len(seqs) * limit, dtype=torch.uint8, device="cuda")
+    ln = torch.zeros(len(seqs), dtype=torch.int32, device="cuda")
+    assert lib.aotx_text_detok(ids.data_ptr(), a.data_ptr(), len(seqs), out.data_ptr(), limit,
+                               ln.data_ptr(), None) == 0
+    torch.cuda.synchronize()
+    o, ln = out.cpu().numpy(), ln.cpu().numpy()
+    return [bytes(o[i * limit:i * limit + int(ln[i])]) for i in range(len(seqs))]
+
+
+@pytest.mark.parametrize("family", ["gpt-2", "llama3", "qwen2", "qwen35"])
+def test_encode_detok_vs_oracle(torch, lib, bpe, family):
+    tokens, merges, _ = bpe
+    types = [1] * len(tokens)
+    v = Vocab(tokens, merges, types, family=family)
+    built = Built(lib, tokens, merges, types, family)
+    try:
+        rep = (ctypes.c_uint32 * 4)()
+        assert lib.aotx_text_vocab_report(rep) == 0
+        assert rep[0] == len(tokens) and rep[1] == len(merges) and rep[2] == 0
+        rng = random.Random(21 + ROWS[family])
+        strings = [text(rng, rng.randint(1, 60)) for _ in range(200)] + ["", "a", " ", "\n\n\n"]
+        got = _encode(torch, lib, strings)
+        for s, g in zip(strings, got):
+            assert g == v.encode(s.encode()), (family, repr(s))
+        back = _detok(torch, lib, got)
+        assert back == [s.encode() for s in strings]
+    finally:
+        built.close()
+
+
+def test_long_piece_and_control(torch, lib, bpe):
+    """A letter run longer than the chunk bound is cut and still decodes to itself; a
+    control token gives no bytes."""
+    tokens, merges, _ = bpe
+    types = [1] * len(tokens)
+    v = Vocab(tokens, merges, types, family="gpt-2")
+    ids = v.encode(b"hello world")
+    types[ids[0]] = aotx_amd.AOTX_SEQ_STATE_DONE   # 3: the control type
+    built = Built(lib, tokens, merges, types, "gpt-2")
+    try:
+        long = "ab" * 3000 + " tail"
+        got = _encode(torch, lib, [long])[0]
+        assert 0 < len(got) < len(long)
+        assert _detok(torch, lib, [got], limit=8192)[0] == long.encode()
+        assert _detok(torch, lib, [got], limit=100)[0] == long.encode()[:100]   # cut at limit
+        assert _detok(torch, lib, [ids])[0] == Vocab(tokens, merges, family="gpt-2").decode(ids[1:])
+    finally:
+        built.close()
