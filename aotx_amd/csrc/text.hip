@@ -137,6 +137,9 @@ struct aotx_text_vocab {
     const unsigned int *pair_rank;
     const unsigned int *pair_result;
     const unsigned int *control;        /* one bit per token */
+    const unsigned int *special;        /* tokens of the control and user types */
+    unsigned int specials;
+    unsigned long long first[4];        /* bits of the first bytes of the specials */
     unsigned int pattern;
     unsigned int whole;
     unsigned int byte_token[256];
@@ -304,19 +307,51 @@ static __device__ unsigned int match(unsigned int pattern, const unsigned char *
     return spaces(b, end, at, span, 1);
 }
 
-/* one thread per text: pre-token p of text t is (start[at[t] + p], len[at[t] + p]) */
-__global__ void aotx_text_pretok_kernel(const unsigned char *bytes, const unsigned long long *at,
-                                        unsigned int texts, unsigned int pattern,
-                                        unsigned int *start, unsigned int *len, unsigned int *pieces)
+/* The longest special token whose bytes start at `at` (cuda/text/pretok.cu:339-372): its
+ * length, 0 for none. */
+static __device__ unsigned int special_at(const aotx_text_vocab &v, const unsigned char *b,
+                                          unsigned int at, unsigned int end, unsigned int *token)
+{
+    const unsigned int c = b[at];
+    if (((v.first[c >> 6] >> (c & 63u)) & 1ull) == 0ull) return 0u;
+    unsigned int best = 0u;
+    for (unsigned int i = 0u; i < v.specials; ++i) {
+        const unsigned int id = v.special[i];
+        const unsigned long long f = v.token_at[id];
+        const unsigned int n = (unsigned int)(v.token_at[id + 1u] - f);
+        if (n <= best || at + n > end) continue;
+        unsigned int k = 0u;
+        while (k < n && v.token_bytes[f + k] == b[at + k]) k += 1u;
+        if (k == n) { best = n; *token = id; }
+    }
+    return best;
+}
+
+/* one thread per text: pre-token p of text t is (start[at[t] + p], len[at[t] + p]), and
+ * tok[at[t] + p] its token when it is a special token (else AOTX_TEXT_NONE). A special
+ * token is a whole match and the pattern reads no text across it. */
+__global__ void aotx_text_pretok_kernel(aotx_text_vocab v, const unsigned char *bytes,
+                                        const unsigned long long *at, unsigned int texts,
+                                        unsigned int *start, unsigned int *len, unsigned int *tok,
+                                        unsigned int *pieces)
 {
     const unsigned int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= texts) return;
     const unsigned long long base = at[t];
     const unsigned char *b = bytes + base;
-    const unsigned int end = (unsigned int)(at[t + 1u] - base);
+    const unsigned int text_end = (unsigned int)(at[t + 1u] - base);
     unsigned int pos = 0u, n = 0u;
-    while (pos < end) {
-        unsigned int m = match(pattern, b, pos, end);
+    while (pos < text_end) {
+        unsigned int stop = pos, special = 0u, id = AOTX_TEXT_NONE;
+        while (stop < text_end && v.specials != 0u) {
+            special = special_at(v, b, stop, text_end, &id);
+            if (special != 0u) break;
+            stop += 1u;
+        }
+        if (v.specials == 0u) stop = text_end;
+        const unsigned int end = stop;
+        while (pos < end) {
+        unsigned int m = match(v.pattern, b, pos, end);
         if (m == 0u) m = 1u;
         if (m > AOTX_TEXT_CHUNK_BYTES) {          /* cut at a character boundary */
             unsigned int cut = 0u;
@@ -330,8 +365,17 @@ __global__ void aotx_text_pretok_kernel(const unsigned char *bytes, const unsign
         }
         start[base + n] = pos;
         len[base + n] = m;
+        tok[base + n] = AOTX_TEXT_NONE;
         n += 1u;
         pos += m;
+        }
+        if (special != 0u) {
+            start[base + n] = stop;
+            len[base + n] = special;
+            tok[base + n] = id;
+            n += 1u;
+            pos = stop + special;
+        }
     }
     pieces[t] = n;
 }
@@ -343,6 +387,7 @@ __global__ void aotx_text_pretok_kernel(const unsigned char *bytes, const unsign
 __global__ __launch_bounds__(64) void aotx_text_merge_kernel(aotx_text_vocab v, const unsigned char *bytes,
                                                              const unsigned long long *at, unsigned int texts,
                                                              const unsigned int *start, const unsigned int *len,
+                                                             const unsigned int *ptok,
                                                              const unsigned int *pieces, unsigned int *out,
                                                              unsigned int *out_count)
 {
@@ -362,6 +407,10 @@ __global__ __launch_bounds__(64) void aotx_text_merge_kernel(aotx_text_vocab v, 
     const unsigned int n = len[s];
     /* a pre-token's tokens (never more than its bytes) go where its bytes are */
     unsigned int *dst = out + at[t] + start[s];
+    if (ptok[s] != AOTX_TEXT_NONE) {
+        if (lane == 0u) { dst[0] = ptok[s]; out_count[s] = 1u; }
+        return;
+    }
     if (v.whole) {
         const unsigned int w = lane == 0u ? find_bytes(v, b, n) : 0u;
         const unsigned int whole = __shfl(w, 0, 64);
@@ -608,6 +657,15 @@ extern "C" int aotx_text_vocab_build(const aotx_text_source *src, aotx_text_stor
             if (src->token_type[t] == AOTX_TEXT_TYPE_CONTROL) { control[t >> 5] |= 1u << (t & 31u); controls += 1u; }
     aotx_text_vocab v;
     memset(&v, 0, sizeof v);
+    std::vector<unsigned int> special;
+    if (src->token_type != nullptr)
+        for (unsigned int t = 0; t < n; ++t)
+            if ((src->token_type[t] == AOTX_TEXT_TYPE_CONTROL || src->token_type[t] == AOTX_TEXT_TYPE_USER)
+                && src->token_at[t + 1u] > src->token_at[t]) {
+                special.push_back(t);
+                const unsigned int c = src->token_bytes[src->token_at[t]];
+                v.first[c >> 6] |= 1ull << (c & 63u);
+            }
     for (unsigned int b = 0; b < 256u; ++b) {
         unsigned char u[4];
         const unsigned int k = utf8_put(byte_point(b), u);
@@ -626,6 +684,8 @@ extern "C" int aotx_text_vocab_build(const aotx_text_source *src, aotx_text_stor
     v.pair_rank = store_put(store, rank.data(), pairs);
     v.pair_result = store_put(store, result.data(), pairs);
     v.control = store_put(store, control.data(), control.size());
+    v.special = store_put(store, special.data(), special.size());
+    v.specials = (unsigned int)special.size();
     v.pattern = kFamilies[src->family].pattern;
     v.whole = kFamilies[src->family].whole;
     g_vocab = v;
@@ -658,17 +718,19 @@ extern "C" int aotx_text_encode(const unsigned char *bytes, const unsigned long 
         AOTX_CHECK(hipStreamSynchronize(s));
         return 0;
     }
-    unsigned int *start = nullptr, *len = nullptr, *pieces = nullptr, *ptok = nullptr, *pcount = nullptr;
+    unsigned int *start = nullptr, *len = nullptr, *pieces = nullptr, *ptok = nullptr, *pcount = nullptr,
+                 *pspecial = nullptr;
     AOTX_CHECK(hipMallocAsync((void **)&start, total * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&len, total * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&ptok, total * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&pcount, total * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&pieces, texts * 4u, s));
-    hipLaunchKernelGGL(aotx_text_pretok_kernel, dim3((texts + 63u) / 64u), dim3(64), 0, s, bytes, at, texts,
-                       g_vocab.pattern, start, len, pieces);
+    AOTX_CHECK(hipMallocAsync((void **)&pspecial, total * 4u, s));
+    hipLaunchKernelGGL(aotx_text_pretok_kernel, dim3((texts + 63u) / 64u), dim3(64), 0, s, g_vocab, bytes, at,
+                       texts, start, len, pspecial, pieces);
     AOTX_LAUNCH_CHECK();
     hipLaunchKernelGGL(aotx_text_merge_kernel, dim3((unsigned int)total), dim3(64), 0, s, g_vocab, bytes, at,
-                       texts, start, len, pieces, ptok, pcount);
+                       texts, start, len, pspecial, pieces, ptok, pcount);
     AOTX_LAUNCH_CHECK();
     hipLaunchKernelGGL(aotx_text_gather_kernel, dim3(texts), dim3(64), 0, s, at, start, pieces, ptok, pcount,
                        ids, count);
@@ -678,6 +740,7 @@ extern "C" int aotx_text_encode(const unsigned char *bytes, const unsigned long 
     AOTX_CHECK(hipFreeAsync(ptok, s));
     AOTX_CHECK(hipFreeAsync(pcount, s));
     AOTX_CHECK(hipFreeAsync(pieces, s));
+    AOTX_CHECK(hipFreeAsync(pspecial, s));
     AOTX_CHECK(hipStreamSynchronize(s));
     return 0;
 }

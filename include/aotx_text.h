@@ -12,6 +12,7 @@ extern "C" {
 #define AOTX_TEXT_NONE        0xFFFFFFFFu   /* no token / no rank: cuda/text/text.cuh:14 */
 #define AOTX_TEXT_CHUNK_BYTES 4096u         /* longest pre-token merged whole: text.cuh:24 */
 #define AOTX_TEXT_TYPE_CONTROL 3            /* token types of the model file: text.cuh:41-43 */
+#define AOTX_TEXT_TYPE_USER    4
 
 /* Split patterns: the rows of cuda/text/families.h:10-14, in that order. */
 #define AOTX_TEXT_PATTERN_QWEN2  0u
@@ -63,9 +64,11 @@ int aotx_text_vocab_report(unsigned int report[4]);
  * bpe.cu:44-223: one thread per text cuts the pre-tokens (a pre-token longer than
  * AOTX_TEXT_CHUNK_BYTES is cut at a character boundary and the rest is matched again),
  * one wave per pre-token merges it (the lowest pair rank first, the leftmost of equal
- * ranks; with the family's whole rule a pre-token that is a token stays whole). Text is
- * taken as UTF-8; special tokens are not matched inside text. Returns 1 with no
- * vocabulary or a bad argument; synchronous. */
+ * ranks; with the family's whole rule a pre-token that is a token stays whole). Tokens
+ * of the control and user types are whole matches found first, the longest at the
+ * leftmost place (cuda/text/pretok.cu:339-372, :404-431); the pattern reads no text across
+ * them. Text is taken as UTF-8. Returns 1 with no vocabulary or a bad argument;
+ * synchronous. */
 int aotx_text_encode(const unsigned char *bytes, const unsigned long long *at, unsigned int texts,
                      unsigned int *ids, unsigned int *count, void *stream);
 

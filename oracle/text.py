@@ -60,6 +60,9 @@ class Vocab:
                 self.rank.setdefault((self.id[left], self.id[right]), (r, self.id[left + right]))
         self.types = list(types) if types is not None else [1] * len(self.tokens)
         self.pattern, self.whole = FAMILY[family]
+        # tokens of the control (3) and user (4) types: whole matches found first
+        self.specials = [(t.encode("utf-8"), i) for i, t in enumerate(self.tokens)
+                         if self.types[i] in (3, 4) and t]
 
     def merge(self, piece_bytes):
         s = byte_string(piece_bytes)
@@ -78,11 +81,33 @@ class Vocab:
             sym[i:i + 2] = [res]
         return sym
 
+    def special_at(self, data, at):
+        """The longest special token starting at `at` (pretok.cu:339-372): (length, id)."""
+        best = (0, None)
+        for s, i in self.specials:
+            if len(s) > best[0] and data.startswith(s, at):
+                best = (len(s), i)
+        return best
+
     def encode(self, data):
-        """Token ids of UTF-8 bytes."""
-        out = []
-        for piece in pretokens(data.decode("utf-8"), self.pattern):
-            out += self.merge(piece.encode("utf-8"))
+        """Token ids of UTF-8 bytes: the leftmost special token splits the text, the
+        pattern and the merges run on the text between (pretok.cu:404-431)."""
+        out, pos = [], 0
+        while pos < len(data):
+            stop, (n, sid) = pos, (0, None)
+            while stop < len(data) and self.specials:
+                n, sid = self.special_at(data, stop)
+                if n:
+                    break
+                stop += 1
+            if not self.specials:
+                stop = len(data)
+            for piece in pretokens(data[pos:stop].decode("utf-8"), self.pattern):
+                out += self.merge(piece.encode("utf-8"))
+            pos = stop
+            if n:
+                out.append(sid)
+                pos = stop + n
         return out
 
     def decode(self, ids):

@@ -77,3 +77,31 @@ def test_family_table(lib):
     for i, n in enumerate(names):
         assert lib.aotx_text_family_find(n.encode(), len(n), ctypes.byref(row)) == 0 and row.value == i
     assert lib.aotx_text_family_find(b"nope", 4, ctypes.byref(row)) == 1
+
+
+SPECIALS = ["<|eot|>", "<|start|>", "<|s"]
+
+
+def with_specials(tokens, merges):
+    """The trained vocabulary plus three special tokens (two control, one user type, one a
+    prefix of another so that the longest match decides)."""
+    toks = list(tokens) + SPECIALS
+    types = [1] * len(tokens) + [3, 3, 4]
+    return toks, types
+
+
+@pytest.mark.parametrize("family", ["gpt-2", "llama3"])
+def test_special_tokens_match_tokenizers_library(bpe, family):
+    from tokenizers import AddedToken
+    tokens, merges, _ = bpe
+    toks, types = with_specials(tokens, merges)
+    pattern, whole = FAMILY[family]
+    hf = hf_with(PATTERNS[pattern], tokens, merges, whole)
+    hf.add_special_tokens([AddedToken(t, special=True, normalized=False) for t in SPECIALS])
+    assert [hf.token_to_id(t) for t in SPECIALS] == [len(tokens), len(tokens) + 1, len(tokens) + 2]
+    v = Vocab(toks, merges, types, family=family)
+    rng = random.Random(15)
+    for _ in range(200):
+        parts = [text(rng, rng.randint(0, 8)) for _ in range(3)]
+        s = rng.choice(SPECIALS).join(parts) + rng.choice(["", "<|start|>x", "<|sx", "<|"])
+        assert v.encode(s.encode()) == hf.encode(s).ids, repr(s)

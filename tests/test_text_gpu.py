@@ -122,3 +122,29 @@ def test_long_piece_and_control(torch, lib, bpe):
         assert _detok(torch, lib, [ids])[0] == Vocab(tokens, merges, family="gpt-2").decode(ids[1:])
     finally:
         built.close()
+
+
+@pytest.mark.parametrize("family", ["gpt-2", "llama3"])
+def test_special_tokens_vs_oracle(torch, lib, bpe, family):
+    """Control and user tokens are whole matches (longest at the leftmost place); control
+    tokens give no bytes back, user tokens give their text."""
+    from tests.test_text import SPECIALS, with_specials
+    tokens, merges, _ = bpe
+    toks, types = with_specials(tokens, merges)
+    v = Vocab(toks, merges, types, family=family)
+    built = Built(lib, toks, merges, types, family)
+    try:
+        rng = random.Random(31)
+        strings = []
+        for _ in range(150):
+            parts = [text(rng, rng.randint(0, 8)) for _ in range(3)]
+            strings.append(rng.choice(SPECIALS).join(parts) + rng.choice(["", "<|start|>x", "<|sx", "<|"]))
+        got = _encode(torch, lib, strings)
+        for s, g in zip(strings, got):
+            assert g == v.encode(s.encode()), (family, repr(s))
+        back = _detok(torch, lib, got)
+        assert back == [v.decode(g) for g in got]
+        assert _detok(torch, lib, [[len(tokens) + 2]])[0] == b"<|s"      # user type: its text
+        assert _detok(torch, lib, [[len(tokens)]])[0] == b""             # control type: nothing
+    finally:
+        built.close()
