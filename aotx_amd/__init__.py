@@ -206,6 +206,7 @@ PROTOTYPES = {
     "aotx_text_vocab_build": (i32, [ctypes.POINTER(TextSource), ctypes.POINTER(TextStore)]),
     "aotx_text_vocab_release": (None, [ctypes.POINTER(TextStore)]),
     "aotx_text_vocab_report": (i32, [ctypes.POINTER(u32)]),
+    "aotx_text_vocab_file": (i32, [vp, ctypes.POINTER(TextStore)]),
     "aotx_text_encode": (i32, [vp, vp, u32, vp, vp, vp]),
     "aotx_text_detok": (i32, [vp, vp, u32, vp, u32, vp, vp]),
     "aotx_kv_open": (i32, [ctypes.POINTER(KvMap)]),

@@ -18,6 +18,7 @@
 #include "aotx_internal.h"
 #include "unicode_classes.h"
 #include "../../include/aotx_text.h"
+#include "../../include/aotx_modelfile.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -695,6 +696,36 @@ extern "C" int aotx_text_vocab_build(const aotx_text_source *src, aotx_text_stor
     g_report[2] = refused;
     g_report[3] = controls;
     return 0;
+}
+
+extern "C" int aotx_text_vocab_file(const aotx_modelfile *file, aotx_text_store *store)
+{
+    if (file == nullptr || store == nullptr) return 1;
+    aotx_string_array tokens, merges;
+    memset(&merges, 0, sizeof merges);
+    if (aotx_modelfile_strings(file, "tokenizer.ggml.tokens", &tokens) != 0) return 1;
+    if (aotx_modelfile_strings(file, "tokenizer.ggml.merges", &merges) != 0) merges.count = 0u;
+    const int32_t *types = nullptr;
+    uint64_t type_count = 0u;
+    if (aotx_modelfile_i32s(file, "tokenizer.ggml.token_type", &types, &type_count) != 0
+        || type_count != tokens.count)
+        types = nullptr;
+    const char *pre = nullptr;
+    size_t pre_len = 0u;
+    unsigned int family = 0u;                       /* row 0 when the file names none */
+    if (aotx_modelfile_string(file, "tokenizer.ggml.pre", &pre, &pre_len) == 0
+        && aotx_text_family_find(pre, pre_len, &family) != 0)
+        return 1;
+    aotx_text_source src;
+    src.token_bytes = tokens.bytes;
+    src.token_at = (const unsigned long long *)tokens.offsets;
+    src.tokens = tokens.count;
+    src.merge_bytes = merges.count ? merges.bytes : nullptr;
+    src.merge_at = merges.count ? (const unsigned long long *)merges.offsets : nullptr;
+    src.merges = merges.count;
+    src.token_type = types;
+    src.family = family;
+    return aotx_text_vocab_build(&src, store);
 }
 
 extern "C" int aotx_text_vocab_report(unsigned int report[4])

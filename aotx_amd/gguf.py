@@ -66,7 +66,7 @@ def write(path, metadata, tensors, alignment=32):
             pos = off + len(data)
 
 
-def export(shape, region, lay, path, arch=None):
+def export(shape, region, lay, path, arch=None, tokenizer=None):
     """Write the synthetic model of `lay` (aotx_amd.model.layout / build_host: the same
     bytes) as a GGUF file with the reference's tensor names (cuda/model/names.h,
     kinds_data.h): llama (adjacent rotary pairs) or qwen3 (split pairs, Q/K norm)."""
@@ -122,6 +122,13 @@ def export(shape, region, lay, path, arch=None):
             (f"{arch}.attention.layer_norm_rms_epsilon", F32, shape.eps)]
     if e:
         meta += [(f"{arch}.expert_count", U32, e), (f"{arch}.expert_used_count", U32, shape.used)]
+    if tokenizer is not None:
+        # (tokens, merges "left right", token types, tokenizer.ggml.pre value)
+        toks, merges, types, pre = tokenizer
+        meta += [("tokenizer.ggml.model", STRING, "gpt2"), ("tokenizer.ggml.pre", STRING, pre),
+                 ("tokenizer.ggml.tokens", ARRAY, (STRING, list(toks))),
+                 ("tokenizer.ggml.token_type", ARRAY, (I32, [int(t) for t in types])),
+                 ("tokenizer.ggml.merges", ARRAY, (STRING, list(merges)))]
     write(path, meta, tensors)
 
 

@@ -54,6 +54,13 @@ int aotx_text_family_find(const char *name, unsigned long long length, unsigned 
 int aotx_text_vocab_build(const aotx_text_source *source, aotx_text_store *store);
 void aotx_text_vocab_release(aotx_text_store *store);
 
+/* Build the vocabulary from an open model file (include/aotx_modelfile.h):
+ * tokenizer.ggml.tokens, .merges, .token_type and .pre (family row 0 when absent), as the
+ * reference's load reads them into aotx_text_source. Returns 1 when the file has no
+ * tokens, names an unknown family, or the build refuses the arrays. */
+struct aotx_modelfile;
+int aotx_text_vocab_file(const struct aotx_modelfile *file, aotx_text_store *store);
+
 /* Counts of the last build: tokens, merges taken, merges refused (a side or the merged
  * string is not a token), control tokens. */
 int aotx_text_vocab_report(unsigned int report[4]);

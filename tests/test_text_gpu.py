@@ -148,3 +148,44 @@ def test_special_tokens_vs_oracle(torch, lib, bpe, family):
         assert _detok(torch, lib, [[len(tokens)]])[0] == b""             # control type: nothing
     finally:
         built.close()
+
+
+def test_text_end_to_end_from_gguf(torch, orc, bpe, tmp_path):
+    """Text in, text out: a GGUF file carrying the tiny model and a tokenizer; the prompt
+    encoded on the GPU (as the oracle does), a prompt pass and greedy steps through the
+    model, the reply decoded on the GPU (as the oracle does)."""
+    from aotx_amd import gguf
+    from aotx_amd.model import TINY, Runtime, build_host
+    from aotx_amd.text import Tokenizer
+    from tests.gpu_util import rel_rms
+    tokens, merges, _ = bpe
+    pad = TINY.vocab - len(tokens)
+    toks = list(tokens) + [f"<unused_{i}>" for i in range(pad)]
+    types = [1] * len(tokens) + [3] * pad
+    region, lay = build_host(TINY, seed=1)
+    path = tmp_path / "tiny_text.gguf"
+    gguf.export(TINY, region, lay, path, tokenizer=(toks, merges, types, "llama-bpe"))
+    region_f, desc = gguf.load(path)
+    v = Vocab(toks, merges, types, family="llama3")
+    tk = Tokenizer(path=path)
+    rt = Runtime(region_f, desc, max_tokens=64, pool_pages=64)
+    try:
+        prompt = "hello world, it's the café 12345 <unused_3> дом"
+        ids = tk.encode([prompt])[0]
+        assert ids == v.encode(prompt.encode()) and 0 < len(ids) < 64
+        ref = orc.Model(lay.desc, region, slots=8, max_context=128)
+        tok, _, logits = rt.step(ids, [0, len(ids)], [2])
+        want = ref.step(ids, [0, len(ids)], [2])
+        assert rel_rms(logits, want) < 1e-2
+        reply = [int(np.argmax(want[0]))]
+        for _ in range(7):
+            tok, _, logits = rt.step([reply[-1]], [0, 1], [2])
+            want = ref.step([reply[-1]], [0, 1], [2])
+            assert rel_rms(logits, want) < 1e-2
+            reply.append(int(np.argmax(want[0])))
+        assert tk.decode([reply])[0] == v.decode(reply)
+        assert tk.decode([ids])[0] == v.decode(ids)
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+        tk.close()
