@@ -109,7 +109,14 @@ AOTX_SEQ_STATE_FREE, AOTX_SEQ_STATE_PREFILL, AOTX_SEQ_STATE_DECODE, AOTX_SEQ_STA
 class PlanSlot(ctypes.Structure):
     """include/aotx_plan.h aotx_plan_slot (the reference's aotx_seq fields the plan reads)."""
     _fields_ = [("state", u32), ("role", u32), ("prompt", u32), ("sampled", u32),
-                ("limit", u32), ("page_limit", u32), ("seed", u64), ("sample", ModelHow)]
+                ("limit", u32), ("page_limit", u32), ("seed", u64), ("sample", ModelHow),
+                ("stop", u32), ("flags", u32), ("last", u32), ("reserved", u32), ("draw", u64)]
+
+
+class TokenRecord(ctypes.Structure):
+    """include/aotx_plan.h aotx_token_record (cuda/seam/wire.h:190-200 without the text)."""
+    _fields_ = [("slot", u32), ("token", u32), ("position", u32), ("flags", u32), ("seed", u64),
+                ("draw", u64), ("role", u32), ("reserved", u32)]
 
 
 class PlanState(ctypes.Structure):
@@ -118,8 +125,9 @@ class PlanState(ctypes.Structure):
         ("ids", i32 * AOTX_SEQ_TICK_BUDGET), ("offset", u32 * (AOTX_SLOTS + 1)),
         ("agent", u32 * AOTX_SLOTS), ("how", ModelHow * AOTX_SLOTS), ("rows", u32 * AOTX_SLOTS),
         ("first", u32 * AOTX_SLOTS), ("place", u32 * AOTX_SLOTS), ("asked", u32 * AOTX_SLOTS),
-        ("cursor", u32 * AOTX_MODEL_ROLES), ("seqs", u32), ("tokens", u32), ("waited", u32),
-        ("short_of", u32), ("steps", u64),
+        ("kept", u32 * AOTX_SLOTS), ("cursor", u32 * AOTX_MODEL_ROLES), ("seqs", u32),
+        ("tokens", u32), ("waited", u32), ("short_of", u32), ("steps", u64), ("records", u32),
+        ("reserved", u32),
     ]
 
 
@@ -201,6 +209,7 @@ PROTOTYPES = {
     # the tick plan (include/aotx_plan.h)
     "aotx_decode_plan": (i32, [u32, vp, vp, u32, u32, u32, vp, vp]),
     "aotx_model_kv_pages": (u32, [u32, u32]),
+    "aotx_decode_commit": (i32, [u32, vp, vp, u32, vp, vp, vp, vp, u32, vp]),
     # the tokenizer (include/aotx_text.h)
     "aotx_text_family_find": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(u32)]),
     "aotx_text_vocab_build": (i32, [ctypes.POINTER(TextSource), ctypes.POINTER(TextStore)]),

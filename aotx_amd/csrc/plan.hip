@@ -144,3 +144,100 @@ extern "C" int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, 
     AOTX_LAUNCH_CHECK();
     return 0;
 }
+
+/* ---- commit (cuda/model/commit.cu:102-201) ------------------------------------------------ */
+
+__global__ __launch_bounds__(64) void aotx_commit_kernel(unsigned int role, aotx_plan_slot *slots,
+                                                         int *tokens, unsigned int stride,
+                                                         const int *token, const unsigned int *draw,
+                                                         aotx_state *st, aotx_plan_state *p,
+                                                         aotx_token_record *rec, unsigned int cap)
+{
+    const unsigned int slot = threadIdx.x;
+    aotx_plan_slot &seq = slots[slot];
+    unsigned int journal = 0u, from = 0u, extra = 0u, tok = 0u, mark = 0u;
+    unsigned long long drawn = 0ull;
+    if (seq.role == role) {
+        if (seq.state == AOTX_SEQ_STATE_DONE) {
+            if (aotx_kv_put(&st->kv, slot, 0u)) st->kv.count[slot] = 0u;   /* pages back */
+            seq.state = AOTX_SEQ_STATE_FREE;
+            p->asked[slot] = 0u;
+        } else if (seq.state == AOTX_SEQ_STATE_PREFILL || seq.state == AOTX_SEQ_STATE_DECODE) {
+            const unsigned int rows = p->rows[slot];
+            const unsigned int list = seq.prompt + seq.sampled;
+            const unsigned int end = p->first[slot] + rows;
+            const unsigned int kept = p->kept[slot];
+            journal = end > kept ? end - kept : 0u;
+            from = kept;
+            /* the draw of a sequence's last row follows the list once all of it is in pages */
+            if (rows > 0u && end == list && list < AOTX_SEQ_MAX_TOKENS_PLAN) {
+                const unsigned int place = p->place[slot];
+                tok = (unsigned int)token[place];
+                drawn = draw[place];
+                extra = 1u;
+            }
+            if (rows > 0u) seq.state = end == list ? AOTX_SEQ_STATE_DECODE : AOTX_SEQ_STATE_PREFILL;
+            if (extra != 0u) {
+                mark = AOTX_TOKEN_SAMPLED;
+                if (list < stride) tokens[(unsigned long long)slot * stride + list] = (int)tok;
+                seq.sampled += 1u;
+                seq.last = tok;
+                seq.draw = drawn;
+                if (tok == seq.stop || seq.sampled >= seq.limit || (seq.flags & AOTX_DECODE_MARK_STOP) != 0u
+                    || list + 1u >= AOTX_SEQ_MAX_TOKENS_PLAN) {
+                    mark |= AOTX_TOKEN_LAST;
+                    seq.flags |= AOTX_TOKEN_LAST;
+                    seq.state = AOTX_SEQ_STATE_DONE;
+                }
+            }
+            p->kept[slot] = kept + journal + extra;
+            if ((seq.flags & AOTX_DECODE_MARK_STOP) != 0u) seq.state = AOTX_SEQ_STATE_DONE;
+        }
+    }
+    /* the tick's records: slots in order, each its list tokens then its sampled token */
+    const unsigned int mine = journal + extra;
+    const unsigned int scan = plan_scan(mine);
+    const unsigned int first = scan - mine;
+    for (unsigned int i = 0u; i < journal; ++i) {
+        const unsigned int r = first + i, at = from + i;
+        if (r >= cap) break;
+        aotx_token_record x;
+        x.slot = slot;
+        x.token = at < stride ? (unsigned int)tokens[(unsigned long long)slot * stride + at] : 0u;
+        x.position = at;
+        x.flags = AOTX_TOKEN_PROMPT;
+        x.seed = seq.seed;
+        x.draw = 0ull;
+        x.role = role;
+        x.reserved = 0u;
+        rec[r] = x;
+    }
+    if (extra != 0u && first + journal < cap) {
+        aotx_token_record x;
+        x.slot = slot;
+        x.token = tok;
+        x.position = seq.prompt + seq.sampled - 1u;
+        x.flags = mark;
+        x.seed = seq.seed;
+        x.draw = drawn;
+        x.role = role;
+        x.reserved = 0u;
+        rec[first + journal] = x;
+    }
+    const unsigned int total = __shfl(scan, 63, 64);
+    if (slot == 0u) p->records = total < cap ? total : cap;
+}
+
+extern "C" int aotx_decode_commit(unsigned int role, aotx_plan_slot *slots, int *tokens,
+                                  unsigned int stride, const int *token, const unsigned int *draw,
+                                  aotx_plan_state *plan, aotx_token_record *records,
+                                  unsigned int capacity, void *stream)
+{
+    if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || token == nullptr
+        || draw == nullptr || plan == nullptr || stride == 0u || (records == nullptr && capacity != 0u))
+        return 1;
+    hipLaunchKernelGGL(aotx_commit_kernel, dim3(1), dim3(64), 0, aotx_stream(stream), role, slots,
+                       tokens, stride, token, draw, aotx_state_device(), plan, records, capacity);
+    AOTX_LAUNCH_CHECK();
+    return 0;
+}

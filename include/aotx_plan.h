@@ -35,7 +35,33 @@ typedef struct aotx_plan_slot {
     unsigned int page_limit;   /* pages the slot may hold (0: no limit) */
     unsigned long long seed;
     aotx_model_how sample;
+    unsigned int stop;         /* the token that ends the reply (AOTX_PLAN_NO_STOP: none) */
+    unsigned int flags;        /* AOTX_TOKEN_LAST once ended; AOTX_DECODE_MARK_STOP: stop now */
+    unsigned int last;         /* the last sampled token */
+    unsigned int reserved;
+    unsigned long long draw;   /* the draw count of that token */
 } aotx_plan_slot;
+
+#define AOTX_PLAN_NO_STOP      0xFFFFFFFFu
+#define AOTX_SEQ_MAX_TOKENS_PLAN 8192u     /* a list's tokens at most (AOTX_SEQ_MAX_TOKENS) */
+#define AOTX_DECODE_MARK_STOP  0x0100u    /* cuda/model/decode_state.cuh:22 */
+/* Token record flags: cuda/seam/wire.h:186-188. */
+#define AOTX_TOKEN_PROMPT      0x0001u
+#define AOTX_TOKEN_SAMPLED     0x0002u
+#define AOTX_TOKEN_LAST        0x0004u
+
+/* One token record of a tick (the reference's aotx_token_body, cuda/seam/wire.h:190-200,
+ * without the detokenized text): what a journal replay needs to rebuild the list. */
+typedef struct aotx_token_record {
+    unsigned int slot;
+    unsigned int token;
+    unsigned int position;     /* in the slot's list, from 0 */
+    unsigned int flags;        /* AOTX_TOKEN_* */
+    unsigned long long seed;
+    unsigned long long draw;   /* 0 for a prompt token */
+    unsigned int role;
+    unsigned int reserved;
+} aotx_token_record;
 
 /* The batch of one tick and the plan's marks (cuda/model/decode_state.cuh:35-55 without
  * the multimodal input rows and the role/replay gates; asked is aotx_seq_asked,
@@ -49,12 +75,15 @@ typedef struct aotx_plan_state {
     unsigned int first[AOTX_SLOTS];         /* the list position of the first of them */
     unsigned int place[AOTX_SLOTS];         /* the slot's sequence, or AOTX_SLOTS */
     unsigned int asked[AOTX_SLOTS];         /* pages each slot has asked the pool for */
+    unsigned int kept[AOTX_SLOTS];          /* tokens of each list already recorded */
     unsigned int cursor[AOTX_MODEL_ROLES];  /* the rotating first slot of each role */
     unsigned int seqs;                      /* sequences of this tick's batch */
     unsigned int tokens;                    /* rows of this tick's batch */
     unsigned int waited;                    /* prefill pieces that got no room, summed */
     unsigned int short_of;                  /* slots that waited for pages, summed */
     unsigned long long steps;               /* ticks that gave a batch of one row or more */
+    unsigned int records;                   /* token records of the last commit */
+    unsigned int reserved;
 } aotx_plan_state;
 
 /* Plan one tick of `role` (cuda/model/plan.cu:54-199): every slot of the role in state
@@ -71,6 +100,20 @@ typedef struct aotx_plan_state {
 int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, const int *tokens,
                      unsigned int stride, unsigned int budget, unsigned int pool_pages,
                      aotx_plan_state *plan, void *stream);
+
+/* Close the tick of `role` (cuda/model/commit.cu:102-201) after the step ran on the plan's
+ * batch: token[place] and draw[place] (device) are the step's outputs. Per slot of the
+ * role, in slot order: a DONE slot gives its pages back (a release request) and becomes
+ * FREE; a slot that gave rows moves to DECODE when its whole list is in the pages (else
+ * stays PREFILL), and then takes the sampled token into its list (slots, tokens [stride]
+ * are updated in place), ending (DONE, AOTX_TOKEN_LAST) on its stop token, its limit, the
+ * list bound or a stop mark. The records of the tick (the list tokens not yet recorded,
+ * then the sampled token) go to records[0 .. plan->records), slots in order, at most
+ * capacity. One wave; asynchronous on the stream. Returns 1 for a bad argument. */
+int aotx_decode_commit(unsigned int role, aotx_plan_slot *slots, int *tokens,
+                       unsigned int stride, const int *token, const unsigned int *draw,
+                       aotx_plan_state *plan, aotx_token_record *records,
+                       unsigned int capacity, void *stream);
 
 /* Pages a slot of `role` needs for a context of `context` positions (the reference's
  * aotx_kvl_pages over the role's KV shape, cuda/model/kv_layout.cuh); 0 when the role has

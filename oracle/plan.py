@@ -35,6 +35,7 @@ class Plan:
     def __init__(self, roles=5):
         self.cursor = [0] * roles
         self.asked = [0] * SLOTS
+        self.kept = [0] * SLOTS
         self.waited = 0
         self.short_of = 0
         self.steps = 0
@@ -117,3 +118,53 @@ class Plan:
             self.steps += 1
             self.cursor[role] = (self.cursor[role] + 1) % SLOTS
         return out
+
+PROMPT, SAMPLED, LAST, MARK_STOP = 0x1, 0x2, 0x4, 0x100
+SEQ_MAX = 8192
+
+
+def commit(plan, role, slots, tokens, out, token, draw, kv):
+    """cuda/model/commit.cu:102-201 without the journal ring, hash and reply wraps: move
+    each slot of the role and return the tick's token records (slot, token, position,
+    flags, seed, draw), slots in order. plan: the Plan (asked, kept); out: the tick's batch;
+    token/draw: the step's outputs by sequence place; kv: dict with count and releases."""
+    records = []
+    for slot in range(SLOTS):
+        s = slots[slot]
+        if s["role"] != role:
+            continue
+        if s["state"] == DONE:
+            kv["releases"].append(slot)
+            kv["count"][slot] = 0
+            s["state"] = FREE
+            plan.asked[slot] = 0
+            continue
+        if s["state"] not in (PREFILL, DECODE):
+            continue
+        rows = out["rows"][slot]
+        lst = s["prompt"] + s["sampled"]
+        end = out["first"][slot] + rows
+        kept = plan.kept[slot]
+        journal = max(end - kept, 0)
+        extra = rows > 0 and end == lst and lst < SEQ_MAX
+        if rows:
+            s["state"] = DECODE if end == lst else PREFILL
+        for i in range(journal):
+            records.append((slot, tokens[slot][kept + i], kept + i, PROMPT, s["seed"], 0))
+        if extra:
+            place = out["place"][slot]
+            tok, drawn = int(token[place]), int(draw[place])
+            mark = SAMPLED
+            tokens[slot].append(tok)
+            s["sampled"] += 1
+            s["last"], s["draw"] = tok, drawn
+            if (tok == s["stop"] or s["sampled"] >= s["limit"] or s["flags"] & MARK_STOP
+                    or lst + 1 >= SEQ_MAX):
+                mark |= LAST
+                s["flags"] |= LAST
+                s["state"] = DONE
+            records.append((slot, tok, lst, mark, s["seed"], drawn))
+        plan.kept[slot] = kept + journal + int(bool(extra))
+        if s["flags"] & MARK_STOP:
+            s["state"] = DONE
+    return records

@@ -59,6 +59,7 @@ STRUCTS = {
     "aotx_kv_table": aotx_amd.KvTable,
     "aotx_plan_slot": aotx_amd.PlanSlot,
     "aotx_plan_state": aotx_amd.PlanState,
+    "aotx_token_record": aotx_amd.TokenRecord,
     "aotx_text_source": aotx_amd.TextSource,
     "aotx_text_store": aotx_amd.TextStore,
 }
@@ -71,8 +72,9 @@ def test_struct_layouts_match_c(tmp_path):
         "aotx_model_run": ["ids", "seed", "seqs", "select", "temperature", "how", "capture_count"],
         "aotx_kv_map": ["limit", "held", "free_count", "created"],
         "aotx_kv_table": ["count", "made", "served", "queue"],
-        "aotx_plan_slot": ["state", "page_limit", "seed", "sample"],
-        "aotx_plan_state": ["offset", "how", "place", "asked", "cursor", "seqs", "short_of", "steps"],
+        "aotx_plan_slot": ["state", "page_limit", "seed", "sample", "stop", "draw"],
+        "aotx_plan_state": ["offset", "how", "place", "asked", "kept", "cursor", "seqs", "short_of", "steps", "records"],
+        "aotx_token_record": ["position", "seed", "draw", "role"],
         "aotx_text_source": ["tokens", "merge_bytes", "merges", "token_type", "family"],
         "aotx_text_store": ["blocks", "bytes"],
     }

@@ -1,6 +1,6 @@
 """The tick plan's oracle (oracle/plan.py) pinned by hand-worked batches and by the
 invariants the reference checks on its plan (tests/decode_roles_test.cu:43-57)."""
-from oracle.plan import DECODE, FREE, PREFILL, SLOTS, Plan, kv_pages
+from oracle.plan import DECODE, DONE, FREE, PREFILL, SLOTS, Plan, kv_pages
 
 BIG = 10 ** 6
 
@@ -113,3 +113,39 @@ def test_reference_invariants():
                 offs = out["offset"]
                 assert all(a < b for a, b in zip(offs, offs[1:]))
             assert all(served), (mode, budget)
+
+
+def test_worked_commit():
+    """cuda/model/commit.cu:112-176 by hand: a prefill slot that got its whole list moves
+    to DECODE and takes the sampled token (its prompt tokens recorded first); a slot cut
+    short stays PREFILL with only the rows it gave recorded; a slot at its limit ends with
+    the LAST flag; a DONE slot gives its pages back; a stop mark ends a slot."""
+    from oracle.plan import LAST, MARK_STOP, PROMPT, SAMPLED, commit
+    slots = [slot() for _ in range(SLOTS)]
+    slots[0] = slot(PREFILL, prompt=3, limit=4, seed=5)
+    slots[1] = slot(PREFILL, prompt=6, limit=4, seed=6)
+    slots[2] = slot(DECODE, prompt=2, sampled=1, limit=2, seed=7)
+    slots[3] = slot(DONE)
+    slots[4] = slot(PREFILL, prompt=2, limit=9)
+    for s in slots:
+        s.update(stop=0xFFFFFFFF, flags=0, last=0, draw=0)
+    slots[4]["flags"] = MARK_STOP
+    toks = [[10 * i + k for k in range(8)] for i in range(SLOTS)]
+    toks[2] = [20, 21, 22]
+    seen = [0] * SLOTS
+    seen[2] = 2
+    p = Plan()
+    p.kept[2] = 3
+    out = p.tick(2, slots, toks, seen, 6, kv(), lambda c: 1, 100)
+    # decode slot 2 first (1 row), then slot 0 (3 rows), slot 1 cut to 2, slot 4 waits
+    assert out["agent"] == [2, 0, 1] and out["offset"] == [0, 1, 4, 6]
+    k = dict(count=[1] * SLOTS, releases=[])
+    toks[0], toks[1] = toks[0][:3], toks[1][:6]
+    rec = commit(p, 2, slots, toks, out, [77, 55, 66], [9, 8, 7], k)
+    assert rec == [(0, 0, 0, PROMPT, 5, 0), (0, 1, 1, PROMPT, 5, 0), (0, 2, 2, PROMPT, 5, 0),
+                   (0, 55, 3, SAMPLED, 5, 8),
+                   (1, 10, 0, PROMPT, 6, 0), (1, 11, 1, PROMPT, 6, 0),
+                   (2, 77, 3, SAMPLED | LAST, 7, 9)]
+    assert [slots[i]["state"] for i in range(5)] == [DECODE, PREFILL, 3, FREE, 3]
+    assert toks[0] == [0, 1, 2, 55] and slots[0]["sampled"] == 1 and slots[2]["flags"] == LAST
+    assert k["releases"] == [3] and p.kept[:3] == [4, 2, 4]
