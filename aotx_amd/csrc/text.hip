@@ -308,6 +308,36 @@ static __device__ unsigned int match(unsigned int pattern, const unsigned char *
     return spaces(b, end, at, span, 1);
 }
 
+/* one thread per text: the text with every byte that does not start a UTF-8 character
+ * (and the bytes of a cut or malformed one) written as U+FFFD, EF BF BD (cuda/text/
+ * text.cuh:367-374); text t goes to out + 3 at[t], its length to clean_len[t] */
+__global__ void aotx_text_clean_kernel(const unsigned char *bytes, const unsigned long long *at,
+                                       unsigned int texts, unsigned char *out,
+                                       unsigned long long *at3, unsigned int *clean_len)
+{
+    const unsigned int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t > texts) return;
+    at3[t] = 3ull * at[t];
+    if (t == texts) return;
+    const unsigned char *b = bytes + at[t];
+    const unsigned int end = (unsigned int)(at[t + 1u] - at[t]);
+    unsigned char *o = out + 3ull * at[t];
+    unsigned int w = 0u;
+    for (unsigned int pos = 0u; pos < end;) {
+        unsigned int p;
+        const unsigned int k = utf8_at(b, end, pos, &p);
+        if (p == 0xFFFDu && k == 1u) {        /* no character starts here */
+            o[w] = 0xEFu; o[w + 1u] = 0xBFu; o[w + 2u] = 0xBDu;
+            w += 3u;
+        } else {
+            for (unsigned int i = 0u; i < k; ++i) o[w + i] = b[pos + i];
+            w += k;
+        }
+        pos += k;
+    }
+    clean_len[t] = w;
+}
+
 /* The longest special token whose bytes start at `at` (cuda/text/pretok.cu:339-372): its
  * length, 0 for none. */
 static __device__ unsigned int special_at(const aotx_text_vocab &v, const unsigned char *b,
@@ -332,15 +362,15 @@ static __device__ unsigned int special_at(const aotx_text_vocab &v, const unsign
  * tok[at[t] + p] its token when it is a special token (else AOTX_TEXT_NONE). A special
  * token is a whole match and the pattern reads no text across it. */
 __global__ void aotx_text_pretok_kernel(aotx_text_vocab v, const unsigned char *bytes,
-                                        const unsigned long long *at, unsigned int texts,
-                                        unsigned int *start, unsigned int *len, unsigned int *tok,
-                                        unsigned int *pieces)
+                                        const unsigned long long *at, const unsigned int *clean_len,
+                                        unsigned int texts, unsigned int *start, unsigned int *len,
+                                        unsigned int *tok, unsigned int *pieces)
 {
     const unsigned int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= texts) return;
     const unsigned long long base = at[t];
     const unsigned char *b = bytes + base;
-    const unsigned int text_end = (unsigned int)(at[t + 1u] - base);
+    const unsigned int text_end = clean_len[t];
     unsigned int pos = 0u, n = 0u;
     while (pos < text_end) {
         unsigned int stop = pos, special = 0u, id = AOTX_TEXT_NONE;
@@ -750,28 +780,33 @@ extern "C" int aotx_text_encode(const unsigned char *bytes, const unsigned long 
         return 0;
     }
     unsigned int *start = nullptr, *len = nullptr, *pieces = nullptr, *ptok = nullptr, *pcount = nullptr,
-                 *pspecial = nullptr;
-    AOTX_CHECK(hipMallocAsync((void **)&start, total * 4u, s));
-    AOTX_CHECK(hipMallocAsync((void **)&len, total * 4u, s));
-    AOTX_CHECK(hipMallocAsync((void **)&ptok, total * 4u, s));
-    AOTX_CHECK(hipMallocAsync((void **)&pcount, total * 4u, s));
+                 *pspecial = nullptr, *clean_len = nullptr;
+    unsigned char *clean = nullptr;
+    unsigned long long *at3 = nullptr;
+    const unsigned long long room = 3ull * total;       /* every byte may become U+FFFD */
+    AOTX_CHECK(hipMallocAsync((void **)&clean, room, s));
+    AOTX_CHECK(hipMallocAsync((void **)&at3, (texts + 1ull) * 8u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&clean_len, texts * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&start, room * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&len, room * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&ptok, room * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&pcount, room * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&pspecial, room * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&pieces, texts * 4u, s));
-    AOTX_CHECK(hipMallocAsync((void **)&pspecial, total * 4u, s));
-    hipLaunchKernelGGL(aotx_text_pretok_kernel, dim3((texts + 63u) / 64u), dim3(64), 0, s, g_vocab, bytes, at,
-                       texts, start, len, pspecial, pieces);
+    hipLaunchKernelGGL(aotx_text_clean_kernel, dim3((texts + 64u) / 64u), dim3(64), 0, s, bytes, at, texts,
+                       clean, at3, clean_len);
     AOTX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(aotx_text_merge_kernel, dim3((unsigned int)total), dim3(64), 0, s, g_vocab, bytes, at,
+    hipLaunchKernelGGL(aotx_text_pretok_kernel, dim3((texts + 63u) / 64u), dim3(64), 0, s, g_vocab, clean, at3,
+                       clean_len, texts, start, len, pspecial, pieces);
+    AOTX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(aotx_text_merge_kernel, dim3((unsigned int)room), dim3(64), 0, s, g_vocab, clean, at3,
                        texts, start, len, pspecial, pieces, ptok, pcount);
     AOTX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(aotx_text_gather_kernel, dim3(texts), dim3(64), 0, s, at, start, pieces, ptok, pcount,
+    hipLaunchKernelGGL(aotx_text_gather_kernel, dim3(texts), dim3(64), 0, s, at3, start, pieces, ptok, pcount,
                        ids, count);
     AOTX_LAUNCH_CHECK();
-    AOTX_CHECK(hipFreeAsync(start, s));
-    AOTX_CHECK(hipFreeAsync(len, s));
-    AOTX_CHECK(hipFreeAsync(ptok, s));
-    AOTX_CHECK(hipFreeAsync(pcount, s));
-    AOTX_CHECK(hipFreeAsync(pieces, s));
-    AOTX_CHECK(hipFreeAsync(pspecial, s));
+    void *tmp[] = {clean, at3, clean_len, start, len, ptok, pcount, pspecial, pieces};
+    for (void *q : tmp) AOTX_CHECK(hipFreeAsync(q, s));
     AOTX_CHECK(hipStreamSynchronize(s));
     return 0;
 }

@@ -43,12 +43,12 @@ class Tokenizer:
         data, at = _runs(texts)
         d = torch.from_numpy(data).cuda()
         a = torch.from_numpy(at.view(np.int64)).cuda()
-        ids = torch.zeros(max(int(at[-1]), 1), dtype=torch.int32, device="cuda")
+        ids = torch.zeros(max(3 * int(at[-1]), 1), dtype=torch.int32, device="cuda")
         cnt = torch.zeros(len(texts), dtype=torch.int32, device="cuda")
         check(self.L.aotx_text_encode(d.data_ptr(), a.data_ptr(), len(texts), ids.data_ptr(),
                                       cnt.data_ptr(), None), "aotx_text_encode")
         ids, cnt = ids.cpu().numpy(), cnt.cpu().numpy()
-        return [[int(x) for x in ids[int(at[i]):int(at[i]) + int(cnt[i])]] for i in range(len(texts))]
+        return [[int(x) for x in ids[3 * int(at[i]):3 * int(at[i]) + int(cnt[i])]] for i in range(len(texts))]
 
     def decode(self, seqs, limit=1 << 16):
         """Bytes of a list of token id lists."""

@@ -66,7 +66,9 @@ int aotx_text_vocab_file(const struct aotx_modelfile *file, aotx_text_store *sto
 int aotx_text_vocab_report(unsigned int report[4]);
 
 /* Encode `texts` byte runs (device: bytes, at[texts + 1] offsets) with the current
- * vocabulary: the tokens of text t go to ids + at[t] (a text never has more tokens than
+ * vocabulary: the tokens of text t go to ids + 3 * at[t] (ids holds 3 * at[texts]: a
+ * byte that starts no UTF-8 character is read as U+FFFD, three bytes, as
+ * cuda/text/text.cuh:367-374 cleans text, and a text never has more tokens than cleaned
  * bytes) and their count to count[t]. The pipeline of cuda/text/pretok.cu:393 and
  * bpe.cu:44-223: one thread per text cuts the pre-tokens (a pre-token longer than
  * AOTX_TEXT_CHUNK_BYTES is cut at a character boundary and the rest is matched again),
@@ -74,8 +76,7 @@ int aotx_text_vocab_report(unsigned int report[4]);
  * ranks; with the family's whole rule a pre-token that is a token stays whole). Tokens
  * of the control and user types are whole matches found first, the longest at the
  * leftmost place (cuda/text/pretok.cu:339-372, :404-431); the pattern reads no text across
- * them. Text is taken as UTF-8. Returns 1 with no vocabulary or a bad argument;
- * synchronous. */
+ * them. Returns 1 with no vocabulary or a bad argument; synchronous. */
 int aotx_text_encode(const unsigned char *bytes, const unsigned long long *at, unsigned int texts,
                      unsigned int *ids, unsigned int *count, void *stream);
 

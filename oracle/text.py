@@ -39,6 +39,40 @@ def byte_string(bs):
     return "".join(chr(byte_point(b)) for b in bs)
 
 
+def clean(data):
+    """Bytes with every byte that starts no UTF-8 character written as U+FFFD (EF BF BD),
+    one per byte (cuda/text/text.cuh:367-374): a lead byte needs its continuation bytes,
+    no overlong form, no surrogate, nothing past U+10FFFF."""
+    out, pos, n = bytearray(), 0, len(data)
+    while pos < n:
+        c = data[pos]
+        if c < 0x80:
+            out.append(c); pos += 1; continue
+        if c & 0xE0 == 0xC0:
+            need, cp, lo = 1, c & 0x1F, 0x80
+        elif c & 0xF0 == 0xE0:
+            need, cp, lo = 2, c & 0x0F, 0x800
+        elif c & 0xF8 == 0xF0:
+            need, cp, lo = 3, c & 0x07, 0x10000
+        else:
+            need = None
+        ok = need is not None and pos + need < n
+        if ok:
+            for i in range(1, need + 1):
+                d = data[pos + i]
+                if d & 0xC0 != 0x80:
+                    ok = False
+                    break
+                cp = (cp << 6) | (d & 0x3F)
+        if ok and (cp < lo or cp > 0x10FFFF or 0xD800 <= cp <= 0xDFFF):
+            ok = False
+        if ok:
+            out += data[pos:pos + need + 1]; pos += need + 1
+        else:
+            out += b"\xef\xbf\xbd"; pos += 1
+    return bytes(out)
+
+
 def pretokens(text, pattern):
     """Pre-tokens of a str (consecutive, covering it)."""
     return [m.group(0) for m in regex.finditer(PATTERNS[pattern], text)]
@@ -93,6 +127,7 @@ class Vocab:
         """Token ids of UTF-8 bytes: the leftmost special token splits the text, the
         pattern and the merges run on the text between (pretok.cu:404-431)."""
         out, pos = [], 0
+        data = clean(data)
         while pos < len(data):
             stop, (n, sid) = pos, (0, None)
             while stop < len(data) and self.specials:

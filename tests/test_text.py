@@ -105,3 +105,17 @@ def test_special_tokens_match_tokenizers_library(bpe, family):
         parts = [text(rng, rng.randint(0, 8)) for _ in range(3)]
         s = rng.choice(SPECIALS).join(parts) + rng.choice(["", "<|start|>x", "<|sx", "<|"])
         assert v.encode(s.encode()) == hf.encode(s).ids, repr(s)
+
+
+def test_clean_by_hand():
+    """Each byte that starts no character becomes U+FFFD (cuda/text/text.cuh:367-374)."""
+    from oracle.text import clean
+    R = "\ufffd".encode()
+    assert clean(b"a\xffb") == b"a" + R + b"b"
+    assert clean("中".encode()[:2]) == R + R                     # cut off by the end
+    assert clean(b"\xe4\xb8x") == R + R + b"x"                   # cut by a non-continuation
+    assert clean(b"\xc0\xaf") == R + R                          # overlong
+    assert clean(b"\xed\xa0\x80") == R + R + R                  # surrogate
+    assert clean(b"\xf4\x90\x80\x80") == R * 4                  # past U+10FFFF
+    assert clean("😀é\ufffd".encode()) == "😀é\ufffd".encode()   # valid text unchanged
+    assert clean(b"\x80") == R and clean(b"") == b""

@@ -28,7 +28,7 @@ def bpe():
 
 
 def _runs(strings):
-    data = [s.encode("utf-8") for s in strings]
+    data = [s if isinstance(s, bytes) else s.encode("utf-8") for s in strings]
     at = np.zeros(len(data) + 1, dtype=np.uint64)
     at[1:] = np.cumsum([len(d) for d in data])
     return np.frombuffer(b"".join(data), dtype=np.uint8).copy(), at
@@ -60,12 +60,12 @@ def _encode(torch, lib, strings):
     data, at = _runs(strings)
     d = torch.from_numpy(data if len(data) else np.zeros(1, np.uint8)).cuda()
     a = torch.from_numpy(at.view(np.int64)).cuda()
-    ids = torch.zeros(max(int(at[-1]), 1), dtype=torch.int32, device="cuda")
+    ids = torch.zeros(max(3 * int(at[-1]), 1), dtype=torch.int32, device="cuda")
     cnt = torch.zeros(len(strings), dtype=torch.int32, device="cuda")
     assert lib.aotx_text_encode(d.data_ptr(), a.data_ptr(), len(strings), ids.data_ptr(),
                                 cnt.data_ptr(), None) == 0
     ids, cnt = ids.cpu().numpy(), cnt.cpu().numpy()
-    return [list(ids[int(at[i]):int(at[i]) + int(cnt[i])]) for i in range(len(strings))]
+    return [list(ids[3 * int(at[i]):3 * int(at[i]) + int(cnt[i])]) for i in range(len(strings))]
 
 
 def _detok(torch, lib, seqs, limit=4096):
@@ -189,3 +189,22 @@ def test_text_end_to_end_from_gguf(torch, orc, bpe, tmp_path):
     finally:
         rt.close()
         tk.close()
+
+
+def test_invalid_utf8_vs_oracle(torch, lib, bpe):
+    """Bytes that start no character are encoded as U+FFFD, as the oracle's clean does."""
+    tokens, merges, _ = bpe
+    v = Vocab(tokens, merges, family="llama3")
+    built = Built(lib, tokens, merges, [1] * len(tokens), "llama3")
+    try:
+        rng = random.Random(41)
+        bad = [b"\xff", b"\x80", b"\xe4\xb8", b"\xc0\xaf", b"\xed\xa0\x80", b"\xf4\x90\x80\x80"]
+        strings = []
+        for _ in range(100):
+            parts = [text(rng, rng.randint(0, 6)).encode() for _ in range(3)]
+            strings.append(rng.choice(bad).join(parts) + rng.choice([b"", b"\xe4", b"\xf0\x9f"]))
+        got = _encode(torch, lib, strings)
+        for s_, g in zip(strings, got):
+            assert g == v.encode(s_), repr(s_)
+    finally:
+        built.close()
