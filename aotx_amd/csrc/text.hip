@@ -8,7 +8,8 @@
  * Encoding is three launches:
  *   - pre-tokens: one thread per text runs the family's split pattern, a state machine
  *     that takes the first alternative matching at a position (cuda/text/pretok.cu:1-45);
- *   - merge: one 64-lane workgroup per pre-token holds its symbols in LDS as a linked list
+ *   - merge: one 64-lane workgroup per pre-token (a work list the pre-token pass appends
+ *     to) holds its symbols in LDS as a linked list
  *     with the rank of each symbol's pair; each round a wave minimum over (rank, position)
  *     picks the pair to merge (the lowest rank, the leftmost of equal ranks), and only
  *     the two pairs next to it are looked up again;
@@ -364,7 +365,8 @@ static __device__ unsigned int special_at(const aotx_text_vocab &v, const unsign
 __global__ void aotx_text_pretok_kernel(aotx_text_vocab v, const unsigned char *bytes,
                                         const unsigned long long *at, const unsigned int *clean_len,
                                         unsigned int texts, unsigned int *start, unsigned int *len,
-                                        unsigned int *tok, unsigned int *pieces)
+                                        unsigned int *tok, unsigned int *pieces, unsigned int *work,
+                                        unsigned int *works)
 {
     const unsigned int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= texts) return;
@@ -409,6 +411,9 @@ __global__ void aotx_text_pretok_kernel(aotx_text_vocab v, const unsigned char *
         }
     }
     pieces[t] = n;
+    /* the merge step takes one workgroup per pre-token of the batch, from this list */
+    const unsigned int first = atomicAdd(works, n);
+    for (unsigned int i = 0u; i < n; ++i) work[first + i] = (unsigned int)(base + i);
 }
 
 /* ---- merge: one 64-lane workgroup per pre-token slot ----------------------------------- */
@@ -419,13 +424,13 @@ __global__ __launch_bounds__(64) void aotx_text_merge_kernel(aotx_text_vocab v, 
                                                              const unsigned long long *at, unsigned int texts,
                                                              const unsigned int *start, const unsigned int *len,
                                                              const unsigned int *ptok,
-                                                             const unsigned int *pieces, unsigned int *out,
-                                                             unsigned int *out_count)
+                                                             const unsigned int *pieces, const unsigned int *work,
+                                                             unsigned int *out, unsigned int *out_count)
 {
     __shared__ unsigned int tok[TX_N], rank[TX_N], res[TX_N];
     __shared__ unsigned short nxt[TX_N], prv[TX_N];
     const unsigned int lane = threadIdx.x;
-    const unsigned long long s = blockIdx.x;
+    const unsigned long long s = work[blockIdx.x];
     /* the text of slot s: at[t] <= s < at[t + 1] */
     unsigned int lo = 0u, hi = texts;
     while (hi - lo > 1u) {
@@ -793,19 +798,28 @@ extern "C" int aotx_text_encode(const unsigned char *bytes, const unsigned long 
     AOTX_CHECK(hipMallocAsync((void **)&pcount, room * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&pspecial, room * 4u, s));
     AOTX_CHECK(hipMallocAsync((void **)&pieces, texts * 4u, s));
+    unsigned int *work = nullptr, *works = nullptr;
+    AOTX_CHECK(hipMallocAsync((void **)&work, room * 4u, s));
+    AOTX_CHECK(hipMallocAsync((void **)&works, 4u, s));
+    AOTX_CHECK(hipMemsetAsync(works, 0, 4u, s));
     hipLaunchKernelGGL(aotx_text_clean_kernel, dim3((texts + 64u) / 64u), dim3(64), 0, s, bytes, at, texts,
                        clean, at3, clean_len);
     AOTX_LAUNCH_CHECK();
     hipLaunchKernelGGL(aotx_text_pretok_kernel, dim3((texts + 63u) / 64u), dim3(64), 0, s, g_vocab, clean, at3,
-                       clean_len, texts, start, len, pspecial, pieces);
+                       clean_len, texts, start, len, pspecial, pieces, work, works);
     AOTX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(aotx_text_merge_kernel, dim3((unsigned int)room), dim3(64), 0, s, g_vocab, clean, at3,
-                       texts, start, len, pspecial, pieces, ptok, pcount);
-    AOTX_LAUNCH_CHECK();
+    unsigned int nwork = 0u;
+    AOTX_CHECK(hipMemcpyAsync(&nwork, works, 4u, hipMemcpyDeviceToHost, s));
+    AOTX_CHECK(hipStreamSynchronize(s));
+    if (nwork > 0u) {
+        hipLaunchKernelGGL(aotx_text_merge_kernel, dim3(nwork), dim3(64), 0, s, g_vocab, clean, at3, texts,
+                           start, len, pspecial, pieces, work, ptok, pcount);
+        AOTX_LAUNCH_CHECK();
+    }
     hipLaunchKernelGGL(aotx_text_gather_kernel, dim3(texts), dim3(64), 0, s, at3, start, pieces, ptok, pcount,
                        ids, count);
     AOTX_LAUNCH_CHECK();
-    void *tmp[] = {clean, at3, clean_len, start, len, ptok, pcount, pspecial, pieces};
+    void *tmp[] = {clean, at3, clean_len, start, len, ptok, pcount, pspecial, pieces, work, works};
     for (void *q : tmp) AOTX_CHECK(hipFreeAsync(q, s));
     AOTX_CHECK(hipStreamSynchronize(s));
     return 0;
