@@ -396,6 +396,100 @@ def prefill_run(args):
                       "gemm": os.environ.get("AOTX_GEMM", "1") != "0", "chunks": out}))
 
 
+def _text_corpus(seed, lines, words=60):
+    """Seeded synthetic text: words from a few scripts, numbers, punctuation, spaces."""
+    rng = np.random.default_rng(seed)
+    vocab = ["hello", "world", "it's", "the", "café", "naïve", "данные", "中文", "αβγ", "12345",
+             "don't", "code", "x", "::", "...", "(", ")", "\n", "  ", "😀"]
+    out = []
+    for _ in range(lines):
+        picks = rng.integers(0, len(vocab), words)
+        out.append(" ".join(vocab[i] for i in picks))
+    return out
+
+
+def text_run(args):
+    """`--text`: the tokenizer (llama3 split, whole rule) on a vocabulary the `tokenizers`
+    library trains on a seeded synthetic corpus: GPU encode and decode throughput over 4096
+    texts (~1.2 MB; synchronous calls, best of 5), the CPU oracle's encode on a bounded
+    sample beside it. Prints one JSON line."""
+    import ctypes
+    import torch
+    from tokenizers import Tokenizer as HF, models, pre_tokenizers, trainers
+    from aotx_amd.text import Tokenizer
+    torch.cuda.init()
+    hf = HF(models.BPE())
+    hf.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=True)
+    hf.train_from_iterator(_text_corpus(1, 300), trainers.BpeTrainer(
+        vocab_size=2000, show_progress=False, initial_alphabet=pre_tokenizers.ByteLevel.alphabet()))
+    model = json.loads(hf.to_str())["model"]
+    tokens = [None] * len(model["vocab"])
+    for tok, i in model["vocab"].items():
+        tokens[i] = tok
+    merges = [m if isinstance(m, str) else f"{m[0]} {m[1]}" for m in model["merges"]]
+    tk = Tokenizer(tokens=tokens, merges=merges, family="llama3")
+    texts = _text_corpus(2, 4096)
+    raw = [t.encode() for t in texts]
+    nbytes = sum(len(r) for r in raw)
+    at = np.zeros(len(raw) + 1, dtype=np.uint64)
+    at[1:] = np.cumsum([len(r) for r in raw])
+    bytes_d = torch.from_numpy(np.frombuffer(b"".join(raw), dtype=np.uint8).copy()).cuda()
+    at_d = torch.from_numpy(at.view(np.int64)).cuda()
+    ids_d = torch.zeros(3 * nbytes, dtype=torch.int32, device="cuda")
+    cnt_d = torch.zeros(len(raw), dtype=torch.int32, device="cuda")
+    L = tk.L
+    enc = []
+    for _ in range(6):           # the library call alone (synchronous), inputs in HBM
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        assert L.aotx_text_encode(bytes_d.data_ptr(), at_d.data_ptr(), len(raw), ids_d.data_ptr(),
+                                  cnt_d.data_ptr(), None) == 0
+        enc.append(time.perf_counter() - t0)
+    cnt = cnt_d.cpu().numpy()
+    ids_h = ids_d.cpu().numpy()
+    seqs = [ids_h[3 * int(at[i]):3 * int(at[i]) + int(cnt[i])] for i in range(len(raw))]
+    flat = torch.from_numpy(np.concatenate(seqs).astype(np.int32)).cuda()
+    tat = np.zeros(len(raw) + 1, dtype=np.uint64)
+    tat[1:] = np.cumsum(cnt.astype(np.uint64))
+    tat_d = torch.from_numpy(tat.view(np.int64)).cuda()
+    limit = 2048
+    out_d = torch.zeros(len(raw) * limit, dtype=torch.uint8, device="cuda")
+    len_d = torch.zeros(len(raw), dtype=torch.int32, device="cuda")
+    dec = []
+    for _ in range(6):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        assert L.aotx_text_detok(flat.data_ptr(), tat_d.data_ptr(), len(raw), out_d.data_ptr(), limit,
+                                 len_d.data_ptr(), None) == 0
+        torch.cuda.synchronize()
+        dec.append(time.perf_counter() - t0)
+    o = out_d[:limit].cpu().numpy()
+    assert bytes(o[:int(len_d[0])]) == raw[0]
+    ntok = int(cnt.sum())
+    e, d = min(enc[1:]), min(dec[1:])
+    cpu = None
+    if not args.no_cpu:
+        from oracle.text import Vocab
+        v = Vocab(tokens, merges, family="llama3")
+        t0, done = time.perf_counter(), 0
+        for r in raw:                  # bounded: at most ~20 s of the same texts
+            v.encode(r)
+            done += len(r)
+            if time.perf_counter() - t0 > 20.0:
+                break
+        el = time.perf_counter() - t0
+        cpu = {"value": round(done / el / 1e6, 4), "unit": "MB/s", "cores": 1, "kind": "port",
+               "sample": f"{done} bytes of the same texts through oracle/text.py encode ({el:.1f} s)"}
+    tk.close()
+    print(json.dumps({"metric": "tokenizer encode MB/s (llama3 split, BPE merge on the GPU)",
+                      "value": round(nbytes / e / 1e6, 2), "unit": "MB/s", "texts": len(texts),
+                      "bytes": nbytes, "tokens": ntok, "encode_ms": round(e * 1e3, 3),
+                      "decode_ms": round(d * 1e3, 3),
+                      "decode_mb_s": round(nbytes / d / 1e6, 2),
+                      "note": "wall clock of the synchronous library calls on inputs in HBM (encode includes its scratch allocations and one 4-byte read-back)",
+                      "cpu_baseline": cpu}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -409,6 +503,8 @@ def main():
                     help="BASELINE config 5 only: the Mixtral-shape routed-expert decoder")
     ap.add_argument("--prefill", action="store_true",
                     help="time one prompt chunk of 128/256/512 tokens (8B shape) and exit")
+    ap.add_argument("--text", action="store_true",
+                    help="time the tokenizer (encode/decode on the GPU) and exit")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the roofline kernel and a calibration copy (counter passes)")
     args = ap.parse_args()
@@ -426,6 +522,9 @@ def main():
         return
     if args.prefill:
         prefill_run(args)
+        return
+    if args.text:
+        text_run(args)
         return
 
     import torch
