@@ -113,9 +113,17 @@ __global__ __launch_bounds__(64) void aotx_plan_kernel(unsigned int role, const 
         aotx_model_how how = seq.sample;
         how.seed = seq.seed;
         p->how[place] = how;
-        for (unsigned int i = 0u; i < rows; ++i) {
-            const unsigned int at = held + i;
-            p->ids[start + i] = at < stride ? tokens[(unsigned long long)slot * stride + at] : 0;
+    }
+    /* the rows' token ids, copied by the whole wave one sequence at a time (a prompt piece
+     * can be the whole budget) */
+    for (unsigned int j = 0u; j < 64u; ++j) {
+        const unsigned int n = __shfl(rows, (int)j, 64);
+        if (n == 0u) continue;
+        const unsigned int at0 = __shfl(held, (int)j, 64), dst = __shfl(start, (int)j, 64);
+        const unsigned int src = __shfl(slot, (int)j, 64);
+        for (unsigned int i = lane; i < n; i += 64u) {
+            const unsigned int at = at0 + i;
+            p->ids[dst + i] = at < stride ? tokens[(unsigned long long)src * stride + at] : 0;
         }
     }
     if (lane == 0u) {
@@ -153,7 +161,7 @@ __global__ __launch_bounds__(64) void aotx_commit_kernel(unsigned int role, aotx
                                                          aotx_state *st, aotx_plan_state *p,
                                                          aotx_token_record *rec, unsigned int cap)
 {
-    const unsigned int slot = threadIdx.x;
+    const unsigned int slot = threadIdx.x, lane = threadIdx.x;
     aotx_plan_slot &seq = slots[slot];
     unsigned int journal = 0u, from = 0u, extra = 0u, tok = 0u, mark = 0u;
     unsigned long long drawn = 0ull;
@@ -198,19 +206,27 @@ __global__ __launch_bounds__(64) void aotx_commit_kernel(unsigned int role, aotx
     const unsigned int mine = journal + extra;
     const unsigned int scan = plan_scan(mine);
     const unsigned int first = scan - mine;
-    for (unsigned int i = 0u; i < journal; ++i) {
-        const unsigned int r = first + i, at = from + i;
-        if (r >= cap) break;
-        aotx_token_record x;
-        x.slot = slot;
-        x.token = at < stride ? (unsigned int)tokens[(unsigned long long)slot * stride + at] : 0u;
-        x.position = at;
-        x.flags = AOTX_TOKEN_PROMPT;
-        x.seed = seq.seed;
-        x.draw = 0ull;
-        x.role = role;
-        x.reserved = 0u;
-        rec[r] = x;
+    /* the list tokens' records, written by the whole wave one slot at a time */
+    const unsigned long long seed = seq.seed;
+    for (unsigned int j = 0u; j < 64u; ++j) {
+        const unsigned int n = __shfl(journal, (int)j, 64);
+        if (n == 0u) continue;
+        const unsigned int f0 = __shfl(first, (int)j, 64), at0 = __shfl(from, (int)j, 64);
+        const unsigned long long sd = __shfl(seed, (int)j, 64);
+        for (unsigned int i = lane; i < n; i += 64u) {
+            const unsigned int r = f0 + i, at = at0 + i;
+            if (r >= cap) break;
+            aotx_token_record x;
+            x.slot = j;
+            x.token = at < stride ? (unsigned int)tokens[(unsigned long long)j * stride + at] : 0u;
+            x.position = at;
+            x.flags = AOTX_TOKEN_PROMPT;
+            x.seed = sd;
+            x.draw = 0ull;
+            x.role = role;
+            x.reserved = 0u;
+            rec[r] = x;
+        }
     }
     if (extra != 0u && first + journal < cap) {
         aotx_token_record x;

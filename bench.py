@@ -490,6 +490,60 @@ def text_run(args):
                       "cpu_baseline": cpu}))
 
 
+def tick_run(args):
+    """`--tick`: the tick plan and commit kernels (one wave each) for 64 prefill slots of the
+    tiny model and a full 512-row batch, timed with HIP events over 200 ticks on one stream.
+    Prints one JSON line."""
+    import ctypes
+    import torch
+    import aotx_amd as A
+    from aotx_amd.model import TINY, Runtime, build_host
+    torch.cuda.init()
+    region, lay = build_host(TINY, seed=1)
+    rt = Runtime(torch.from_numpy(region).cuda(), lay.desc, max_tokens=512, pool_pages=256)
+    L = rt.L
+    table = (A.PlanSlot * A.AOTX_SLOTS)()
+    for i in range(A.AOTX_SLOTS):
+        t = table[i]
+        # prefill slots of long prompts: with no model step between ticks nothing enters the
+        # pages, so every tick packs the same full batch (512 rows) and records 512 tokens
+        t.state, t.role, t.prompt, t.sampled, t.limit = A.AOTX_SEQ_STATE_PREFILL, 2, 4000, 0, 64
+        t.seed, t.stop, t.sample = 1000 + i, 0xFFFFFFFF, A.neutral_how()
+    slots = torch.from_numpy(np.frombuffer(bytes(table), dtype=np.uint8).copy()).cuda()
+    lists = torch.zeros((A.AOTX_SLOTS, 4096), dtype=torch.int32, device="cuda")
+    plan = torch.zeros(ctypes.sizeof(A.PlanState), dtype=torch.uint8, device="cuda")
+    recs = torch.zeros(1024 * ctypes.sizeof(A.TokenRecord), dtype=torch.uint8, device="cuda")
+    tok = torch.zeros(A.AOTX_SLOTS, dtype=torch.int32, device="cuda")
+    drw = torch.zeros(A.AOTX_SLOTS, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+
+    def tick():
+        assert L.aotx_decode_plan(2, slots.data_ptr(), lists.data_ptr(), 4096, 512, rt.map.limit,
+                                  plan.data_ptr(), ctypes.c_void_p(s.cuda_stream)) == 0
+        assert L.aotx_decode_commit(2, slots.data_ptr(), lists.data_ptr(), 4096, tok.data_ptr(),
+                                    drw.data_ptr(), plan.data_ptr(), recs.data_ptr(), 1024,
+                                    ctypes.c_void_p(s.cuda_stream)) == 0
+    tick()                                  # asks for the pages
+    torch.cuda.synchronize()
+    L.aotx_kv_serve(ctypes.byref(rt.map), None)
+    for _ in range(5):
+        tick()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(200):
+        tick()
+    e1.record(s)
+    torch.cuda.synchronize()
+    st = A.PlanState.from_buffer_copy(plan.cpu().numpy().tobytes())
+    us = e0.elapsed_time(e1) * 1e3 / 200
+    rt.close()
+    print(json.dumps({"metric": "tick plan + commit us per tick (64 slots, 512-row batch)",
+                      "value": round(us, 2), "unit": "us", "seqs": st.seqs, "rows": st.tokens,
+                      "records": st.records,
+                      "note": "two one-wave launches per tick, back to back on one stream"}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -503,6 +557,8 @@ def main():
                     help="BASELINE config 5 only: the Mixtral-shape routed-expert decoder")
     ap.add_argument("--prefill", action="store_true",
                     help="time one prompt chunk of 128/256/512 tokens (8B shape) and exit")
+    ap.add_argument("--tick", action="store_true",
+                    help="time the tick plan + commit kernels and exit")
     ap.add_argument("--text", action="store_true",
                     help="time the tokenizer (encode/decode on the GPU) and exit")
     ap.add_argument("--traffic", action="store_true",
@@ -525,6 +581,9 @@ def main():
         return
     if args.text:
         text_run(args)
+        return
+    if args.tick:
+        tick_run(args)
         return
 
     import torch
