@@ -561,6 +561,9 @@ def main():
                     help="time the tick plan + commit kernels and exit")
     ap.add_argument("--text", action="store_true",
                     help="time the tokenizer (encode/decode on the GPU) and exit")
+    ap.add_argument("--step-only", action="store_true",
+                    help="only the decode steps at batch 32 and 1 (no GEMV table, attention "
+                         "timing, ragged case or CPU baseline): the kernel-trace workload")
     ap.add_argument("--traffic", action="store_true",
                     help="run only the roofline kernel and a calibration copy (counter passes)")
     args = ap.parse_args()
@@ -595,12 +598,12 @@ def main():
 
     # Q8 GEMV table (config 2) and the roofline of the dominant kernel.
     shapes = [(4096, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
-    table = gemv_table(torch, L, shapes, [1, 4, 8, 32])
+    table = [] if args.step_only else gemv_table(torch, L, shapes, [1, 4, 8, 32])
     for row in table:
         log(f"gemv n={row['n']} k={row['k']} m={row['m']}: file {row['file_us']} us "
             f"{row['file_gbs']} GB/s | repacked {row['repacked_us']} us {row['repacked_gbs']} GB/s")
-    dom = next(r for r in table if r["n"] == 14336 and r["k"] == 4096 and r["m"] == args.batch) \
-        if args.batch in (1, 4, 8, 32) else None
+    dom = next((r for r in table if r["n"] == 14336 and r["k"] == 4096 and r["m"] == args.batch),
+               None)
 
     # 8B-shape decoder, synthetic weights on the GPU.
     shape = LLAMA_8B
@@ -616,6 +619,13 @@ def main():
                  pool_pages=per_slot * (len(batch_slots) + 1) + 8)
     seat_context(torch, rt, batch_slots + one_slot, args.context, reserve, shape.layers,
                  shape.kv_heads, shape.head_dim)
+    if args.step_only:
+        tps, ms = decode(torch, rt, batch_slots, args.steps, args.warmup, A.neutral_how())
+        tps1, ms1 = decode(torch, rt, one_slot, args.steps, args.warmup, A.neutral_how())
+        rt.close()
+        print(json.dumps({"step_only": True, "batch": args.batch, "tokens_per_s": round(tps, 2),
+                          "ms_per_step": round(ms, 4), "batch1_ms_per_step": round(ms1, 4)}))
+        return
     att_us, att_bytes = attention_rate(torch, L, batch_slots, args.context, shape.heads,
                                        shape.kv_heads, shape.head_dim, shape.layers)
     log(f"bench: attention batch {args.batch} ctx {args.context}: {att_us:.2f} us, "

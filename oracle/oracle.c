@@ -90,27 +90,47 @@ struct orc_gemv_job {
     const float *xf;
 };
 
+/* half(f) for the weight reader: the normal half range by integer rounding to nearest
+ * even (identical to orc_round_half there), everything else through orc_round_half. */
+static float orc_round_half_w(float f)
+{
+    union { float f; uint32_t u; } v = { f };
+    uint32_t mag = v.u & 0x7FFFFFFFu;
+    if (mag < 0x38800000u || mag >= 0x477FE000u) return orc_round_half(f);
+    v.u = (v.u + 0xFFFu + ((v.u >> 13) & 1u)) & 0xFFFFE000u;
+    return v.f;
+}
+
+/* Rows of a product. The reference reads a Q8_0 weight two ways: passes of up to 16 rows
+ * (gemv.cuh:68-98 through the group reader, matrix.cuh:499-512, and the one-row PTX
+ * module, gemv_q8.ptx:135-147) keep the fp32 product scale * q; passes of 17 rows or more
+ * run the tensor-core tile, which stages the weights as half (gemm.cuh:108-113), the
+ * value reader's half(scale * q) (matrix.cuh:413-422). The sum over k is serial fp32. */
 static void *orc_gemv_worker(void *arg)
 {
     struct orc_gemv_job *jb = (struct orc_gemv_job *)arg;
     size_t stride = (size_t)(jb->k / 32u) * 34u;
     unsigned int blocks = jb->k / 32u;
+    const int half_w = jb->m >= 17u;
+    float *wrow = (float *)malloc((size_t)jb->k * sizeof(float));
     for (unsigned int j = jb->lo; j < jb->hi; ++j) {
         const uint8_t *row = jb->w + stride * j;
+        for (unsigned int b = 0; b < blocks; ++b) {
+            const uint8_t *blk = row + (size_t)b * 34u;
+            float scale = orc_q8_scale(blk);
+            for (unsigned int e = 0; e < 32u; ++e) {
+                float wv = (float)(int)(int8_t)blk[2u + e] * scale;
+                wrow[b * 32u + e] = half_w ? orc_round_half_w(wv) : wv;
+            }
+        }
         for (unsigned int i = 0; i < jb->m; ++i) {
             const float *xr = jb->xf + (size_t)i * jb->k;
             float acc = 0.0f;
-            for (unsigned int b = 0; b < blocks; ++b) {
-                const uint8_t *blk = row + (size_t)b * 34u;
-                float scale = orc_q8_scale(blk);
-                for (unsigned int e = 0; e < 32u; ++e) {
-                    float wv = (float)(int)(int8_t)blk[2u + e] * scale;
-                    acc += wv * xr[b * 32u + e];
-                }
-            }
+            for (unsigned int c = 0; c < jb->k; ++c) acc += wrow[c] * xr[c];
             jb->y[(size_t)i * jb->n + j] = acc;
         }
     }
+    free(wrow);
     return NULL;
 }
 
@@ -443,6 +463,13 @@ void orc_model_forget(orc_model *m)
 }
 
 const float *orc_model_last_xnorm(const orc_model *m) { return m->last_xnorm; }
+
+/* The model's cache as fp16 words [slots][layers][max_context][kv_heads * head_dim]:
+ * which = 0 keys, 1 values. For tests that write the same cache into the device pages. */
+const uint16_t *orc_model_cache(const orc_model *m, unsigned int which)
+{
+    return which == 0u ? m->keys : m->values;
+}
 
 /* rows of half values in, fp32 products out: y[t][n] = W x[t] (reference GEMV sums) */
 static void orc_matmul(const orc_model *m, const uint8_t *w, unsigned int n, unsigned int k,

@@ -91,6 +91,7 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
 int orc_model_seat(orc_model *m, unsigned int slot, unsigned int position, uint64_t seed);
 /* The xnorm (half values as float) of the last row of each sequence of the last step. */
 const float *orc_model_last_xnorm(const orc_model *m);
+const uint16_t *orc_model_cache(const orc_model *m, unsigned int which);
 
 #ifdef __cplusplus
 }

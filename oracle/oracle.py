@@ -51,6 +51,8 @@ def lib():
         L.orc_model_seat.argtypes = [vp, u32, u32, u64]
         L.orc_model_last_xnorm.restype = ctypes.POINTER(f32)
         L.orc_model_last_xnorm.argtypes = [vp]
+        L.orc_model_cache.restype = ctypes.POINTER(ctypes.c_uint16)
+        L.orc_model_cache.argtypes = [vp, u32]
         _lib = L
     return _lib
 
@@ -121,6 +123,8 @@ class Model:
         self.weights = np.ascontiguousarray(weights, dtype=np.uint8)
         self.vocab = desc.vocab
         self.hidden = desc.hidden
+        self.max_context = max_context
+        self.slots = slots
         self.h = lib().orc_model_new(ctypes.byref(desc), _p(self.weights), slots,
                                      max_context, threads)
 
@@ -138,6 +142,17 @@ class Model:
     def last_xnorm(self, seqs):
         p = lib().orc_model_last_xnorm(self.h)
         return np.ctypeslib.as_array(p, shape=(seqs * self.hidden,)).reshape(seqs, self.hidden).copy()
+
+    def cache(self):
+        """Views of the cache, (keys, values) fp16 words [slots][layers][max_context][kv_heads *
+        head_dim], shared with the oracle (valid while the model lives)."""
+        d = self.desc
+        shp = (self.slots, d.layers, self.max_context, d.kv_heads * d.head_dim)
+        out = []
+        for which in (0, 1):
+            p = lib().orc_model_cache(self.h, which)
+            out.append(np.ctypeslib.as_array(p, shape=(int(np.prod(shp)),)).reshape(shp))
+        return out
 
     def seat(self, slots, position, seed=7):
         for s in slots:

@@ -108,6 +108,35 @@ def test_q8_gemv_f32_close_to_f64(orc):
     assert (np.abs(a - b) / np.maximum(np.abs(b), rms)).max() < 1e-2
 
 
+def test_q8_gemv_f32_reader_by_rows(orc):
+    """Passes of 17 rows or more read half(scale * q) (the tensor-core tile stages half
+    weights, cuda/model/gemm.cuh:108-113); 16 rows or fewer keep fp32(scale) * q. Each form
+    equals the double product of its own weights to fp32 sum rounding and not the other's;
+    a batch-16 row equals the same row inside a batch of 17 only to the half rounding."""
+    from aotx_amd.model import dequant_q8
+    rng = np.random.default_rng(8)
+    n, k = 96, 2048
+    w = _q8_random(rng, n, k)
+    x16 = rng.normal(0, 1, (17, k)).astype(np.float16)
+    blk = w.reshape(n, k // 32, 34)
+    sc = blk[:, :, :2].copy().view(np.float16).astype(np.float32)
+    q = blk[:, :, 2:].copy().view(np.int8).astype(np.float32)
+    w_f32 = (q * sc).reshape(n, k).astype(np.float64)
+    w_half = dequant_q8(w, k).astype(np.float64)
+    assert np.abs(w_f32 - w_half).max() > 0          # the two readers differ on these weights
+    xf = x16.astype(np.float64)
+    want_f32, want_half = xf @ w_f32.T, xf @ w_half.T
+    rms = np.sqrt((want_f32 ** 2).mean())
+
+    def err(a, b):
+        return (np.abs(a - b) / np.maximum(np.abs(b), rms)).max()
+    wide = orc.q8_gemv_f32(w, n, k, x16.view(np.uint16), threads=3)
+    narrow = orc.q8_gemv_f32(w, n, k, x16[:16].view(np.uint16), threads=3)
+    assert err(wide, want_half) < 2e-5 and err(wide, want_f32) > 5e-5
+    assert err(narrow, want_f32[:16]) < 2e-5 and err(narrow, want_half[:16]) > 5e-5
+    assert err(narrow, wide[:16]) < 1e-2
+
+
 def _allowed_numpy(row, top_k, top_p, min_p, temperature):
     """The allowed set restated in double precision (tests/sample_test.cu:177-224)."""
     row = np.asarray(row, dtype=np.float32)
