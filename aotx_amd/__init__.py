@@ -234,6 +234,7 @@ PROTOTYPES = {
     "aotx_q8r_gemv": (i32, [vp, u32, u32, vp, u32, vp, vp]),
     "aotx_q8r_gemv_f16": (i32, [vp, u32, u32, vp, u32, vp, vp]),
     "aotx_attend_paged": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
+    "aotx_attend_paged_static": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, u32, vp, vp]),
     "aotx_kv_write": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp]),
     "aotx_pick": (i32, [vp, u32, u32, vp, vp, u32, f32, f32, u64, vp, vp, vp]),
     "aotx_philox": (i32, [vp, vp, u32, vp, vp]),

@@ -38,6 +38,7 @@ struct aotx_state {
 
 /* The device state of the current device, allocated and zeroed on first use. */
 aotx_state *aotx_state_device(void);
+aotx_state *aotx_state_existing(void);
 
 /* Per-call scratch of the library (partial sums, arrival counters). One growable buffer
  * per use; counters are zeroed once at allocation and every kernel that uses one puts

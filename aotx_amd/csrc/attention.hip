@@ -147,6 +147,84 @@ extern "C" int aotx_attend_paged(const void *q, const unsigned int *pos,
                               AOTX_SEQ_MAX_TOKENS, nullptr, nullptr, aotx_stream(stream));
 }
 
+/* ---------------------------------------------------------------------------------------
+ * The allocation-free form of aotx_attend_paged.
+ *
+ * Its chunk partials and arrival counters live in `scratch`, a fixed array in device
+ * memory that each GPU holds from library load to process end, instead of the library's
+ * grow-on-demand scratch (which calls hipMalloc). Host code never uses the array's name as
+ * an address: the device address comes from hipGetSymbolAddress, once per device, and is
+ * kept per device. Every call on a GPU shares that GPU's array, so calls that overlap on
+ * one GPU race.
+ * ------------------------------------------------------------------------------------- */
+
+#define AOTX_ATTN_STATIC_PARTIAL (2u * 1024u * 1024u)   /* chunk partials, bytes */
+#define AOTX_ATTN_STATIC_COUNTS  4096u                    /* arrival counters, words */
+#define AOTX_MAX_DEVICES         64
+
+static __device__ __align__(256) unsigned char scratch[AOTX_ATTN_STATIC_PARTIAL + AOTX_ATTN_STATIC_COUNTS * 4u];
+
+static unsigned char *aotx_attn_static[AOTX_MAX_DEVICES];
+
+/* The device address of this device's `scratch` (0 when it cannot be resolved). */
+static unsigned char *aotx_attn_static_ptr(void)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= AOTX_MAX_DEVICES) return nullptr;
+    if (aotx_attn_static[dev] == nullptr) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            fprintf(stderr, "aotx: the attention scratch array has no device address\n");
+            return nullptr;
+        }
+        aotx_attn_static[dev] = (unsigned char *)ptr;
+    }
+    return aotx_attn_static[dev];
+}
+
+__global__ void aotx_attn_clear_kernel(unsigned int *count, unsigned int n)
+{
+    for (unsigned int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        count[i] = 0u;
+}
+
+extern "C" int aotx_attend_paged_static(const void *q, const unsigned int *pos,
+                                        const unsigned int *agent, unsigned int tokens,
+                                        unsigned int heads, unsigned int kv_heads,
+                                        unsigned int head_dim, unsigned int layer,
+                                        unsigned int layers, void *out, void *stream)
+{
+    if (q == nullptr || pos == nullptr || agent == nullptr || out == nullptr) return 1;
+    if (tokens == 0u || kv_heads == 0u || heads % kv_heads != 0u) return 1;
+    aotx_state *state = aotx_state_existing();
+    if (state == nullptr) {
+        fprintf(stderr, "aotx_attend_paged_static: no page pool is open on this process\n");
+        return 1;
+    }
+    /* the scratch this launch needs must fit the fixed array */
+    const unsigned int splits = aotx_attn_splits(tokens, kv_heads, AOTX_SEQ_MAX_TOKENS);
+    const size_t units = (size_t)tokens * kv_heads;
+    const size_t need = aotx_attn_scratch(tokens, kv_heads, splits, heads / kv_heads, head_dim);
+    if (units > AOTX_ATTN_STATIC_COUNTS || need > AOTX_ATTN_STATIC_PARTIAL) {
+        fprintf(stderr, "aotx_attend_paged_static: %u tokens x %u KV heads need %zu bytes of "
+                "partials and %zu counters; the fixed scratch holds %u and %u\n", tokens,
+                kv_heads, need, units, AOTX_ATTN_STATIC_PARTIAL, AOTX_ATTN_STATIC_COUNTS);
+        return 1;
+    }
+    unsigned char *base = aotx_attn_static_ptr();
+    if (base == nullptr) return 1;
+    float *partial = (float *)base;
+    unsigned int *count = (unsigned int *)(base + AOTX_ATTN_STATIC_PARTIAL);
+    hipStream_t s = aotx_stream(stream);
+    /* counters start at zero (a fill kernel, which a graph capture may hold) */
+    hipLaunchKernelGGL(aotx_attn_clear_kernel, dim3(((unsigned int)units + 255u) / 256u), dim3(256),
+                       0, s, count, (unsigned int)units);
+    AOTX_LAUNCH_CHECK();
+    return aotx_attend_launch((const unsigned short *)q, (unsigned short *)out, pos, agent,
+                              nullptr, tokens, heads, kv_heads, head_dim, layer, layers,
+                              AOTX_SEQ_MAX_TOKENS, partial, count, s);
+}
+
 /* K/V rows into the pages (the page-write half of cuda/model/rope.cu:128-196). */
 __global__ void aotx_kv_write_kernel(const unsigned short *k, const unsigned short *v,
                                      const unsigned int *pos, const unsigned int *agent,

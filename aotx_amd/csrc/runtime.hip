@@ -21,6 +21,12 @@ aotx_state *aotx_state_device(void)
     return aotx_state_ptr;
 }
 
+/* The state block if some call has created it, else null (allocates nothing). */
+aotx_state *aotx_state_existing(void)
+{
+    return aotx_state_ptr;
+}
+
 /* A small pinned host buffer for the few words the host reads back each step (the queue
  * marks of the page pool, a pass's offsets): copies into it skip the pageable staging. */
 void *aotx_pinned(void)

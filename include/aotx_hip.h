@@ -352,6 +352,20 @@ int aotx_attend_paged(const void *q, const unsigned int *pos, const unsigned int
                       unsigned int head_dim, unsigned int layer, unsigned int layers,
                       void *out, void *stream);
 
+/* aotx_attend_paged without any allocation: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The chunk partials and arrival counters live in a fixed
+ * device array of the library (2 MiB of partials, 4096 counters, held by each GPU the
+ * library runs on until the process ends) instead of the grow-on-demand scratch. Same
+ * arguments, kernels and results as aotx_attend_paged. Returns 1 (and prints why) when
+ * the launch's partials or counters exceed the array (at most 4096 tokens x KV heads;
+ * split launches of few tokens need partials), or when no page pool has been opened.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race. */
+int aotx_attend_paged_static(const void *q, const unsigned int *pos, const unsigned int *agent,
+                             unsigned int tokens, unsigned int heads, unsigned int kv_heads,
+                             unsigned int head_dim, unsigned int layer, unsigned int layers,
+                             void *out, void *stream);
+
 /* Write K (rotated) and V rows of tokens into the pages (the KV half of
  * cuda/model/rope.cu:200-234); k, v fp16 [tokens][kv_heads][d] already rotated. */
 int aotx_kv_write(const void *k, const void *v, const unsigned int *pos,
