@@ -197,7 +197,6 @@ PROTOTYPES = {
     "aotx_model_restream": (None, []),
     "aotx_model_faulted": (u32, []),
     "aotx_model_nodes": (u32, [u32]),
-    "aotx_model_chained": (u32, [u32, u32]),
     "aotx_model_pages": (i32, [u32, vp, u32, vp]),
     "aotx_model_launch": (i32, [u32, ctypes.POINTER(ModelRun)]),
     "aotx_model_sample": (i32, [u32, vp, vp, u32, vp, ctypes.POINTER(ModelHow), vp, vp,

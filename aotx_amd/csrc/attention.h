@@ -11,8 +11,7 @@ unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
 size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned int splits,
                          unsigned int group, unsigned int head_dim);
 struct aotx_attn_args;
-/* The arguments of a launch over these operands (the layer chain runs them as a stage);
- * 1 when the shape is refused. */
+/* The arguments of a launch over these operands; 1 when the shape is refused. */
 int aotx_attend_plan(aotx_attn_args *args, const unsigned short *q, unsigned short *out,
                      const unsigned int *pos, const unsigned int *agent,
                      const unsigned int *m_dev, unsigned int tokens, unsigned int heads,

@@ -28,8 +28,7 @@
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_mma(aotx_attn_args a)
 {
-    aotx_no_wait w;
-    aotx_attend_body<D, G, W, false>(a, blockIdx.x, w);
+    aotx_attend_body<D, G, W>(a, blockIdx.x);
 }
 
 /* ---------------------------------------------------------------------------------------
@@ -61,7 +60,7 @@ size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned in
     return (size_t)tokens * kv_heads * splits * group * (head_dim + 2u) * sizeof(float);
 }
 
-/* The arguments of one launch (or chain stage); 1 when the shape is refused. */
+/* The arguments of one launch; 1 when the shape is refused. */
 int aotx_attend_plan(aotx_attn_args *out_args, const unsigned short *q, unsigned short *out,
                      const unsigned int *pos, const unsigned int *agent,
                      const unsigned int *m_dev, unsigned int tokens, unsigned int heads,

@@ -1,5 +1,4 @@
-/* Device code of paged decode attention (attention.hip): the per-workgroup body, shared
- * by the standalone kernel and the layer chain (chain.hip).
+/* Device code of paged decode attention (attention.hip): the per-workgroup body.
  */
 #ifndef AOTX_ATTENTION_DEV_H
 #define AOTX_ATTENTION_DEV_H
@@ -76,9 +75,8 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
  *     against bank conflicts) to a private LDS slot and reads 16-bit columns back;
  *   - online softmax in base 2 per head with a max over the 4 lane groups of the head.
  * The output accumulators hold heads 4g..4g+3 x 16 d columns per lane and PV step. */
-template <int D, int G, int W, bool CH, class Wait>
-static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a, unsigned int bx,
-                                                        Wait &wait)
+template <int D, int G, int W>
+static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a, unsigned int bx)
 {
     static_assert(G <= 16, "one MFMA tile of query heads");
     constexpr int KK = D / 32;          /* score MFMA steps */
@@ -115,13 +113,12 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const aotx_kv_table *kv = &a.state->kv;
     const float scale = 1.4426950408889634f / sqrtf((float)D);
 
-    wait();
     aotx_h8a qb[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
         aotx_u4a w = {0u, 0u, 0u, 0u};
         if (r < (unsigned int)G)
-            w = co_load4<CH>(a.q + ((unsigned long long)t * a.heads + kh * G + r) * D
+            w = co_load4(a.q + ((unsigned long long)t * a.heads + kh * G + r) * D
                              + 32 * kk + 8 * g);
         qb[kk] = __builtin_bit_cast(aotx_h8a, w);
     }
@@ -135,9 +132,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     unsigned short *vw = vl[wave];
 
     aotx_u4a kr[2][KK], vr[2][VP];
-    /* in a chain the newest position's keys and values were written by an earlier stage of
-     * the same launch: every block is read with device-scope loads (sc1) */
-    constexpr int CPOL = CH ? 16 : 0;
+    constexpr int CPOL = 0;                  /* cache policy of the block loads */
     bool absent[2];
     unsigned long long pages = 0ull;
     unsigned int wbase = b0;
@@ -273,7 +268,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         }
         if (st == 1u) {
             float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-            co_store2h<CH>(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+            co_store2h(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
                            aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
         } else {
             aotx_attn_put(mine + j * (D + 2) + 2 + e, osum[0]);
@@ -327,7 +322,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
             }
         }
         const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-        co_store2h<CH>(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+        co_store2h(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
                        aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
     }
 }

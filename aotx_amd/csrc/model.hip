@@ -24,7 +24,6 @@
 #include "aotx_internal.h"
 #include "../../include/aotx_plan.h"
 #include "attention.h"
-#include "chain.h"
 #include "experts.h"
 #include "gemv.h"
 #include "norm.h"
@@ -82,14 +81,6 @@ struct aotx_hold {
     unsigned int *elist, *ecount;
     void *piece[48];
     unsigned int pieces;
-    /* the layer chain of each token bucket it serves (null: per-kernel sequence) */
-    aotx_chain_stage *chain[AOTX_BUCKETS];
-    unsigned int chain_stages[AOTX_BUCKETS];
-    size_t chain_lds[AOTX_BUCKETS];
-    unsigned int *chain_done;     /* arrival counters, zero between launches */
-    float *chain_partial;         /* split partials of chain stages */
-    size_t chain_partial_bytes;
-    unsigned int *chain_stall;    /* host-visible: a chain wait ran out of time */
     /* graphs per row selection, token bucket and head-row bucket */
     hipGraphExec_t exec[2][AOTX_BUCKETS][AOTX_BUCKETS];
     unsigned int nodes;
@@ -291,159 +282,6 @@ static void aotx_roperands(aotx_rgemv_args *p, const aotx_rgemv_args &tmpl)
     }
 }
 
-/* ---- the layer chain ---------------------------------------------------------------- */
-
-#define AOTX_CHAIN_MAX_TOKENS 16u
-
-/* A model whose every layer the chain can run: dense, adjacent-pair rotary with the page
- * write fused into the QKV product, d = 128 with 4 query heads per KV head. The chain is
- * opt-in (AOTX_CHAIN=1 at model open): at the 8B shape and batch 1 it measured 3.4 ms per
- * step against 2.54 ms for the per-kernel sequence. A workgroup's arrival poll and its x
- * loads retire behind the weights it prefetched (the vector memory counter is in order),
- * the stage hand-offs cross the memory system under that prefetch traffic (3-5 us each),
- * and the attention body keeps the launch at one workgroup per CU. */
-static int aotx_chain_fits(const aotx_model_desc *d)
-{
-    const char *v = getenv("AOTX_CHAIN");
-    if (v == nullptr || v[0] != '1') return 0;
-    if (d->expert_count != 0u || d->head_dim != 128u || d->heads != 4u * d->kv_heads) return 0;
-    if (d->hidden % 8u != 0u || d->ffn % 8u != 0u) return 0;
-    for (unsigned int l = 0; l < d->layers; ++l)
-        if (!aotx_fused_qkv(d, l)) return 0;
-    return 1;
-}
-
-/* One product stage of the chain; 1 when the plan is refused or exceeds the buffers. */
-static int aotx_chain_product(aotx_hold *h, aotx_chain_stage *st, const void *const *w,
-                              const unsigned int *rows, unsigned int nseg, unsigned int k,
-                              int epi, unsigned int T, const aotx_rgemv_args &tmpl)
-{
-    memset(st, 0, sizeof *st);
-    aotx_rgemv_args &a = st->g;
-    if (aotx_rgemv_plan_chain(&a, w, rows, nseg, k, epi, T, AOTX_CHAIN_LDS) != 0) return 1;
-    aotx_roperands(&a, tmpl);
-    a.m_dev = &h->step->run.tokens;
-    a.m0 = 0u;
-    if (a.splits > 1u) {
-        const size_t need = aotx_rgemv_partial_bytes(a);
-        if (a.groups > AOTX_GEMV_COUNTS) return 1;
-        if (need > h->chain_partial_bytes) {
-            /* a larger buffer for this and later tables (earlier ones keep theirs) */
-            h->chain_partial = (float *)aotx_take(h, need);
-            h->chain_partial_bytes = need;
-        }
-        a.partial = h->chain_partial;
-        a.count = h->gemv_count;
-    }
-    /* quads per load: a wave's share of an item in two loads where that fits */
-    const unsigned int per = (a.qps + 7u) / 8u;
-    st->kind = epi == AOTX_EPI_SWIGLU ? AOTX_CHAIN_PAIR
-             : (per > 4u ? AOTX_CHAIN_TILE_LONG : AOTX_CHAIN_TILE);
-    st->items = a.groups * a.splits;
-    return 0;
-}
-
-/* The stage table of token bucket T (every layer, five stages each), uploaded to the
- * device; 1 when some stage cannot run in the chain. */
-static int aotx_chain_build(aotx_hold *h, unsigned int bt)
-{
-    const aotx_model_desc *d = &h->desc;
-    const unsigned int T = 1u << bt;
-    const unsigned int hd = d->head_dim;
-    const unsigned int wide = d->heads * hd, narrow = d->kv_heads * hd;
-    const unsigned int n = 5u * d->layers;
-    aotx_chain_stage *tab = (aotx_chain_stage *)calloc(n, sizeof *tab);
-    if (tab == nullptr) return 1;
-    int bad = 0;
-    for (unsigned int l = 0; l < d->layers && !bad; ++l) {
-        const aotx_model_layer *L = &d->layer[l];
-        const aotx_rlayer *RL = &h->rl[l];
-        aotx_chain_stage *st = tab + 5u * l;
-        /* QKV: x = the attention norm of the residual stream; rotary turn + page write */
-        aotx_rgemv_args t;
-        memset(&t, 0, sizeof t);
-        t.xmode = AOTX_X_NORM;
-        t.resid = h->resid;
-        t.norm_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_ATTN_NORM]);
-        t.sumsq = h->sumsq;
-        t.eps = d->rms_eps;
-        t.qkv.qh = h->qh;
-        t.qkv.pos = h->pos;
-        t.qkv.agent = h->tagent;
-        t.qkv.state = aotx_state_device();
-        t.qkv.shape = aotx_kvl_make(d->layers, d->kv_heads, hd);
-        t.qkv.layer = l;
-        t.qkv.heads = d->heads;
-        t.qkv.kv_heads = d->kv_heads;
-        t.qkv.head_dim = hd;
-        t.qkv.theta = d->rope_theta;
-        t.qkv.factor = (const float *)aotx_tensor(d->rope_freqs);
-        const void *qkv_w[3] = {RL->q, RL->k, RL->v};
-        unsigned int qkv_rows[3] = {wide, narrow, narrow};
-        bad |= aotx_chain_product(h, st + 0, qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_QKV, T, t);
-        /* attention */
-        st[1].kind = AOTX_CHAIN_ATTEND;
-        bad |= aotx_attend_plan(&st[1].t, h->qh, h->att, h->pos, h->tagent, &h->step->run.tokens,
-                                T, d->heads, d->kv_heads, hd, l, d->layers, AOTX_SEQ_MAX_TOKENS,
-                                h->attn_partial, h->attn_count);
-        st[1].items = T * d->kv_heads * st[1].t.splits;
-        /* O + residual */
-        memset(&t, 0, sizeof t);
-        t.xmode = AOTX_X_F16;
-        t.x = h->att;
-        t.ldx = wide;
-        t.y = h->resid;
-        t.ldy = d->hidden;
-        t.sumsq_out = h->sumsq;
-        const void *o_w[1] = {RL->o};
-        unsigned int o_rows[1] = {d->hidden};
-        bad |= aotx_chain_product(h, st + 2, o_w, o_rows, 1u, wide, AOTX_EPI_RESID, T, t);
-        /* gate/up + SwiGLU: x = the FFN norm of the residual stream */
-        memset(&t, 0, sizeof t);
-        t.xmode = AOTX_X_NORM;
-        t.resid = h->resid;
-        t.norm_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_FFN_NORM]);
-        t.sumsq = h->sumsq;
-        t.eps = d->rms_eps;
-        t.y = h->act;
-        t.ldy = d->ffn;
-        const void *gu_w[2] = {RL->gate, RL->up};
-        unsigned int gu_rows[2] = {d->ffn, d->ffn};
-        bad |= aotx_chain_product(h, st + 3, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, t);
-        /* down + residual */
-        memset(&t, 0, sizeof t);
-        t.xmode = AOTX_X_F16;
-        t.x = h->act;
-        t.ldx = d->ffn;
-        t.y = h->resid;
-        t.ldy = d->hidden;
-        t.sumsq_out = h->sumsq;
-        const void *dn_w[1] = {RL->down};
-        unsigned int dn_rows[1] = {d->hidden};
-        bad |= aotx_chain_product(h, st + 4, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_RESID, T, t);
-    }
-    /* each stage waits for the one before it (the first for nothing: its inputs come from
-     * the gather kernel, an earlier launch) */
-    size_t lds = 0u;
-    for (unsigned int i = 0; i < n && !bad; ++i) {
-        tab[i].wait = i == 0u ? 0u : i;
-        tab[i].wait_items = i == 0u ? 0u : tab[i - 1u].items;
-        if (tab[i].kind != AOTX_CHAIN_ATTEND) {
-            const size_t b = aotx_rgemv_chain_lds(tab[i].g);
-            lds = b > lds ? b : lds;
-        }
-    }
-    if (!bad && aotx_chain_grid(lds) == 0u) bad = 1;
-    if (!bad) {
-        h->chain[bt] = (aotx_chain_stage *)aotx_take(h, n * sizeof *tab);
-        AOTX_CHECK(hipMemcpy(h->chain[bt], tab, n * sizeof *tab, hipMemcpyHostToDevice));
-        h->chain_stages[bt] = n;
-        h->chain_lds[bt] = lds;
-    }
-    free(tab);
-    return bad;
-}
-
 /* ---- the step ---------------------------------------------------------------------- */
 
 static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br)
@@ -459,7 +297,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     const unsigned int wide = d->heads * hd, narrow = d->kv_heads * hd;
     const aotx_kvl_shape shape = aotx_kvl_make(d->layers, d->kv_heads, hd);
     const unsigned int max_context = AOTX_SEQ_MAX_TOKENS;
-    const bool fused_norm = T <= 16u;                /* x staged from the residual stream */
+    const bool fused_norm = T <= AOTX_NARROW_ROWS;   /* x staged from the residual stream */
     const bool experts = d->expert_count != 0u;
     /* wide batches of a dense model: the residual epilogue that ends each half also writes
      * x = half(resid * w) for the next norm's weights w, and the next product multiplies its
@@ -480,11 +318,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     nrm.hidden = d->hidden;
     nrm.x = h->x;
 
-    const bool chained = h->chain[bt] != nullptr;
-    if (chained)
-        aotx_chain_launch(h->chain[bt], h->chain_stages[bt], h->chain_done, h->chain_stall,
-                          h->chain_lds[bt], s);
-    for (unsigned int l = 0; l < d->layers && !chained; ++l) {
+    for (unsigned int l = 0; l < d->layers; ++l) {
         const aotx_model_layer *L = &d->layer[l];
         const aotx_rlayer *RL = &h->rl[l];
         const float *attn_w = (const float *)aotx_tensor(L->offset[AOTX_SLOT_ATTN_NORM]);
@@ -835,13 +669,6 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     AOTX_CHECK(hipHostMalloc((void **)&h->pinned, sizeof(aotx_step), hipHostMallocDefault));
     memset(h->pinned, 0, sizeof(aotx_step));
     h->step = (aotx_step *)aotx_take(h, sizeof(aotx_step));
-    if (aotx_chain_fits(d)) {
-        AOTX_CHECK(hipHostMalloc((void **)&h->chain_stall, sizeof(unsigned int), hipHostMallocDefault));
-        *h->chain_stall = 0u;
-        h->chain_done = (unsigned int *)aotx_take(h, aotx_chain_words(5u * d->layers) * sizeof(unsigned int));
-        for (unsigned int bt = 0; (1u << bt) <= cap && (1u << bt) <= AOTX_CHAIN_MAX_TOKENS; ++bt)
-            if (aotx_chain_build(h, bt) != 0) h->chain[bt] = nullptr;
-    }
     AOTX_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     AOTX_CHECK(hipDeviceSynchronize());
     h->ready = 1;
@@ -860,7 +687,6 @@ extern "C" void aotx_model_shut(unsigned int role)
                 if (h->exec[a][i][j] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->exec[a][i][j]));
     AOTX_CHECK(hipStreamDestroy(h->stream));
     AOTX_CHECK(hipHostFree(h->pinned));
-    if (h->chain_stall != nullptr) AOTX_CHECK(hipHostFree(h->chain_stall));
     for (unsigned int i = 0; i < h->pieces; ++i) AOTX_CHECK(hipFree(h->piece[i]));
     aotx_model_desc keep = h->desc;
     int described = h->described;
@@ -907,14 +733,6 @@ extern "C" unsigned int aotx_model_nodes(unsigned int role)
 {
     if (role >= AOTX_MODEL_ROLES) return 0u;
     return aotx_holds[role].nodes;
-}
-
-extern "C" unsigned int aotx_model_chained(unsigned int role, unsigned int tokens)
-{
-    if (role >= AOTX_MODEL_ROLES || tokens == 0u) return 0u;
-    const aotx_hold *h = &aotx_holds[role];
-    if (!h->ready || tokens > h->max_tokens) return 0u;
-    return h->chain[aotx_bucket_of(tokens)] != nullptr ? 1u : 0u;
 }
 
 extern "C" int aotx_model_pages(unsigned int role, const unsigned int *offset, unsigned int seqs,
@@ -969,11 +787,6 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
                                   hipMemcpyDeviceToDevice, h->stream));
     }
     AOTX_CHECK(hipStreamSynchronize(h->stream));
-    if (h->chain_stall != nullptr && *(volatile unsigned int *)h->chain_stall != 0u) {
-        fprintf(stderr, "aotx: a wait of the layer chain ran out of time; the step's results are void\n");
-        *h->chain_stall = 0u;
-        return 1;
-    }
     return 0;
 }
 

@@ -90,19 +90,13 @@ struct aotx_rgemv_args {
 };
 
 /* Plan a product over Q8R tensors; rows per segment; returns 1 when refused. mt is the
- * pass capacity: up to 16 rows take the streaming kernel, up to 32 the wide kernel, and
- * up to AOTX_RGEMM_ROWS the GEMM. */
+ * pass capacity: up to AOTX_NARROW_ROWS rows take the streaming kernel (which can stage x
+ * as the RMSNorm of the residual stream), up to 32 the wide kernel, and up to
+ * AOTX_RGEMM_ROWS the GEMM. */
+#define AOTX_NARROW_ROWS 4u
 #define AOTX_RGEMM_ROWS 512u
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                     unsigned int nseg, unsigned int k, int epi, unsigned int mt);
-/* Plan a product as a stage of the layer chain (chain.hip): one 16-row tile per item (a
- * gate/up pair for SWIGLU), 8 waves, k split only as far as the staged x rows of an item
- * need to fit `lds_cap` bytes. */
-int aotx_rgemv_plan_chain(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
-                          unsigned int nseg, unsigned int k, int epi, unsigned int mt,
-                          size_t lds_cap);
-/* Dynamic LDS bytes of a chain stage of the plan (staged x, then the wave reduction). */
-size_t aotx_rgemv_chain_lds(const aotx_rgemv_args &a);
 /* Launch one pass (<= 32 rows) and, with splits > 1, the kernel that adds the partials
  * and applies the epilogue. */
 void aotx_rgemv_launch(const aotx_rgemv_args &a, hipStream_t stream);

@@ -72,8 +72,7 @@ template <int MT, int RT, int PD, int NW>
 __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    aotx_no_wait w;
-    rg_narrow<MT, RT, PD, NW, false>(a, blockIdx.x, blockIdx.y, lds, w);
+    rg_narrow<MT, RT, PD, NW>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 /* Wide batches (17..32 rows of fp16 x): a workgroup owns T 16-row tiles; its W = T * P
@@ -510,7 +509,11 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         a->qps = a->qn;
         return 0;
     }
-    if (mt > 16u) {
+    /* 5 to 32 rows: the wide kernel. With 32 batch columns per MFMA it wastes matrix-core
+     * work below 32 rows, but the matrix cores are not what bounds these products: at 8
+     * rows it streams the config-2 shapes 1.0-1.5x faster than the streaming kernel, whose
+     * per-workgroup x staging grows with the rows; at 2 rows the streaming kernel wins. */
+    if (mt > AOTX_NARROW_ROWS) {
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
         /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
          * tiles (gate/up pair, head), 4 x 2 for a 14336-row matrix, 2 x 4 for few (QKV, O,
@@ -534,10 +537,10 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
     }
-    /* rows per workgroup: 4 tiles share the staged x of 9-16 batch rows; fewer rows take
-     * one tile (measured best at every 8B shape), the gated unit two gate/up pairs. */
+    /* rows per workgroup: one tile (measured best at every 8B shape), the gated unit two
+     * gate/up pairs. */
     const aotx_rgemv_tune &tune = aotx_rgemv_tuning();
-    unsigned int rt = mt > 8u ? 4u : 1u;
+    unsigned int rt = 1u;
     if (tune.rt != 0u) rt = tune.rt;
     /* the gated unit takes two gate/up pairs per workgroup: its 448 workgroups are resident
      * at once (896 single pairs ran in two rounds) */
@@ -566,29 +569,6 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
      * the quads to dequantise after its data arrives), 4 otherwise */
     a->nw = a->groups * a->splits <= tune_nw_limit() ? 8u : 4u;
     return 0;
-}
-
-int aotx_rgemv_plan_chain(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
-                          unsigned int nseg, unsigned int k, int epi, unsigned int mt,
-                          size_t lds_cap)
-{
-    if (mt > 16u || aotx_rgemv_plan(a, w, rows, nseg, k, epi, mt) != 0) return 1;
-    a->rt = epi == AOTX_EPI_SWIGLU ? 2u : 1u;
-    a->pd = 4u;
-    a->nw = 8u;
-    a->groups = epi == AOTX_EPI_SWIGLU ? (unsigned int)aotx_q8r_tiles(a->n)
-                                       : (a->n + 15u) / 16u;
-    for (unsigned int s = 1u; s <= a->qn; ++s) {
-        a->qps = (a->qn + s - 1u) / s;
-        a->splits = (a->qn + a->qps - 1u) / a->qps;
-        if (aotx_rgemv_chain_lds(*a) <= lds_cap) return 0;
-    }
-    return 1;
-}
-
-size_t aotx_rgemv_chain_lds(const aotx_rgemv_args &a)
-{
-    return (size_t)rg_chain_xbytes(a) + (size_t)(a.nw + 1u) * a.rt * 16u * 16u * 4u;
 }
 
 size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)

@@ -1,5 +1,5 @@
 /* Device code of the streaming Q8 product (rgemv.hip): operand helpers, epilogues and
- * the narrow-batch body, shared by the standalone kernels and the layer chain (chain.hip).
+ * the narrow-batch body.
  */
 #ifndef AOTX_RGEMV_DEV_H
 #define AOTX_RGEMV_DEV_H
@@ -45,8 +45,8 @@ static __device__ __forceinline__ void rg_dequant4(unsigned int u, rg_h2 s2, uns
 
 /* The segment holding output row v, and the first row of that segment. Written as sums
  * of one-sided selects, never a select between two fields: the compiler turns the latter
- * into one load from a computed offset, which keeps a copy of the arguments (the layer
- * chain makes one) in scratch memory instead of registers. */
+ * into one load from a computed offset, which can keep a copy of the arguments in
+ * scratch memory instead of registers. */
 static __device__ __forceinline__ unsigned int rg_seg(const aotx_rgemv_args &a, unsigned int v,
                                                       unsigned int &begin)
 {
@@ -133,10 +133,8 @@ static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a,
     return (group * rt + j) * 16u + rr;
 }
 
-/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. CH: the
- * results are read by later stages of the same launch (device-scope stores; the F16 and
- * plain residual forms are not used there). */
-template <int MT, int NT, bool CH = false>
+/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. */
+template <int MT, int NT>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
                                                    unsigned int mrows, const unsigned int *list,
@@ -162,9 +160,9 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             float v = 0.0f;
             if (col_ok) {
                 float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
-                v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : co_loadf<CH>(p))
+                v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : co_loadf(p))
                   + out[(j * 16u + rr) * MT + mm];
-                co_storef<CH>(p, v);
+                co_storef(p, v);
             }
             if (a.xg_out != nullptr && col_ok)
                 a.xg_out[(unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
@@ -174,7 +172,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             sq += __shfl_xor(sq, 4, 64);
             sq += __shfl_xor(sq, 8, 64);
             if (row_ok && rr == 0u)
-                co_storef<CH>(a.sumsq_out + (unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
+                co_storef(a.sumsq_out + (unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
         }
     } else if (a.epi == AOTX_EPI_F32 || a.epi == AOTX_EPI_F16 || a.epi == AOTX_EPI_RESID) {
         for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
@@ -183,7 +181,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             if (mm >= mrows || v >= a.n) continue;
             float val = out[row * MT + mm];
             unsigned long long at = (unsigned long long)RG_YROW(mm) * a.ldy + v;
-            if (a.epi == AOTX_EPI_F32) co_storef<CH>((float *)a.y + at, val);
+            if (a.epi == AOTX_EPI_F32) co_storef((float *)a.y + at, val);
             else if (a.epi == AOTX_EPI_F16) ((unsigned short *)a.y)[at] = aotx_f2h(val);
             else ((float *)a.y)[at] += val;
         }
@@ -203,8 +201,8 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                 h[e] = aotx_f2h(unit * up);
             }
             unsigned short *dst = (unsigned short *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v;
-            if (v + 1u < a.n) co_store2h<CH>(dst, h[0], h[1]);
-            else dst[0] = (unsigned short)h[0];            /* odd n (never in a chain) */
+            if (v + 1u < a.n) co_store2h(dst, h[0], h[1]);
+            else dst[0] = (unsigned short)h[0];            /* odd n */
         }
     } else if (a.epi == AOTX_EPI_QKV) {
         const aotx_qkv_epi &e = a.qkv;
@@ -230,7 +228,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                 float sn, cs;
                 sincosf(angle, &sn, &cs);
                 unsigned short *dst = e.qh + (unsigned long long)t * e.heads * d + local;
-                co_store2h<CH>(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
+                co_store2h(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
                 continue;
             }
             unsigned char *blk = aotx_kvl_block(e.shape, &e.state->kv, e.agent[t], e.layer, position);
@@ -246,9 +244,9 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                 if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
                 float sn, cs;
                 sincosf(angle, &sn, &cs);
-                co_store2h<CH>(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
+                co_store2h(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
             } else {
-                co_store2h<CH>(dst, aotx_f2h(a0), aotx_f2h(a1));
+                co_store2h(dst, aotx_f2h(a0), aotx_f2h(a1));
             }
         }
     }
@@ -308,25 +306,24 @@ static __device__ __forceinline__ rg_u4 rg_norm_piece(rg_u4 r0, rg_u4 r1, rg_u4 
 
 /* Eight values of row `src` of x from k = kk (fp16 x, or the fused norm of the residual
  * stream when scale != 0 is given for AOTX_X_NORM); k past a.k gives zeros. */
-template <bool CH>
 static __device__ __forceinline__ rg_u4 rg_x_piece(const aotx_rgemv_args &a, unsigned int src,
                                                    unsigned int kk, float scale)
 {
     if (a.xmode == AOTX_X_NORM) {
         const float *rrow = a.resid + (unsigned long long)src * a.k;
         if (kk + 8u <= a.k)
-            return rg_norm_piece(co_load4<CH>(rrow + kk), co_load4<CH>(rrow + kk + 4u),
+            return rg_norm_piece(co_load4(rrow + kk), co_load4(rrow + kk + 4u),
                                  *(const rg_u4 *)(a.norm_w + kk), *(const rg_u4 *)(a.norm_w + kk + 4u),
                                  scale);
         unsigned int h[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             unsigned int kc = kk + (unsigned int)e;
-            h[e] = kc < a.k ? aotx_f2h(scale * co_loadf<CH>(rrow + kc) * a.norm_w[kc]) : 0u;
+            h[e] = kc < a.k ? aotx_f2h(scale * co_loadf(rrow + kc) * a.norm_w[kc]) : 0u;
         }
         return (rg_u4){h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
     }
-    if (kk + 8u <= a.k) return co_load4<CH>(a.x + (unsigned long long)src * a.ldx + kk);
+    if (kk + 8u <= a.k) return co_load4(a.x + (unsigned long long)src * a.ldx + kk);
     unsigned int h[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -383,10 +380,9 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
  * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
  * few tiles, so that each wave's share of the dequantisation is short). */
-template <int MT, int RT, int PD, int NW, bool CH, class Wait>
+template <int MT, int RT, int PD, int NW>
 static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsigned int bx,
-                                                 unsigned int expert, unsigned char *lds,
-                                                 Wait &wait)
+                                                 unsigned int expert, unsigned char *lds)
 {
     constexpr unsigned int NT = 64u * NW;
     const unsigned int tid = threadIdx.x;
@@ -498,9 +494,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
      * be waited for without it. ---- */
     constexpr int RG_PRE = 2;
     const bool direct = list == nullptr && a.xrow == nullptr;
-    /* in a chain (CH) x is the product of an earlier stage of the same launch: it is
-     * loaded before the weights only once this workgroup has seen that stage complete */
-    const bool early = direct && (!CH || wait.seen);
+    const bool early = direct;
     const bool norm = a.xmode == AOTX_X_NORM;
     const bool resid_pre = early && a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
     const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
@@ -521,12 +515,12 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
             if (mm < cap && kk + 8u <= a.k) {
                 if (norm) {
                     const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
-                    pre[i][0] = co_load4<CH>(rrow);
-                    pre[i][1] = co_load4<CH>(rrow + 4);
+                    pre[i][0] = co_load4(rrow);
+                    pre[i][1] = co_load4(rrow + 4);
                     pre[i][2] = *(const rg_u4 *)(a.norm_w + kk);
                     pre[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
                 } else {
-                    pre[i][0] = co_load4<CH>(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
+                    pre[i][0] = co_load4(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
                 }
             }
         }
@@ -535,7 +529,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const unsigned int at = l + 16u * (unsigned int)i;
-                ssp[i] = mm < cap && at < nss ? co_loadf<CH>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
+                ssp[i] = mm < cap && at < nss ? co_loadf(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
             }
         }
     }
@@ -548,15 +542,14 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
             const unsigned int j = rest % RT, mm = rest / RT;
             const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
             rold[it] = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n
-                ? co_loadf<CH>((const float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr) : 0.0f;
+                ? co_loadf((const float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr) : 0.0f;
         }
     }
 
     /* with one tile per workgroup only the first buffer goes out before the staging, so
      * every workgroup's x requests queue behind less of the grid's weight stream (measured
      * faster for every one-tile shape; a gate/up pair keeps both buffers ahead) */
-    /* (a chain item that still has to wait issues both, so that they load while it waits) */
-    const bool both_first = RT > 1 || (CH && !early);
+    const bool both_first = RT > 1;
     RG_LOAD(0, wq0);
     if (both_first) RG_LOAD(1, wq0 + PD);
     if (a.expert_stride == 0ull && a.m_dev != nullptr) {
@@ -566,7 +559,6 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     if (mrows > a.m) mrows = a.m;
     if (mrows > (unsigned int)MT) mrows = MT;
     if (mrows == 0u) return;
-    if (!early) wait();
 
     /* ---- stage the batch rows of x for [q0, q1) ---- */
     {
@@ -584,11 +576,11 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                     for (int i = 0; i < 16; ++i) sum += ssp[i];
                     if (mm < mrows)
                         for (unsigned int i = l + 256u; i < nss; i += 16u)
-                            sum += co_loadf<CH>(a.sumsq + (unsigned long long)src * nss + i);
+                            sum += co_loadf(a.sumsq + (unsigned long long)src * nss + i);
                 } else if (mm < mrows) {
                     const float *ss = a.sumsq + (unsigned long long)src * nss;
 #pragma unroll 4
-                    for (unsigned int i = l; i < nss; i += 16u) sum += co_loadf<CH>(ss + i);
+                    for (unsigned int i = l; i < nss; i += 16u) sum += co_loadf(ss + i);
                 }
                 sum += __shfl_xor(sum, 1, 64);
                 sum += __shfl_xor(sum, 2, 64);
@@ -618,13 +610,13 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                     v = norm ? rg_norm_piece(pre[i][0], pre[i][1], pre[i][2], pre[i][3], xscale[mm])
                              : pre[i][0];
                 else
-                    v = rg_x_piece<CH>(a, xsrc[mm], kk, norm ? xscale[mm] : 0.0f);
+                    v = rg_x_piece(a, xsrc[mm], kk, norm ? xscale[mm] : 0.0f);
                 *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
             }
         }
         for (unsigned int idx = tid + RG_PRE * NT; idx < total; idx += NT) {
             const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-            *(rg_u4 *)(xl + mm * xs + p * 8u) = rg_x_piece<CH>(a, xsrc[mm], kbeg + p * 8u,
+            *(rg_u4 *)(xl + mm * xs + p * 8u) = rg_x_piece(a, xsrc[mm], kbeg + p * 8u,
                                                               norm ? xscale[mm] : 0.0f);
         }
         rg_sync_lds();
@@ -674,298 +666,8 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
         __shared__ unsigned int last;
         if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
-    rg_epilogue<MT, NT, CH>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
+    rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
 }
 
-
-/* Bytes of the staged x rows of a chain stage (the front of its dynamic LDS; the wave
- * reduction area follows). */
-static __host__ __device__ __forceinline__ unsigned int rg_chain_xbytes(const aotx_rgemv_args &a)
-{
-    return (a.m * (a.qps * 128u + 8u) * 2u + 15u) / 16u * 16u;
-}
-
-/* One workgroup's share of a product stage of the layer chain: items it0, it0 + step, ...
- * below `items` (item = group * splits + split, as for rg_narrow; direct batch rows,
- * operands written by earlier stages of the same launch). Each wave's weight loads form
- * one stream over all of its items, two chunks of PD quads ahead of the MFMAs, so the
- * loads of the next item are in flight while this one is reduced and written; the staged
- * x stays in LDS for every item of the same k range. The first item's loads are issued
- * before the wait for the stage's inputs. Returns the number of items done. */
-template <int MT, int RT, int PD, int NW, class Wait>
-static __device__ __forceinline__ unsigned int rg_chain_stage(const aotx_rgemv_args &a,
-                                                              unsigned int it0, unsigned int step,
-                                                              unsigned int items,
-                                                              unsigned char *lds, Wait &wait)
-{
-    constexpr unsigned int NT = 64u * NW;
-    const unsigned int tid = threadIdx.x;
-    const unsigned int lane = tid & 63u;
-    const unsigned int wave = tid >> 6;
-    const unsigned int r = lane & 15u, g = lane >> 4;
-    if (it0 >= items) return 0u;
-    const unsigned int nitems = (items - it0 + step - 1u) / step;
-
-    unsigned int mrows = a.m;
-    if (a.m_dev != nullptr) {
-        const unsigned int total = rg_scalar(a.m_dev);
-        mrows = total > a.m0 ? total - a.m0 : 0u;
-    }
-    if (mrows > a.m) mrows = a.m;
-    if (mrows > (unsigned int)MT) mrows = MT;
-
-    const unsigned int xs = a.qps * 128u + 8u;     /* LDS x row stride (halves) */
-    unsigned short *xl = (unsigned short *)lds;
-    float *part = (float *)(lds + rg_chain_xbytes(a));   /* [NW][RT*16][MT] then out */
-    __shared__ float xscale[MT];
-    const bool norm = a.xmode == AOTX_X_NORM;
-
-    /* ---- the load stream: item lk, chunk lc ---- */
-    unsigned int lk = 0u, lc = 0u, lchunks = 0u, lq0 = 0u, llast = 0u;
-    const unsigned char *lqb[RT];
-    const unsigned short *lsb[RT];
-#define RGC_RANGE(K, WQ0, WQ1, Q0)                                                       \
-    do {                                                                                 \
-        const unsigned int it_ = it0 + (K) * step;                                       \
-        const unsigned int sp_ = it_ % a.splits;                                         \
-        (Q0) = sp_ * a.qps;                                                              \
-        const unsigned int q1_ = (Q0) + a.qps < a.qn ? (Q0) + a.qps : a.qn;              \
-        const unsigned int per_ = (q1_ - (Q0) + NW - 1u) / NW;                           \
-        (WQ0) = (Q0) + wave * per_ < q1_ ? (Q0) + wave * per_ : q1_;                     \
-        (WQ1) = (WQ0) + per_ < q1_ ? (WQ0) + per_ : q1_;                                 \
-    } while (0)
-    /* move the stream to the first item at or after lk in which this wave has quads */
-#define RGC_SEEK()                                                                       \
-    do {                                                                                 \
-        for (; lk < nitems; ++lk) {                                                      \
-            unsigned int w0_, w1_, q0_;                                                  \
-            RGC_RANGE(lk, w0_, w1_, q0_);                                                \
-            lchunks = ((w1_ - w0_ + PD - 1u) / PD + 1u) & ~1u;   /* even: see below */   \
-            if (lchunks == 0u) continue;                                                 \
-            lq0 = w0_;                                                                   \
-            llast = w1_ - 1u;                                                            \
-            const unsigned int grp_ = (it0 + lk * step) / a.splits;                      \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
-                unsigned int dummy_ = 0u;                                                \
-                lqb[j] = rg_tile(a, grp_, (unsigned int)j, RT, 0u, dummy_) + lane * 16u; \
-                lsb[j] = rg_scales(a, grp_, (unsigned int)j, RT, 0u) + lane;             \
-            }                                                                            \
-            break;                                                                       \
-        }                                                                                \
-    } while (0)
-
-    rg_u4 wa[2][PD][RT][2];
-    unsigned int ws[2][PD][RT];
-    /* Every call issues the same loads: past the end of the stream it repeats the last
-     * chunk (a cache hit, never computed). A load issued on one path only would make the
-     * compiler wait for all outstanding loads (vmcnt(0)) where the paths join, so each
-     * chunk would wait for the one issued after it. */
-#define RGC_LOAD(BUF)                                                                    \
-    do {                                                                                 \
-        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            unsigned int qq = lq0 + lc * PD + (unsigned int)qi;                          \
-            if (qq > llast) qq = llast;                                                  \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
-                const rg_u4 *src = (const rg_u4 *)(lqb[j] + (unsigned long long)qq * 2048ull); \
-                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
-                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
-                ws[BUF][qi][j] = lsb[j][(unsigned long long)qq * 64ull];                 \
-            }                                                                            \
-        }                                                                                \
-        if (lk < nitems && ++lc >= lchunks) {                                            \
-            lc = 0u;                                                                     \
-            ++lk;                                                                        \
-            RGC_SEEK();                                                                  \
-            if (lk >= nitems) lc = 0u;   /* repeat a chunk already read */               \
-        }                                                                                \
-    } while (0)
-
-    /* the stream starts on the first item (also for a wave with no quads in any item, so
-     * that its repeated loads read valid weights) */
-    {
-        unsigned int w0_, w1_, q0_;
-        RGC_RANGE(0u, w0_, w1_, q0_);
-        lq0 = q0_;
-        llast = q0_;
-        lchunks = 1u;
-        const unsigned int grp_ = it0 / a.splits;
-#pragma unroll
-        for (int j = 0; j < RT; ++j) {
-            unsigned int dummy_ = 0u;
-            lqb[j] = rg_tile(a, grp_, (unsigned int)j, RT, 0u, dummy_) + lane * 16u;
-            lsb[j] = rg_scales(a, grp_, (unsigned int)j, RT, 0u) + lane;
-        }
-    }
-    RGC_SEEK();
-    if (lk >= nitems) lc = 0u;
-    RGC_LOAD(0);
-    RGC_LOAD(1);
-    wait();
-
-    unsigned int staged = 0xffffffffu;   /* the split whose x rows are in LDS */
-    for (unsigned int k = 0; k < nitems; ++k) {
-        const unsigned int it = it0 + k * step;
-        const unsigned int group = it / a.splits, split = it % a.splits;
-        unsigned int wq0, wq1, q0;
-        RGC_RANGE(k, wq0, wq1, q0);
-        const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
-
-        /* ---- stage the batch rows of x for [q0, q1) when the k range changes ---- */
-        if (split != staged) {
-            /* one round trip: the first pieces of x (or of the residual rows and norm
-             * weights) and the rows' partial sums of squares are all loaded before any is
-             * used */
-            staged = split;
-            const unsigned int pieces = (q1 - q0) * 16u;
-            const unsigned int total = mrows * pieces;
-            const unsigned int nss = (a.k + 15u) / 16u;
-            rg_u4 pr[2][4];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const unsigned int idx = tid + (unsigned int)i * NT;
-                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-                const unsigned int kk = q0 * 128u + p * 8u;
-                pr[i][0] = pr[i][1] = pr[i][2] = pr[i][3] = (rg_u4){0u, 0u, 0u, 0u};
-                if (idx < total && kk + 8u <= a.k) {
-                    if (norm) {
-                        const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
-                        pr[i][0] = co_load4<true>(rrow);
-                        pr[i][1] = co_load4<true>(rrow + 4);
-                        pr[i][2] = *(const rg_u4 *)(a.norm_w + kk);
-                        pr[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
-                    } else {
-                        pr[i][0] = co_load4<true>(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
-                    }
-                }
-            }
-            if (norm) {
-                const unsigned int mm = tid >> 4, l = tid & 15u;
-                float ssp[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const unsigned int at = l + 16u * (unsigned int)i;
-                    ssp[i] = mm < mrows && at < nss
-                           ? co_loadf<true>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
-                }
-                float sum = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sum += ssp[i];
-                if (mm < mrows)
-                    for (unsigned int i = l + 256u; i < nss; i += 16u)
-                        sum += co_loadf<true>(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + i);
-                sum += __shfl_xor(sum, 1, 64);
-                sum += __shfl_xor(sum, 2, 64);
-                sum += __shfl_xor(sum, 4, 64);
-                sum += __shfl_xor(sum, 8, 64);
-                if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
-                rg_sync_lds();
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const unsigned int idx = tid + (unsigned int)i * NT;
-                if (idx < total) {
-                    const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-                    const unsigned int kk = q0 * 128u + p * 8u;
-                    rg_u4 v;
-                    if (kk + 8u <= a.k)
-                        v = norm ? rg_norm_piece(pr[i][0], pr[i][1], pr[i][2], pr[i][3], xscale[mm])
-                                 : pr[i][0];
-                    else
-                        v = rg_x_piece<true>(a, a.m0 + mm, kk, norm ? xscale[mm] : 0.0f);
-                    *(rg_u4 *)(xl + mm * xs + p * 8u) = v;
-                }
-            }
-            for (unsigned int idx = tid + 2u * NT; idx < total; idx += NT) {
-                const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-                *(rg_u4 *)(xl + mm * xs + p * 8u) =
-                    rg_x_piece<true>(a, a.m0 + mm, q0 * 128u + p * 8u, norm ? xscale[mm] : 0.0f);
-            }
-            rg_sync_lds();
-        }
-
-        rg_f4 acc[RT][MT / 16];
-#pragma unroll
-        for (int j = 0; j < RT; ++j)
-#pragma unroll
-            for (int t = 0; t < MT / 16; ++t) acc[j][t] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
-        const unsigned int qlast = wq0 < wq1 ? wq1 - 1u : q0;
-        /* an even number of chunks per item (an odd count takes one chunk of zero scales),
-         * so every item starts on buffer 0: with the buffer order fixed in the code the
-         * compiler's wait before each chunk covers that chunk's loads only */
-        const unsigned int chunks = ((wq1 - wq0 + PD - 1u) / PD + 1u) & ~1u;
-#define RGC_COMPUTE(BUF, QS)                                                             \
-    do {                                                                                 \
-        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                              \
-            const unsigned int qq = (QS) + (unsigned int)qi;                             \
-            const unsigned int qx = qq > qlast ? qlast : qq;                             \
-            const unsigned short *xq = xl + (qx - q0) * 128u + 32u * g;                  \
-            rg_h8 B[MT / 16][4];                                                         \
-            _Pragma("unroll") for (int t = 0; t < MT / 16; ++t) {                        \
-                const unsigned int mm = (unsigned int)t * 16u + r;                       \
-                const unsigned int mr = mm < mrows ? mm : 0u;                            \
-                _Pragma("unroll") for (int s = 0; s < 4; ++s)                            \
-                    B[t][s] = *(const rg_h8 *)(xq + mr * xs + 8u * s);                   \
-            }                                                                            \
-            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                             \
-                const unsigned int sbits = qq < wq1 ? ws[BUF][qi][j] : 0u;               \
-                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));             \
-                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];            \
-                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                    \
-                                      q1v[0], q1v[1], q1v[2], q1v[3]};                   \
-                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
-                    unsigned int d0, d1, d2, d3;                                         \
-                    rg_dequant4(qd[2 * s], s2, d0, d1);                                  \
-                    rg_dequant4(qd[2 * s + 1], s2, d2, d3);                              \
-                    rg_u4 av = {d0, d1, d2, d3};                                         \
-                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                             \
-                    _Pragma("unroll") for (int t = 0; t < MT / 16; ++t)                  \
-                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(               \
-                            A, B[t][s], acc[j][t], 0, 0, 0);                             \
-                }                                                                        \
-            }                                                                            \
-        }                                                                                \
-    } while (0)
-        /* each buffer is refilled from the stream right after it is used */
-        for (unsigned int c = 0; c < chunks; c += 2u) {
-            RGC_COMPUTE(0, wq0 + c * PD);
-            RGC_LOAD(0);
-            RGC_COMPUTE(1, wq0 + (c + 1u) * PD);
-            RGC_LOAD(1);
-        }
-#undef RGC_COMPUTE
-
-        /* ---- add the NW waves' accumulators in wave order ---- */
-        const unsigned int gr = RT * 16u;
-#pragma unroll
-        for (int j = 0; j < RT; ++j)
-#pragma unroll
-            for (int t = 0; t < MT / 16; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    unsigned int row = (unsigned int)j * 16u + 4u * g + (unsigned int)i;
-                    part[(wave * gr + row) * MT + (unsigned int)t * 16u + r] = acc[j][t][i];
-                }
-        rg_sync_lds();
-        float *out = part + NW * gr * MT;
-        for (unsigned int idx = tid; idx < gr * MT; idx += NT) {
-            float sum = part[idx];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * gr * MT + idx];
-            out[idx] = sum;
-        }
-        rg_sync_lds();
-        bool mine = true;
-        if (a.splits > 1u) {
-            __shared__ unsigned int last;
-            mine = rg_split_merge<NT>(a, out, gr * MT, 0u, group, split, &last);
-        }
-        if (mine) rg_epilogue<MT, NT, true>(a, out, group, RT, mrows, nullptr, nullptr);
-        __syncthreads();          /* out and part are rewritten by the next item */
-    }
-#undef RGC_RANGE
-#undef RGC_SEEK
-#undef RGC_LOAD
-    return nitems;
-}
 
 #endif

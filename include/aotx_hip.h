@@ -255,9 +255,6 @@ void aotx_model_restream(void);
 unsigned int aotx_model_faulted(void);
 /* Kernel nodes of the largest captured step graph of a role (model_host.cu:243-250). */
 unsigned int aotx_model_nodes(unsigned int role);
-/* 1 when a pass of `tokens` rows runs every layer as one chained launch (no counterpart
- * in the reference, whose layers are separate kernels; for tests and measurement). */
-unsigned int aotx_model_chained(unsigned int role, unsigned int tokens);
 /* Ask the page cache for the pages of the next pass (model_host.cu:202-220). offset and
  * agent are device pointers. The caller answers with aotx_kv_serve before launching. */
 int aotx_model_pages(unsigned int role, const unsigned int *offset, unsigned int seqs,

@@ -285,39 +285,6 @@ def test_8b_width_experts_wide_batch_vs_oracle(torch, orc):
         rt.close()
 
 
-def test_8b_width_layer_chain_vs_oracle(torch, orc, monkeypatch):
-    """With AOTX_CHAIN=1 at open, an 8B-width model (2 layers: d_model 4096, FFN 14336,
-    32/8 heads x 128) at 16 tokens or fewer runs all layers as one chained launch (stages
-    waiting on arrival counts):
-    a 12-token prompt (bucket 16, 12 live rows), three single-token decode steps (bucket 1),
-    and a 5-slot step (bucket 8), logits vs the oracle each time."""
-    shape = Shape(layers=2, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
-                  vocab=1024)
-    region_dev, region, lay = _device_model(torch, shape, 9)
-    monkeypatch.setenv("AOTX_CHAIN", "1")
-    rt = Runtime(region_dev, lay.desc, max_tokens=32, pool_pages=64)
-    try:
-        assert rt.L.aotx_model_chained(rt.role, 1) == 1 and rt.L.aotx_model_chained(rt.role, 16) == 1
-        ref = orc.Model(lay.desc, region, slots=8, max_context=64, threads=8)
-        rng = np.random.default_rng(9)
-        ids = rng.integers(0, shape.vocab, 12).tolist()
-        tok, _, lg = rt.step(ids, [0, 12], [2])
-        want = ref.step(ids, [0, 12], [2])
-        assert rel_rms(lg, want) < 1e-2
-        for _ in range(3):
-            ids = [int(tok[0])]
-            tok, _, lg = rt.step(ids, [0, 1], [2])
-            want = ref.step(ids, [0, 1], [2])
-            assert rel_rms(lg, want) < 1e-2
-        ids = rng.integers(0, shape.vocab, 5).tolist()
-        _, _, lg = rt.step(ids, list(range(6)), [0, 1, 2, 3, 4])
-        want = ref.step(ids, list(range(6)), [0, 1, 2, 3, 4])
-        assert rel_rms(lg, want) < 1e-2
-        assert rt.faulted() == 0
-    finally:
-        rt.close()
-
-
 def test_gguf_file_through_place_and_step(torch, orc, tiny, tmp_path):
     """The tiny model written as a GGUF file, read back by the library's reader, placed into
     a new weights region (aotx_model_place) and run: the same logits, bit for bit, as the
