@@ -127,7 +127,7 @@ class PlanState(ctypes.Structure):
         ("first", u32 * AOTX_SLOTS), ("place", u32 * AOTX_SLOTS), ("asked", u32 * AOTX_SLOTS),
         ("kept", u32 * AOTX_SLOTS), ("cursor", u32 * AOTX_MODEL_ROLES), ("seqs", u32),
         ("tokens", u32), ("waited", u32), ("short_of", u32), ("steps", u64), ("records", u32),
-        ("reserved", u32),
+        ("dropped", u32), ("refused", u32), ("reserved", u32),
     ]
 
 
@@ -209,6 +209,8 @@ PROTOTYPES = {
     "aotx_decode_plan": (i32, [u32, vp, vp, u32, u32, u32, vp, vp]),
     "aotx_model_kv_pages": (u32, [u32, u32]),
     "aotx_decode_commit": (i32, [u32, vp, vp, u32, vp, vp, vp, vp, u32, vp]),
+    "aotx_decode_tick": (i32, [u32, vp, vp, u32, u32, u32, vp, vp, u32, vp]),
+    "aotx_seq_apply": (i32, [u32, vp, vp, u32, vp, vp, u32, vp]),
     # the tokenizer (include/aotx_text.h)
     "aotx_text_family_find": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(u32)]),
     "aotx_text_vocab_build": (i32, [ctypes.POINTER(TextSource), ctypes.POINTER(TextStore)]),

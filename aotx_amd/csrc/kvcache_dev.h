@@ -24,6 +24,7 @@ static __device__ __forceinline__ int aotx_kv_put(aotx_kv_table *kv, unsigned in
     }
     kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].agent = agent;
     kv->queue[at & (AOTX_KV_QUEUE_MAX - 1u)].pages = pages;
+    __threadfence();                 /* the entry is visible before later work that reads it */
     return 1;
 }
 

@@ -29,6 +29,7 @@
 #include "norm.h"
 #include "rgemv.h"
 #include "sample.h"
+#include "tick.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -37,6 +38,19 @@ unsigned long long aotx_mem_weights_bytes(void);
 
 #define AOTX_BUCKETS 10u   /* 1, 2, 4, ..., 512 */
 #define AOTX_GEMV_COUNTS 65536u   /* split arrival counters: experts x product groups */
+
+/* The operands of a decode tick; a tick graph is captured for one set of them. */
+struct aotx_tick_setup {
+    const aotx_plan_slot *slots;
+    int *tokens;
+    unsigned int stride;
+    unsigned int budget;
+    unsigned int pool_pages;
+    aotx_plan_state *plan;
+    aotx_token_record *records;
+    unsigned int capacity;
+    float *logits;
+};
 
 /* Repacked (Q8R) copies of one layer's matrices; the library owns them. */
 struct aotx_rlayer {
@@ -81,6 +95,14 @@ struct aotx_hold {
     unsigned int *elist, *ecount;
     void *piece[48];
     unsigned int pieces;
+    /* the decode tick (aotx_decode_tick): the step's outputs, the sampler's adjustment
+     * scratch, and one graph per token bucket with the operands it was captured for */
+    int *tick_token;
+    unsigned int *tick_draw;
+    unsigned int *pen_count, *pen_last;
+    float *pen_raw;
+    aotx_tick_setup tick_setup[AOTX_BUCKETS];
+    hipGraphExec_t tick_exec[AOTX_BUCKETS];
     /* graphs per row selection, token bucket and head-row bucket */
     hipGraphExec_t exec[2][AOTX_BUCKETS][AOTX_BUCKETS];
     unsigned int nodes;
@@ -284,7 +306,8 @@ static void aotx_roperands(aotx_rgemv_args *p, const aotx_rgemv_args &tmpl)
 
 /* ---- the step ---------------------------------------------------------------------- */
 
-static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br)
+static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br,
+                             const aotx_tick_setup *tk)
 {
     (void)sel_all;    /* the head's rows are selected on the device from the call block */
     const aotx_model_desc *d = &h->desc;
@@ -304,7 +327,17 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
      * outputs by the rows' RMSNorm scale, so no norm kernel runs between them */
     const bool scaled_x = !fused_norm && !experts;
 
-    AOTX_CHECK(hipMemcpyAsync(h->step, h->pinned, sizeof(aotx_step), hipMemcpyHostToDevice, s));
+    if (tk != nullptr) {
+        /* the tick: the plan packs the batch on the device and the call block points at it */
+        if (aotx_plan_launch(h->role, tk->slots, tk->tokens, tk->stride, tk->budget,
+                             tk->pool_pages, tk->plan, s) != 0) {
+            fprintf(stderr, "aotx: the tick plan was refused\n");
+            exit(1);
+        }
+        aotx_launch_tick_begin(h->step, tk->plan, h->tick_token, h->tick_draw, s);
+    } else {
+        AOTX_CHECK(hipMemcpyAsync(h->step, h->pinned, sizeof(aotx_step), hipMemcpyHostToDevice, s));
+    }
     aotx_launch_rows(h->step, T, h->pos, h->tagent, h->last, s);
     aotx_launch_gather(h->step, T, aotx_tensor(d->token_embd), d->embd_type, d->hidden, d->vocab,
                        h->resid, h->sumsq, s);
@@ -526,9 +559,37 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
         unsigned int hrows[1] = {d->vocab};
         aotx_rproduct(h, hw, hrows, 1u, d->hidden, AOTX_EPI_F32, R, m_rows, t);
     }
+    aotx_pen_args pen;
+    if (tk != nullptr) {
+        /* the sample's penalties over each sequence's list, around the pick */
+        pen.step = h->step;
+        pen.slots = tk->slots;
+        pen.tokens = tk->tokens;
+        pen.stride = tk->stride;
+        pen.logits = h->logits;
+        pen.ld = d->vocab;
+        pen.vocab = d->vocab;
+        pen.count = h->pen_count;
+        pen.last = h->pen_last;
+        pen.raw = h->pen_raw;
+        aotx_launch_pen(pen, R, 0, s);
+    }
     aotx_launch_pick(h->logits, d->vocab, d->vocab, m_rows, R, nullptr, nullptr, 0u, 1.0f, 0.0f,
                      0ull, nullptr, nullptr, &h->step->run, h->pick_best, s);
+    if (tk != nullptr) {
+        aotx_launch_pen(pen, R, 1, s);
+        if (tk->logits != nullptr)
+            AOTX_CHECK(hipMemcpyAsync(tk->logits, h->logits, (size_t)R * d->vocab * sizeof(float),
+                                      hipMemcpyDeviceToDevice, s));
+    }
     aotx_launch_shut_rows(h->step, s);
+    if (tk != nullptr
+        && aotx_commit_launch(h->role, (aotx_plan_slot *)tk->slots, tk->tokens, tk->stride,
+                              h->tick_token, h->tick_draw, tk->plan, tk->records, tk->capacity,
+                              s) != 0) {
+        fprintf(stderr, "aotx: the tick commit was refused\n");
+        exit(1);
+    }
 }
 
 /* ---- lifecycle ----------------------------------------------------------------------- */
@@ -685,6 +746,8 @@ extern "C" void aotx_model_shut(unsigned int role)
         for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
             for (unsigned int j = 0; j < AOTX_BUCKETS; ++j)
                 if (h->exec[a][i][j] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->exec[a][i][j]));
+    for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
+        if (h->tick_exec[i] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->tick_exec[i]));
     AOTX_CHECK(hipStreamDestroy(h->stream));
     AOTX_CHECK(hipHostFree(h->pinned));
     for (unsigned int i = 0; i < h->pieces; ++i) AOTX_CHECK(hipFree(h->piece[i]));
@@ -769,7 +832,7 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
         if (exec == nullptr) {
             hipGraph_t graph = nullptr;
             AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
-            aotx_record_step(h, all, bt, br);
+            aotx_record_step(h, all, bt, br, nullptr);
             AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
             size_t count = 0;
             AOTX_CHECK(hipGraphGetNodes(graph, nullptr, &count));
@@ -779,13 +842,71 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
         }
         AOTX_CHECK(hipGraphLaunch(exec, h->stream));
     } else {
-        aotx_record_step(h, all, bt, br);
+        aotx_record_step(h, all, bt, br, nullptr);
     }
     if (set->logits != nullptr) {
         AOTX_CHECK(hipMemcpyAsync(set->logits, h->logits,
                                   (size_t)set->rows * h->desc.vocab * sizeof(float),
                                   hipMemcpyDeviceToDevice, h->stream));
     }
+    AOTX_CHECK(hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+/* One decode tick as one graph (cuda/model/decode_host.cu:136-157): plan -> the step over
+ * the plan's batch, each row sampled with its sequence's own sample and penalties -> commit.
+ * The graph of a token bucket (the bucket of `budget`) is captured on first use and again
+ * when the operands change. */
+extern "C" int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *tokens,
+                                unsigned int stride, unsigned int budget, unsigned int pool_pages,
+                                aotx_plan_state *plan, aotx_token_record *records,
+                                unsigned int capacity, float *logits)
+{
+    if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || plan == nullptr
+        || stride == 0u || (records == nullptr && capacity != 0u))
+        return 1;
+    aotx_hold *h = &aotx_holds[role];
+    if (!h->ready) return 1;
+    if (budget > AOTX_SEQ_TICK_BUDGET) budget = AOTX_SEQ_TICK_BUDGET;
+    if (budget == 0u || budget > h->max_tokens) return 1;
+    const aotx_model_desc *d = &h->desc;
+    if (h->tick_token == nullptr) {
+        h->tick_token = (int *)aotx_take(h, AOTX_SLOTS * sizeof(int));
+        h->tick_draw = (unsigned int *)aotx_take(h, AOTX_SLOTS * sizeof(unsigned int));
+        const size_t cells = (size_t)AOTX_SLOTS * d->vocab;
+        h->pen_count = (unsigned int *)aotx_take(h, cells * sizeof(unsigned int));
+        h->pen_last = (unsigned int *)aotx_take(h, cells * sizeof(unsigned int));
+        h->pen_raw = (float *)aotx_take(h, cells * sizeof(float));
+    }
+    const unsigned int bt = aotx_bucket_of(budget);
+    const unsigned int T = 1u << bt;
+    const unsigned int br = aotx_bucket_of(T < AOTX_SLOTS ? T : AOTX_SLOTS);
+    aotx_tick_setup tk;
+    memset(&tk, 0, sizeof tk);
+    tk.slots = slots;
+    tk.tokens = tokens;
+    tk.stride = stride;
+    tk.budget = budget;
+    tk.pool_pages = pool_pages;
+    tk.plan = plan;
+    tk.records = records;
+    tk.capacity = capacity;
+    tk.logits = logits;
+    hipGraphExec_t &exec = h->tick_exec[bt];
+    if (exec != nullptr && memcmp(&h->tick_setup[bt], &tk, sizeof tk) != 0) {
+        AOTX_CHECK(hipGraphExecDestroy(exec));
+        exec = nullptr;
+    }
+    if (exec == nullptr) {
+        hipGraph_t graph = nullptr;
+        AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        aotx_record_step(h, 0u, bt, br, &tk);
+        AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
+        AOTX_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        AOTX_CHECK(hipGraphDestroy(graph));
+        h->tick_setup[bt] = tk;
+    }
+    AOTX_CHECK(hipGraphLaunch(exec, h->stream));
     AOTX_CHECK(hipStreamSynchronize(h->stream));
     return 0;
 }

@@ -8,6 +8,7 @@
 #include "aotx_internal.h"
 #include "kvcache_dev.h"
 #include "../../include/aotx_plan.h"
+#include "tick.h"
 
 static_assert(AOTX_SLOTS == 64u, "one lane per slot in one wave");
 
@@ -59,7 +60,10 @@ __global__ __launch_bounds__(64) void aotx_plan_kernel(unsigned int role, const 
 
     /* tokens of the list no page holds yet, if the slot's pages are there */
     unsigned int want = 0u;
-    if (seq.role == role && (state == AOTX_SEQ_STATE_PREFILL || state == AOTX_SEQ_STATE_DECODE)) {
+    if (seq.role == role && (state == AOTX_SEQ_STATE_PREFILL || state == AOTX_SEQ_STATE_DECODE)
+        && seq.prompt > stride) {
+        atomicAdd(&p->refused, 1u);              /* the list cannot hold the prompt */
+    } else if (seq.role == role && (state == AOTX_SEQ_STATE_PREFILL || state == AOTX_SEQ_STATE_DECODE)) {
         const unsigned int list = seq.prompt + seq.sampled;
         unsigned int pending = list > held ? list - held : 0u;
         if (pending > budget) pending = budget;
@@ -137,9 +141,9 @@ __global__ __launch_bounds__(64) void aotx_plan_kernel(unsigned int role, const 
     }
 }
 
-extern "C" int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, const int *tokens,
-                                unsigned int stride, unsigned int budget, unsigned int pool_pages,
-                                aotx_plan_state *plan, void *stream)
+int aotx_plan_launch(unsigned int role, const aotx_plan_slot *slots, const int *tokens,
+                     unsigned int stride, unsigned int budget, unsigned int pool_pages,
+                     aotx_plan_state *plan, hipStream_t s)
 {
     if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || plan == nullptr
         || stride == 0u)
@@ -147,10 +151,18 @@ extern "C" int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, 
     aotx_kvl_shape shape;
     if (aotx_role_kv_shape(role, &shape) != 0) return 1;
     if (budget > AOTX_SEQ_TICK_BUDGET) budget = AOTX_SEQ_TICK_BUDGET;
-    hipLaunchKernelGGL(aotx_plan_kernel, dim3(1), dim3(64), 0, aotx_stream(stream), role, slots,
-                       tokens, stride, budget, pool_pages, shape, aotx_state_device(), plan);
+    hipLaunchKernelGGL(aotx_plan_kernel, dim3(1), dim3(64), 0, s, role, slots, tokens, stride,
+                       budget, pool_pages, shape, aotx_state_device(), plan);
     AOTX_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int aotx_decode_plan(unsigned int role, const aotx_plan_slot *slots, const int *tokens,
+                                unsigned int stride, unsigned int budget, unsigned int pool_pages,
+                                aotx_plan_state *plan, void *stream)
+{
+    return aotx_plan_launch(role, slots, tokens, stride, budget, pool_pages, plan,
+                            aotx_stream(stream));
 }
 
 /* ---- commit (cuda/model/commit.cu:102-201) ------------------------------------------------ */
@@ -192,7 +204,7 @@ __global__ __launch_bounds__(64) void aotx_commit_kernel(unsigned int role, aotx
                 seq.last = tok;
                 seq.draw = drawn;
                 if (tok == seq.stop || seq.sampled >= seq.limit || (seq.flags & AOTX_DECODE_MARK_STOP) != 0u
-                    || list + 1u >= AOTX_SEQ_MAX_TOKENS_PLAN) {
+                    || list + 1u >= AOTX_SEQ_MAX_TOKENS_PLAN || list + 1u >= stride) {
                     mark |= AOTX_TOKEN_LAST;
                     seq.flags |= AOTX_TOKEN_LAST;
                     seq.state = AOTX_SEQ_STATE_DONE;
@@ -241,7 +253,23 @@ __global__ __launch_bounds__(64) void aotx_commit_kernel(unsigned int role, aotx
         rec[first + journal] = x;
     }
     const unsigned int total = __shfl(scan, 63, 64);
-    if (slot == 0u) p->records = total < cap ? total : cap;
+    if (slot == 0u) {
+        p->records = total < cap ? total : cap;
+        p->dropped = total > cap ? total - cap : 0u;
+    }
+}
+
+int aotx_commit_launch(unsigned int role, aotx_plan_slot *slots, int *tokens, unsigned int stride,
+                       const int *token, const unsigned int *draw, aotx_plan_state *plan,
+                       aotx_token_record *records, unsigned int capacity, hipStream_t s)
+{
+    if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || token == nullptr
+        || draw == nullptr || plan == nullptr || stride == 0u || (records == nullptr && capacity != 0u))
+        return 1;
+    hipLaunchKernelGGL(aotx_commit_kernel, dim3(1), dim3(64), 0, s, role, slots, tokens, stride,
+                       token, draw, aotx_state_device(), plan, records, capacity);
+    AOTX_LAUNCH_CHECK();
+    return 0;
 }
 
 extern "C" int aotx_decode_commit(unsigned int role, aotx_plan_slot *slots, int *tokens,
@@ -249,11 +277,6 @@ extern "C" int aotx_decode_commit(unsigned int role, aotx_plan_slot *slots, int 
                                   aotx_plan_state *plan, aotx_token_record *records,
                                   unsigned int capacity, void *stream)
 {
-    if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || token == nullptr
-        || draw == nullptr || plan == nullptr || stride == 0u || (records == nullptr && capacity != 0u))
-        return 1;
-    hipLaunchKernelGGL(aotx_commit_kernel, dim3(1), dim3(64), 0, aotx_stream(stream), role, slots,
-                       tokens, stride, token, draw, aotx_state_device(), plan, records, capacity);
-    AOTX_LAUNCH_CHECK();
-    return 0;
+    return aotx_commit_launch(role, slots, tokens, stride, token, draw, plan, records, capacity,
+                              aotx_stream(stream));
 }

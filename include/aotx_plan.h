@@ -82,7 +82,12 @@ typedef struct aotx_plan_state {
     unsigned int waited;                    /* prefill pieces that got no room, summed */
     unsigned int short_of;                  /* slots that waited for pages, summed */
     unsigned long long steps;               /* ticks that gave a batch of one row or more */
-    unsigned int records;                   /* token records of the last commit */
+    unsigned int records;                   /* token records of the last commit (at most the
+                                               capacity given to it) */
+    unsigned int dropped;                   /* records of the last commit past the capacity */
+    unsigned int refused;                   /* slots and records refused, summed: a prompt
+                                               longer than the list stride, a record that
+                                               does not continue its slot */
     unsigned int reserved;
 } aotx_plan_state;
 
@@ -114,6 +119,36 @@ int aotx_decode_commit(unsigned int role, aotx_plan_slot *slots, int *tokens,
                        unsigned int stride, const int *token, const unsigned int *draw,
                        aotx_plan_state *plan, aotx_token_record *records,
                        unsigned int capacity, void *stream);
+
+/* One decode tick of `role` as one captured HIP graph (the tick graph of
+ * cuda/model/decode_host.cu:136-157): aotx_decode_plan, then the model step over the plan's
+ * batch in device memory (no host copy of the batch), each sequence sampled with its own
+ * sample (plan->how: temperature, top-k, top-p, min-p, seed) and with the presence,
+ * frequency and repeat penalties of that sample over the slot's list (the pick's value
+ * function, cuda/model/sample.cu:277-319), then aotx_decode_commit. The arguments are those
+ * of the plan and the commit; budget is at most the role's open token capacity. logits
+ * (device, may be null) receives the model logits of each sequence's last row,
+ * [64][vocab] room. The graph of budget's token bucket is captured on first use and again
+ * when an operand changes. Synchronous. The caller serves the pool's page requests
+ * (aotx_kv_serve) between ticks. Returns 1 for a bad argument or a role not open. Not
+ * built: the reply-wrap thinking mask of the value function (the descriptor carries no
+ * wrap tokens). */
+int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *tokens, unsigned int stride,
+                     unsigned int budget, unsigned int pool_pages, aotx_plan_state *plan,
+                     aotx_token_record *records, unsigned int capacity, float *logits);
+
+/* Restore slots of `role` from token records, in order (the reference's aotx_seq_apply,
+ * cuda/model/decode.cu:230-305): a record at position 0 opens its slot (a slot that held a
+ * sequence gives its pages back first) keeping the slot's limit, stop and sample and taking
+ * the record's seed; prompt records rebuild the prompt, sampled records append their token
+ * and set the slot's draw counter to the record's draw + 1, so the next sample continues
+ * the same Philox stream; a LAST record ends the slot. The slot's pages are empty after an
+ * open, so the following ticks prefill the whole list again. A record that does not
+ * continue its slot is refused and counted in plan->refused. Device pointers; one thread,
+ * asynchronous on the stream. Returns 1 for a bad argument. */
+int aotx_seq_apply(unsigned int role, aotx_plan_slot *slots, int *tokens, unsigned int stride,
+                   aotx_plan_state *plan, const aotx_token_record *records, unsigned int count,
+                   void *stream);
 
 /* Pages a slot of `role` needs for a context of `context` positions (the reference's
  * aotx_kvl_pages over the role's KV shape, cuda/model/kv_layout.cuh); 0 when the role has

@@ -321,6 +321,36 @@ int orc_pick(const float *row, unsigned int vocab, unsigned int top_k, float top
 }
 
 /* ------------------------------------------------------------------------------------
+ * The pick's adjusted logit (cuda/model/sample.cu:277-319) with the penalties of a
+ * sample over a sequence's token list: presence and frequency penalties on every token the
+ * list holds, then the repeat penalty on a token inside the last `repeat_window` tokens.
+ * The reference's compiler contracts presence + frequency * count into one fused
+ * multiply-add, written here as fmaf. The row is adjusted in place.
+ * ---------------------------------------------------------------------------------- */
+void orc_pick_adjust(float *row, unsigned int vocab, const int *list, unsigned int n,
+                     float presence, float frequency, float repeat_penalty,
+                     unsigned int repeat_window)
+{
+    const int pf = presence != 0.0f || frequency != 0.0f;
+    const int rp = repeat_window != 0u && repeat_penalty != 1.0f;
+    if (!pf && !rp) return;
+    unsigned int first = n > repeat_window ? n - repeat_window : 0u;
+    for (unsigned int t = 0; t < vocab; ++t) {
+        float value = row[t];
+        unsigned int count = 0u, inside = 0u;
+        for (unsigned int i = 0; i < n; ++i) {
+            if ((unsigned int)list[i] == t) {
+                count += 1u;
+                if (i >= first) inside = 1u;
+            }
+        }
+        if (pf && count != 0u) value -= fmaf(frequency, (float)count, presence);
+        if (rp && inside) value = value > 0.0f ? value / repeat_penalty : value * repeat_penalty;
+        row[t] = value;
+    }
+}
+
+/* ------------------------------------------------------------------------------------
  * Router (cuda/model/experts.cu:10-75), in double as tests/expert_test.cu:118-152 checks.
  * ---------------------------------------------------------------------------------- */
 void orc_route(const float *router, const uint16_t *x, unsigned int tokens,

@@ -92,6 +92,9 @@ int orc_model_seat(orc_model *m, unsigned int slot, unsigned int position, uint6
 /* The xnorm (half values as float) of the last row of each sequence of the last step. */
 const float *orc_model_last_xnorm(const orc_model *m);
 const uint16_t *orc_model_cache(const orc_model *m, unsigned int which);
+void orc_pick_adjust(float *row, unsigned int vocab, const int *list, unsigned int n,
+                     float presence, float frequency, float repeat_penalty,
+                     unsigned int repeat_window);
 
 #ifdef __cplusplus
 }

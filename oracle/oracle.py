@@ -39,6 +39,7 @@ def lib():
         L.orc_rng_unit.argtypes = [u64, u32, u32, u64]
         L.orc_pick.restype = i32
         L.orc_pick.argtypes = [vp, u32, u32, f32, f32, f32, u64, u32, u64, vp, vp, vp]
+        L.orc_pick_adjust.argtypes = [vp, u32, vp, u32, f32, f32, f32, u32]
         L.orc_route.argtypes = [vp, vp, u32, u32, u32, u32, vp, vp]
         L.orc_attend_one.argtypes = [vp, vp, vp, u32, u32, u32, vp]
         L.orc_model_new.restype = vp
@@ -93,6 +94,15 @@ def pick(row, top_k=0, top_p=1.0, min_p=0.0, temperature=0.0, seed=0, agent=0, p
     tok = lib().orc_pick(_p(row), row.size, top_k, top_p, min_p, temperature, seed, agent,
                          position, ctypes.byref(count), ctypes.byref(taken), _p(allowed))
     return tok, count.value, allowed[:taken.value].copy()
+
+
+def pick_adjust(row, tokens, presence=0.0, frequency=0.0, repeat_penalty=1.0, repeat_window=0):
+    """The row with the sample's penalties over a token list applied (sample.cu:277-319)."""
+    out = np.array(row, dtype=np.float32, copy=True)
+    lst = np.ascontiguousarray(tokens, dtype=np.int32)
+    lib().orc_pick_adjust(_p(out), out.size, _p(lst), lst.size, presence, frequency,
+                          repeat_penalty, repeat_window)
+    return out
 
 
 def route(router, x16, experts, used):

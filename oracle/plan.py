@@ -38,6 +38,7 @@ class Plan:
         self.kept = [0] * SLOTS
         self.waited = 0
         self.short_of = 0
+        self.refused = 0
         self.steps = 0
 
     def pages(self, kv, slot, need, page_limit, pool_pages, made0):
@@ -60,10 +61,11 @@ class Plan:
             self.asked[slot] = need
         return False
 
-    def tick(self, role, slots, tokens, seen, budget, kv, pages_of, pool_pages):
+    def tick(self, role, slots, tokens, seen, budget, kv, pages_of, pool_pages, stride=8192):
         """One tick. slots: list of dicts (state, role, prompt, sampled, limit, page_limit,
         seed); tokens[slot] = the slot's list; seen[slot] = tokens its pages hold;
-        pages_of(context) = pages a slot needs. Returns the batch as a dict."""
+        pages_of(context) = pages a slot needs; stride = the list capacity (a slot whose
+        prompt exceeds it is refused). Returns the batch as a dict."""
         budget = min(budget, TICK_BUDGET)
         order = [(i + self.cursor[role]) % SLOTS for i in range(SLOTS)]
         want = {}
@@ -71,7 +73,9 @@ class Plan:
         for slot in order:
             s = slots[slot]
             w = 0
-            if s["role"] == role and s["state"] in (PREFILL, DECODE):
+            if s["role"] == role and s["state"] in (PREFILL, DECODE) and s["prompt"] > stride:
+                self.refused += 1
+            elif s["role"] == role and s["state"] in (PREFILL, DECODE):
                 lst = s["prompt"] + s["sampled"]
                 pending = min(max(lst - seen[slot], 0), budget)
                 if pending:
@@ -123,11 +127,12 @@ PROMPT, SAMPLED, LAST, MARK_STOP = 0x1, 0x2, 0x4, 0x100
 SEQ_MAX = 8192
 
 
-def commit(plan, role, slots, tokens, out, token, draw, kv):
+def commit(plan, role, slots, tokens, out, token, draw, kv, stride=8192):
     """cuda/model/commit.cu:102-201 without the journal ring, hash and reply wraps: move
     each slot of the role and return the tick's token records (slot, token, position,
     flags, seed, draw), slots in order. plan: the Plan (asked, kept); out: the tick's batch;
-    token/draw: the step's outputs by sequence place; kv: dict with count and releases."""
+    token/draw: the step's outputs by sequence place; kv: dict with count and releases;
+    stride: the list capacity (a sequence whose list fills it ends)."""
     records = []
     for slot in range(SLOTS):
         s = slots[slot]
@@ -159,7 +164,7 @@ def commit(plan, role, slots, tokens, out, token, draw, kv):
             s["sampled"] += 1
             s["last"], s["draw"] = tok, drawn
             if (tok == s["stop"] or s["sampled"] >= s["limit"] or s["flags"] & MARK_STOP
-                    or lst + 1 >= SEQ_MAX):
+                    or lst + 1 >= SEQ_MAX or lst + 1 >= stride):
                 mark |= LAST
                 s["flags"] |= LAST
                 s["state"] = DONE

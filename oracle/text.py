@@ -8,14 +8,75 @@ the leftmost of equal ranks; with the family's whole rule a pre-token that is a 
 stays whole, cuda/text/families.h:18-23), and the detokenizer of cuda/text/detok.cu
 (byte-level code points give their byte, control tokens give nothing).
 """
+import os
+import sys
+
 import regex
 
-PATTERNS = {
+PATTERNS_17 = {
     "qwen2": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
     "llama3": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}{1,3}| ?[^\s\p{L}\p{N}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
     "gpt2": r"'s|'t|'re|'ve|'m|'ll|'d| ?\p{L}+| ?\p{N}+| ?[^\s\p{L}\p{N}]+|\s+(?!\S)|\s+",
     "qwen35": r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}\p{M}]?[\p{L}\p{M}]+|\p{N}| ?[^\s\p{L}\p{N}\p{M}]+[\r\n]*|\s*[\r\n]+|\s+(?!\S)|\s+",
 }
+
+
+def _unicode15():
+    """The letter/number/mark class bodies at Unicode 15.0, the reference's table version
+    (cuda/text/unicode_tables.cu:7), from the generator of the device tables
+    (aotx_amd/csrc/gen_unicode.py: the `regex` module's 17.0 classes minus the code
+    points of 15.1-17.0); tests/test_unicode.py pins those tables."""
+    here = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "aotx_amd", "csrc")
+    sys.path.insert(0, here)
+    try:
+        import gen_unicode
+    finally:
+        sys.path.remove(here)
+    body = {}
+    for name, pred in gen_unicode.classes():
+        if name == "space":
+            continue
+        body[name] = "".join(f"\\U{a:08x}-\\U{b:08x}" for a, b in gen_unicode.ranges(pred))
+    return body
+
+
+def _at15(pattern, body):
+    """A pattern with \\p{L}, \\p{N}, \\p{M} replaced by the 15.0 class bodies (inside a
+    bracket expression the body alone, outside it a bracket expression of its own)."""
+    key = {"L": body["letter"], "N": body["number"], "M": body["mark"]}
+    out, i, depth = [], 0, 0
+    while i < len(pattern):
+        if pattern.startswith("\\p{", i) and pattern[i + 3] in key and pattern[i + 4] == "}":
+            b = key[pattern[i + 3]]
+            out.append(b if depth else "[" + b + "]")
+            i += 5
+            continue
+        ch = pattern[i]
+        if ch == "\\":
+            out.append(pattern[i:i + 2])
+            i += 2
+            continue
+        if ch == "[":
+            depth += 1
+        elif ch == "]" and depth:
+            depth -= 1
+        out.append(ch)
+        i += 1
+    return "".join(out)
+
+
+class _Patterns(dict):
+    """The family patterns at Unicode 15.0, built on first use."""
+
+    def __missing__(self, name):
+        if not hasattr(self, "_body"):
+            self._body = _unicode15()
+        self[name] = regex.compile(_at15(PATTERNS_17[name], self._body))
+        return self[name]
+
+
+PATTERNS = _Patterns()
+
 # pattern row and whole rule of each family (cuda/text/families.h:10-43)
 FAMILY = {"qwen2": ("qwen2", False), "llama3": ("llama3", True), "llama-bpe": ("llama3", True),
           "gpt-2": ("gpt2", False), "qwen35": ("qwen35", False)}
@@ -75,7 +136,7 @@ def clean(data):
 
 def pretokens(text, pattern):
     """Pre-tokens of a str (consecutive, covering it)."""
-    return [m.group(0) for m in regex.finditer(PATTERNS[pattern], text)]
+    return [m.group(0) for m in PATTERNS[pattern].finditer(text)]
 
 
 class Vocab:

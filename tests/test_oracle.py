@@ -259,3 +259,20 @@ def test_attend_one_vs_two_pass_softmax(orc):
     k = np.ones((1, 64), np.float32)
     v = np.arange(64, dtype=np.float32)[None, :] / 7
     assert np.array_equal(orc.attend_one(q, k, v, 0), v[0].astype(np.float16).astype(np.float32))
+
+
+def test_pick_adjust_hand_worked(orc):
+    """The penalties of the pick's value function (cuda/model/sample.cu:277-319) on a worked
+    case: list [3, 3, 5, 1, 3], presence 0.5, frequency 0.25, repeat penalty 2 over the last
+    2 tokens (positions 3 and 4: tokens 1 and 3).
+      token 1: -1 - (0.5 + 0.25 * 1) = -1.75, in the window and negative: * 2 = -3.5
+      token 3:  3 - (0.5 + 0.25 * 3) =  1.75, in the window and positive: / 2 = 0.875
+      token 5:  1 - (0.5 + 0.25 * 1) =  0.25, outside the window
+      tokens 0, 2, 4 are not in the list and keep their logit."""
+    row = np.array([2.0, -1.0, 0.5, 3.0, -2.0, 1.0], np.float32)
+    got = orc.pick_adjust(row, [3, 3, 5, 1, 3], presence=0.5, frequency=0.25,
+                          repeat_penalty=2.0, repeat_window=2)
+    assert got.tolist() == [2.0, -3.5, 0.5, 0.875, -2.0, 0.25]
+    # neutral values leave the row; a window of 0 turns the repeat penalty off
+    assert orc.pick_adjust(row, [3, 3]).tolist() == row.tolist()
+    assert orc.pick_adjust(row, [3], repeat_penalty=2.0, repeat_window=0).tolist() == row.tolist()

@@ -14,8 +14,9 @@ def h(x):
     return np.asarray(x, dtype=np.float64).astype(np.float16).astype(np.float64)
 
 
-def numpy_forward(region, lay, shape, ids_per_step):
-    """ids_per_step: list of token lists for one sequence (each list = one pass)."""
+def numpy_forward(region, lay, shape, ids_per_step, renorm=False):
+    """ids_per_step: list of token lists for one sequence (each list = one pass). renorm
+    (a negative control): routed weights renormalised over the chosen experts."""
     d = lay.desc
     def t(off, rows, k):
         return dequant_q8(region[off:off + rows * (k // 32) * 34].reshape(rows, -1), k).astype(np.float64)
@@ -81,10 +82,30 @@ def numpy_forward(region, lay, shape, ids_per_step):
                     att[hh * hd:(hh + 1) * hd] = h((p / p.sum()) @ V)
                 resid = resid + t(L.offset[SLOT["attn_o"]], H, wide) @ att
                 x = rms(resid, f(L.offset[SLOT["ffn_norm"]], H))
-                gate = t(L.offset[SLOT["ffn_gate"]], F, H) @ x
-                up = t(L.offset[SLOT["ffn_up"]], F, H) @ x
-                act = h(gate / (1 + np.exp(-gate)) * up)
-                resid = resid + t(L.offset[SLOT["ffn_down"]], H, F) @ act
+                if shape.experts:
+                    # routed experts (cuda/model/experts.cu:10-98): softmax over every
+                    # expert of router . half(x), the `used` largest (lower index first
+                    # on ties), their outputs weighted by those probabilities as they are
+                    # (no renormalisation over the chosen ones)
+                    E = shape.experts
+                    logit = f(L.offset[SLOT["router"]], E * H).reshape(E, H) @ x
+                    prob = np.exp(logit - logit.max())
+                    prob /= prob.sum()
+                    order = sorted(range(E), key=lambda e: (-prob[e], e))[:shape.used]
+                    if renorm:
+                        prob = prob / prob[order].sum()
+                    gate_all = t(L.offset[SLOT["ffn_gate"]], E * F, H).reshape(E, F, H)
+                    up_all = t(L.offset[SLOT["ffn_up"]], E * F, H).reshape(E, F, H)
+                    down_all = t(L.offset[SLOT["ffn_down"]], E * H, F).reshape(E, H, F)
+                    for e in order:
+                        gate, up = gate_all[e] @ x, up_all[e] @ x
+                        act = h(gate / (1 + np.exp(-gate)) * up)
+                        resid = resid + prob[e] * (down_all[e] @ act)
+                else:
+                    gate = t(L.offset[SLOT["ffn_gate"]], F, H) @ x
+                    up = t(L.offset[SLOT["ffn_up"]], F, H) @ x
+                    act = h(gate / (1 + np.exp(-gate)) * up)
+                    resid = resid + t(L.offset[SLOT["ffn_down"]], H, F) @ act
             pos += 1
         xn = rms(resid, f(d.output_norm, H))
         head_off = d.token_embd if shape.tied else d.output
@@ -92,12 +113,15 @@ def numpy_forward(region, lay, shape, ids_per_step):
     return outs
 
 
-@pytest.mark.parametrize("variant", ["llama", "qknorm_split"])
+@pytest.mark.parametrize("variant", ["llama", "qknorm_split", "experts"])
 def test_oracle_model_vs_numpy(orc, variant):
     shape = Shape(layers=2, hidden=128, ffn=192, heads=4, kv_heads=2, head_dim=64, vocab=512)
     if variant == "qknorm_split":
         shape.qk_norm = True
         shape.pairs = 0
+    if variant == "experts":
+        shape.experts, shape.used = 8, 2
+        shape.sigma = 0.2            # router logits far enough apart that the choice is clear
     region, lay = build_host(shape, seed=21)
     steps = [[5, 77, 300, 12, 9], [400], [13]]
     want = numpy_forward(region, lay, shape, steps)
@@ -109,6 +133,12 @@ def test_oracle_model_vs_numpy(orc, variant):
         assert err < 5e-3, (i, err)
         assert int(np.argmax(got)) == int(np.argmax(want[i])) or \
             np.sort(want[i])[-1] - np.sort(want[i])[-2] < 2 * np.abs(got - want[i]).max()
+    if variant == "experts":
+        # the control: renormalising the routed weights is caught by the same figure
+        wrong = numpy_forward(region, lay, shape, steps[:1], renorm=True)[0]
+        m2 = orc.Model(lay.desc, region, slots=2, max_context=64)
+        got = m2.step(steps[0], [0, len(steps[0])], [1])[0]
+        assert np.abs(got - wrong).max() / np.abs(wrong).max() > 2e-2
 
 
 def test_oracle_model_batch_equals_serial(orc):

@@ -5,7 +5,7 @@ import random
 
 import pytest
 
-from oracle.text import FAMILY, PATTERNS, Vocab, pretokens
+from oracle.text import FAMILY, PATTERNS_17, Vocab, pretokens
 from tests.text_util import hf_with, text, trained
 
 
@@ -19,7 +19,7 @@ def test_oracle_matches_tokenizers_library(bpe, family):
     tokens, merges, _ = bpe
     pattern, whole = FAMILY[family]
     v = Vocab(tokens, merges, family=family)
-    hf = hf_with(PATTERNS[pattern], tokens, merges, whole)
+    hf = hf_with(PATTERNS_17[pattern], tokens, merges, whole)
     rng = random.Random(11)
     for _ in range(300):
         s = text(rng, rng.randint(1, 40))
@@ -38,7 +38,7 @@ def test_gpt2_split_is_the_byte_level_pretokenizer(bpe):
 
 def test_pretokens_cover_text_and_known_splits():
     rng = random.Random(13)
-    for pattern in PATTERNS:
+    for pattern in PATTERNS_17:
         for _ in range(100):
             s = text(rng, 20)
             assert "".join(pretokens(s, pattern)) == s
@@ -96,7 +96,7 @@ def test_special_tokens_match_tokenizers_library(bpe, family):
     tokens, merges, _ = bpe
     toks, types = with_specials(tokens, merges)
     pattern, whole = FAMILY[family]
-    hf = hf_with(PATTERNS[pattern], tokens, merges, whole)
+    hf = hf_with(PATTERNS_17[pattern], tokens, merges, whole)
     hf.add_special_tokens([AddedToken(t, special=True, normalized=False) for t in SPECIALS])
     assert [hf.token_to_id(t) for t in SPECIALS] == [len(tokens), len(tokens) + 1, len(tokens) + 2]
     v = Vocab(toks, merges, types, family=family)

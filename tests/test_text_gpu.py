@@ -208,3 +208,35 @@ def test_invalid_utf8_vs_oracle(torch, lib, bpe):
             assert g == v.encode(s_), repr(s_)
     finally:
         built.close()
+
+
+NEW_POINTS = ["\u0870", "\U00010570", "\U0001E290", "\u0C3C", "\U0001E4D0", "\U0001E4F0",
+              "\U00011F00", "\U00011F04", "\U0001D2C0", "\U0001E030", "\U00031350", "\u0CF3",
+              "\U0002EBF0", "\U00016D40", "\U00010D40", "\U0001CCF0", "\u0897", "\uA7CB",
+              "\U00011F5A", "\U000323B0"]
+
+
+@pytest.mark.parametrize("family", ["gpt-2", "llama3", "qwen2", "qwen35"])
+def test_unicode_15_classes_vs_oracle(torch, lib, bpe, family):
+    """Code points added in Unicode 14.0 and 15.0 split as letters, numbers and marks; those
+    added in 15.1-17.0 as unassigned code points (the reference's tables are 15.0)."""
+    tokens, merges, _ = bpe
+    types = [1] * len(tokens)
+    v = Vocab(tokens, merges, types, family=family)
+    built = Built(lib, tokens, merges, types, family)
+    try:
+        rng = random.Random(77 + ROWS[family])
+        strings = []
+        for _ in range(120):
+            parts = []
+            for _ in range(rng.randint(1, 12)):
+                r = rng.random()
+                parts.append(rng.choice(NEW_POINTS) * rng.randint(1, 3) if r < 0.5
+                             else rng.choice(["a", "xy", " ", "12", "\n", "!", "é", "中"]))
+            strings.append("".join(parts))
+        got = _encode(torch, lib, strings)
+        for s, g in zip(strings, got):
+            assert g == v.encode(s.encode()), (family, repr(s))
+        assert _detok(torch, lib, got) == [s.encode() for s in strings]
+    finally:
+        built.close()
