@@ -11,6 +11,9 @@ unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
 size_t aotx_attn_scratch(unsigned int tokens, unsigned int kv_heads, unsigned int splits,
                          unsigned int group, unsigned int head_dim);
 struct aotx_attn_args;
+/* Launches of at least this many tokens (more than the sequence slots, so with prompt
+ * pieces) run the piece kernel: the queries of a sequence share their key reads. */
+#define AOTX_ATTN_PIECE_TOKENS 128u
 /* The arguments of a launch over these operands; 1 when the shape is refused. */
 int aotx_attend_plan(aotx_attn_args *args, const unsigned short *q, unsigned short *out,
                      const unsigned int *pos, const unsigned int *agent,

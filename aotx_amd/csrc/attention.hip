@@ -20,6 +20,7 @@
  *     chunks in chunk order, so the result does not depend on timing and no second
  *     launch is needed.
  */
+#include "attention.h"
 #include "attention_dev.h"
 
 #include <algorithm>
@@ -28,7 +29,15 @@
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_mma(aotx_attn_args a)
 {
-    aotx_attend_body<D, G, W>(a, blockIdx.x);
+    aotx_attend_body<D, G, W, 1>(a, blockIdx.x);
+}
+
+/* Prompt pieces: 16 / G consecutive queries of a sequence per workgroup, all of them on
+ * one read of their keys and values (the score tile's 16 columns are queries x heads). */
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) void aotx_attend_piece(aotx_attn_args a)
+{
+    aotx_attend_body<D, G, W, 16 / G>(a, blockIdx.x);
 }
 
 /* ---------------------------------------------------------------------------------------
@@ -112,6 +121,30 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
                          layer, layers, max_context, partial, count) != 0)
         return 1;
     const unsigned int g = heads / kv_heads;
+    if (tokens >= AOTX_ATTN_PIECE_TOKENS) {
+        /* more tokens than sequence slots: a batch with prompt pieces. One workgroup per
+         * token and KV head; the ones that lead a run of queries compute it. */
+        a.splits = 1u;
+        dim3 grid(tokens * kv_heads);
+#define AOTX_PIECE_GO(DD, GG)                                                              \
+        do {                                                                               \
+            hipLaunchKernelGGL((aotx_attend_piece<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
+            AOTX_LAUNCH_CHECK();                                                           \
+        } while (0)
+        if (head_dim == 128u) {
+            if (g == 1u) AOTX_PIECE_GO(128, 1);
+            else if (g == 2u) AOTX_PIECE_GO(128, 2);
+            else if (g == 4u) AOTX_PIECE_GO(128, 4);
+            else AOTX_PIECE_GO(128, 8);
+        } else {
+            if (g == 1u) AOTX_PIECE_GO(64, 1);
+            else if (g == 2u) AOTX_PIECE_GO(64, 2);
+            else if (g == 4u) AOTX_PIECE_GO(64, 4);
+            else AOTX_PIECE_GO(64, 8);
+        }
+#undef AOTX_PIECE_GO
+        return 0;
+    }
     dim3 grid(tokens * kv_heads * a.splits);
 #define AOTX_ATTN_GO(DD, GG)                                                               \
     do {                                                                                   \

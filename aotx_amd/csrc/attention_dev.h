@@ -75,16 +75,17 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
  *     against bank conflicts) to a private LDS slot and reads 16-bit columns back;
  *   - online softmax in base 2 per head with a max over the 4 lane groups of the head.
  * The output accumulators hold heads 4g..4g+3 x 16 d columns per lane and PV step. */
-template <int D, int G, int W>
+template <int D, int G, int W, int QT>
 static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a, unsigned int bx)
 {
-    static_assert(G <= 16, "one MFMA tile of query heads");
+    constexpr int C = G * QT;           /* score columns: QT queries x G heads */
+    static_assert(C <= 16, "one MFMA tile of query columns");
     constexpr int KK = D / 32;          /* score MFMA steps */
     constexpr int VP = D / 32;          /* 16-byte value pieces per lane per block */
     constexpr int NS = D / 16;          /* P.V MFMAs (16 d columns each) */
     constexpr int VS = D + 8;           /* LDS row stride of a value block (halves) */
-    __shared__ float wm[W][G], wl[W][G];
-    __shared__ float wo[W][G][D];
+    __shared__ float wm[W][C], wl[W][C];
+    __shared__ float wo[W][C][D];
     __shared__ __attribute__((aligned(16))) unsigned short vl[W][16 * VS];
 
     const unsigned int lane = threadIdx.x & 63u;
@@ -92,18 +93,42 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const unsigned int r = lane & 15u, g = lane >> 4;
     unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
     if (tokens > a.tokens) tokens = a.tokens;
-    const unsigned int S = a.splits;
-    const unsigned int c = bx % S;
-    const unsigned int rest = bx / S;
-    const unsigned int kh = rest % a.kv_heads;
-    const unsigned int t = rest / a.kv_heads;
-    if (t >= tokens) return;
-    const unsigned int n = a.pos[t] + 1u;
-    const unsigned int chunk = aotx_attn_chunk(n, S);
-    const unsigned int st = (n + chunk - 1u) / chunk;
-    if (c >= st) return;
-    const unsigned int p0 = c * chunk;
-    const unsigned int p1 = (p0 + chunk < n) ? p0 + chunk : n;
+    unsigned int S, c, kh, t, n, st, p0, p1, nq = 1u, plim;
+    if constexpr (QT == 1) {
+        S = a.splits;
+        c = bx % S;
+        const unsigned int rest = bx / S;
+        kh = rest % a.kv_heads;
+        t = rest / a.kv_heads;
+        if (t >= tokens) return;
+        n = a.pos[t] + 1u;
+        const unsigned int chunk = aotx_attn_chunk(n, S);
+        st = (n + chunk - 1u) / chunk;
+        if (c >= st) return;
+        p0 = c * chunk;
+        p1 = (p0 + chunk < n) ? p0 + chunk : n;
+        plim = p1;
+    } else {
+        /* a prompt piece: the workgroup of token t leads when t starts its sequence's run
+         * in the batch or sits at a multiple of QT, and takes the next tokens of the same
+         * sequence up to the next multiple; every query reads the keys once */
+        S = 1u;
+        c = 0u;
+        st = 1u;
+        kh = bx % a.kv_heads;
+        t = bx / a.kv_heads;
+        if (t >= tokens) return;
+        const unsigned int agent0 = a.agent[t], pos0 = a.pos[t];
+        if (t != 0u && a.agent[t - 1u] == agent0 && pos0 % QT != 0u) return;
+        while (nq < (unsigned int)QT && t + nq < tokens && a.agent[t + nq] == agent0
+               && a.pos[t + nq] % QT != 0u)
+            ++nq;
+        n = a.pos[t + nq - 1u] + 1u;
+        p0 = 0u;
+        p1 = n;
+        /* this lane's column: query r / G; a column with no query sees position 0 only */
+        plim = r / (unsigned int)G < nq ? a.pos[t + r / (unsigned int)G] + 1u : 1u;
+    }
     const unsigned int nblk = (p1 - p0 + 15u) / 16u;
     const unsigned int per = (nblk + W - 1u) / W;
     const unsigned int b0 = p0 / 16u + wave * per;
@@ -117,8 +142,9 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
         aotx_u4a w = {0u, 0u, 0u, 0u};
-        if (r < (unsigned int)G)
-            w = co_load4(a.q + ((unsigned long long)t * a.heads + kh * G + r) * D
+        const unsigned int qi = r / (unsigned int)G, hh = r % (unsigned int)G;
+        if (r < (unsigned int)C && qi < nq)
+            w = co_load4(a.q + ((unsigned long long)(t + qi) * a.heads + kh * G + hh) * D
                              + 32 * kk + 8 * g);
         qb[kk] = __builtin_bit_cast(aotx_h8a, w);
     }
@@ -174,19 +200,21 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         float mb = -INFINITY;                                                               \
         _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
             const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
-            const bool ok = p >= p0 && p < p1 && !absent[BUF];                              \
+            const bool ok = p >= p0 && p < plim && !absent[BUF];                            \
             pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
             mb = fmaxf(mb, pr[i]);                                                          \
         }                                                                                   \
         mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
         mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
         const float mnew = fmaxf(mrun, mb);                                                 \
-        const float shift = aotx_exp2(mrun - mnew);        /* 0 from -inf */                \
+        /* 0 from -inf; a column with no position yet keeps its (empty) sums */           \
+        const float shift = mnew == -INFINITY ? 1.0f : aotx_exp2(mrun - mnew);              \
         mrun = mnew;                                                                        \
         aotx_h4a pa;                                                                        \
         float mass = 0.0f;                                                                  \
         _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
-            const _Float16 ph = (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
+            const _Float16 ph = mnew == -INFINITY ? (_Float16)0.0f                          \
+                              : (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
             pa[i] = ph;                                                                     \
             mass += (float)ph;                                                              \
         }                                                                                   \
@@ -236,14 +264,14 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     lrun += __shfl_xor(lrun, 32, 64);
     missing = __any(missing);
     if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
-    if (g == 0u && r < (unsigned int)G) {
+    if (g == 0u && r < (unsigned int)C) {
         wm[wave][r] = missing ? -INFINITY : mrun;
         wl[wave][r] = missing ? 0.0f : lrun;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned int head = 4u * g + (unsigned int)i;
-        if (head < (unsigned int)G) {
+        if (head < (unsigned int)C) {
 #pragma unroll
             for (int cc = 0; cc < NS; ++cc) wo[wave][head][16 * cc + r] = missing ? 0.0f : o[cc][i];
         }
@@ -253,8 +281,11 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const unsigned int unit = t * a.kv_heads + kh;
     const unsigned int stride = G * (D + 2);
     float *mine = a.partial + ((unsigned long long)unit * S + c) * stride;
-    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D / 2); idx += 64u * W) {
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(C * D / 2); idx += 64u * W) {
         const unsigned int j = idx / (D / 2), e = 2u * (idx - j * (D / 2));
+        /* column j: query j / G (of the prompt piece; 0 in decode), head j % G */
+        const unsigned int qj = j / (unsigned int)G, hj = j % (unsigned int)G;
+        if (qj >= nq) continue;
         float top = wm[0][j];
 #pragma unroll
         for (int w = 1; w < W; ++w) top = fmaxf(top, wm[w][j]);
@@ -268,7 +299,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         }
         if (st == 1u) {
             float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-            co_store2h(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+            co_store2h(a.out + ((unsigned long long)(t + qj) * a.heads + kh * G + hj) * D + e,
                            aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
         } else {
             aotx_attn_put(mine + j * (D + 2) + 2 + e, osum[0]);

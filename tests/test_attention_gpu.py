@@ -184,3 +184,47 @@ def test_kv_release_and_reuse(torch, lib):
         assert t.page[4][0] != 0
     finally:
         lib.aotx_kv_close(ctypes.byref(m))
+
+
+@pytest.mark.parametrize("heads,kvh,d", [(32, 8, 128), (16, 2, 64), (8, 8, 64)])
+def test_attend_prompt_pieces_vs_oracle(torch, lib, orc, heads, kvh, d):
+    """A launch of 128 tokens or more (prompt pieces: more tokens than sequence slots) runs
+    the piece kernel, whose workgroups take 16 / G consecutive queries of one sequence on a
+    single read of their keys: pieces that start mid-cache at positions that are not
+    multiples of 16 / G, a run cut by the next sequence, single decode rows, causal limits
+    per query; every (token, head) vs the oracle's online softmax at its own position."""
+    layers, layer = 2, 0
+    rng = np.random.default_rng(heads + kvh + d)
+    # (slot, cached positions before the piece, piece length)
+    pieces = [(3, 0, 57), (9, 13, 30), (21, 0, 1), (40, 301, 49), (5, 7, 3), (63, 1000, 1)]
+    contexts = [c + n for _, c, n in pieces]
+    slots = [s for s, _, _ in pieces]
+    m = _open_pool(lib, 256)
+    try:
+        for s, n in zip(slots, contexts):
+            assert lib.aotx_kv_request(s, layout_pages(n, layers, kvh, d)) == 1
+        lib.aotx_kv_serve(ctypes.byref(m), None)
+        keys, vals = _fill(torch, lib, slots, contexts, layers, layer, kvh, d, rng)
+        pos = np.concatenate([np.arange(c, c + n) for _, c, n in pieces]).astype(np.uint32)
+        ag = np.concatenate([np.full(n, s) for s, _, n in pieces]).astype(np.uint32)
+        tokens = len(pos)
+        assert tokens >= 128
+        q = rng.normal(0, 1, (tokens, heads, d)).astype(np.float16)
+        out = torch.zeros(tokens * heads * d, dtype=torch.float16, device="cuda")
+        lib.aotx_model_forget()
+        assert lib.aotx_attend_paged(p(dev(q, torch)), p(dev(pos, torch)), p(dev(ag, torch)),
+                                     tokens, heads, kvh, d, layer, layers, p(out), None) == 0
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(tokens, heads, d).astype(np.float32)
+        g = heads // kvh
+        for i in range(tokens):
+            s, last = int(ag[i]), int(pos[i])
+            for hh in range(heads):
+                kk = keys[s][:, hh // g, :].astype(np.float32)
+                vv = vals[s][:, hh // g, :].astype(np.float32)
+                want = orc.attend_one(q[i, hh].astype(np.float32), kk, vv, last)
+                err = np.abs(got[i, hh] - want).max()
+                assert err < 4e-3, (i, s, last, hh, err)
+        assert lib.aotx_model_faulted() == 0
+    finally:
+        lib.aotx_kv_close(ctypes.byref(m))

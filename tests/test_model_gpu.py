@@ -285,6 +285,36 @@ def test_8b_width_experts_wide_batch_vs_oracle(torch, orc):
         rt.close()
 
 
+@pytest.mark.parametrize("prompt", [300, 512])
+def test_8b_width_long_prompt_logits_vs_oracle(torch, orc, prompt):
+    """A prompt of 300 and of 512 tokens in one pass through aotx_model_prefill on an
+    8B-width model (2 layers: d_model 4096, FFN 14336, 32/8 heads x 128): the GEMM of 256
+    rows or more with its QKV rotary/page-write, residual and SwiGLU epilogues, and the
+    prompt-piece attention; the logits of tokens 1, 17, 130 and 257 and of the last vs the
+    oracle
+    (cuda/model/gemm.cuh:55-189, cuda/model/attention.cu:22-154)."""
+    shape = Shape(layers=2, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
+                  vocab=1024)
+    region_dev, region, lay = _device_model(torch, shape, 13)
+    rt = Runtime(region_dev, lay.desc, max_tokens=512, pool_pages=64)
+    try:
+        rng = np.random.default_rng(prompt)
+        ids = rng.integers(0, shape.vocab, prompt).tolist()
+        lg = rt.prefill_logits(ids, [0, prompt], [3])
+        ref = orc.Model(lay.desc, region, slots=4, max_context=prompt + 2, threads=8)
+        # the oracle in one pass too (its products then read half weights, as the
+        # reference's tensor-core tile does for 17 rows or more)
+        want = ref.step(ids, [0, prompt], [3])
+        assert rel_rms(lg[prompt - 1:prompt], want) < 1e-2
+        for n in (1, 17, 130, 257):
+            r2 = orc.Model(lay.desc, region, slots=4, max_context=prompt + 2, threads=8)
+            w = r2.step(ids[:n], [0, n], [3])
+            assert rel_rms(lg[n - 1:n], w) < 1e-2, n
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
 def test_gguf_file_through_place_and_step(torch, orc, tiny, tmp_path):
     """The tiny model written as a GGUF file, read back by the library's reader, placed into
     a new weights region (aotx_model_place) and run: the same logits, bit for bit, as the
