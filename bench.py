@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+CONFIG4_STEPS = 128           # 128 decode steps from a 2048-token cache
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "attention_b32_ctx2048_traffic.md")
 
 
@@ -45,6 +46,23 @@ def measured_traffic():
     except OSError:
         pass
     return None
+
+
+def step_bytes(lay, shape, batch, ctx_mean):
+    """Algorithmic HBM bytes of one decode step: every weight the step reads once (all layer
+    matrices, the head, the norm vectors, the routers; every expert of a routed layer, which
+    a batch of 64 tokens touches with probability 1 - 1e-8), the B embedding rows (not the
+    table), the keys and values of every attended position and the new position of every
+    layer, and the logits written and read once."""
+    d = lay.desc
+    weights = 0
+    for at, kind, rows, k, _, _ in lay.tensors:
+        if at == d.token_embd:
+            continue
+        weights += rows * (k // 32) * 34 if kind == "q8" else rows * k * 4
+    emb = batch * (shape.hidden // 32) * 34
+    kv_tok = 2 * shape.kv_heads * shape.head_dim * 2 * shape.layers
+    return weights + emb + batch * (ctx_mean * kv_tok + kv_tok + shape.vocab * 8)
 
 
 def log(*a):
@@ -352,15 +370,14 @@ def moe_run(args):
     log(f"moe: seated {batch} x {context} in {time.perf_counter() - t0:.1f}s")
     tps, ms = decode(torch, rt, slots, args.steps, args.warmup, A.neutral_how())
     rt.close()
-    wbytes = region.numel()
-    ctx_mid = context + args.warmup + args.steps // 2
-    kv_tok = 2 * shape.kv_heads * shape.head_dim * 2 * shape.layers
-    step_bytes = wbytes + batch * (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
+    # attended positions per token, averaged over the timed steps (pos + 1)
+    ctx_mean = context + args.warmup + (args.steps + 1) / 2.0
+    sb = step_bytes(lay, shape, batch, ctx_mean)
     out = {"metric": "Mixtral-shape MoE decode tokens/s (BASELINE config 5)",
            "value": round(tps, 2), "unit": "tokens/s", "ms_per_step": round(ms, 4),
            "steps": args.steps, "warmup": args.warmup, "batch": batch, "context": context,
-           "weights_gb": round(wbytes / 1e9, 3), "step_gb": round(step_bytes / 1e9, 3),
-           "step_roofline_frac": round(step_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+           "step_gb": round(sb / 1e9, 3),
+           "step_roofline_frac": round(sb / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
            "data": "synthetic (seeded N(0,0.02) Q8_0 weights; random fp16 KV; greedy ids)"}
     print(json.dumps(out))
 
@@ -610,7 +627,7 @@ def main():
     t0 = time.perf_counter()
     region, lay = build_device(shape, seed=0x5EED)
     log(f"bench: weights {region.numel() / 1e9:.2f} GB built in {time.perf_counter() - t0:.1f}s")
-    reserve = args.warmup * 3 + args.steps * 3 + 8
+    reserve = args.warmup * 3 + args.steps * 3 + 8 + 2 * CONFIG4_STEPS
     from aotx_amd.model import layout_pages
     per_slot = layout_pages(args.context + reserve, shape.layers, shape.kv_heads, shape.head_dim)
     batch_slots = list(range(args.batch))
@@ -639,12 +656,17 @@ def main():
     tpss, mss = decode(torch, rt, batch_slots, max(4, args.steps // 2), 1, sampled)
     log(f"bench: batch {args.batch} top-k 40/top-p 0.9/T 0.8: {tpss:.1f} tokens/s")
 
-    # algorithmic bytes of one decode step: weights + KV read/write + logits
-    wbytes = region.numel()
-    ctx_mid = args.context + args.warmup + args.steps // 2
-    kv_tok = 2 * shape.kv_heads * shape.head_dim * 2 * shape.layers
-    step_bytes = wbytes + args.batch * (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
-    step_bytes1 = wbytes + (ctx_mid * kv_tok + kv_tok + shape.vocab * 8)
+    # BASELINE config 4 exactly: 128 greedy steps of the 32 slots from context 2048
+    for sl in batch_slots:
+        A.check(L.aotx_model_seat(sl, args.context), "aotx_model_seat")
+    tps4, ms4 = decode(torch, rt, batch_slots, CONFIG4_STEPS, 0, greedy)
+    log(f"bench: config 4 ({CONFIG4_STEPS} steps from {args.context}): {tps4:.1f} tokens/s")
+
+    # algorithmic bytes of one decode step (positions attended averaged over the timed steps)
+    ctx_mean = args.context + args.warmup + (args.steps + 1) / 2.0
+    step_bytes_b = step_bytes(lay, shape, args.batch, ctx_mean)
+    step_bytes1 = step_bytes(lay, shape, 1, ctx_mean)
+    step_bytes4 = step_bytes(lay, shape, args.batch, args.context + (CONFIG4_STEPS + 1) / 2.0)
 
     result = {
         "metric": "decode tokens/s at batch 1 & 32 (8B-shape Q8); Q8 GEMV achieved HBM GB/s",
@@ -666,8 +688,14 @@ def main():
         "batch1_tokens_per_s": round(tps1, 2),
         "batch1_ms_per_step": round(ms1, 4),
         "sampled_tokens_per_s": round(tpss, 2),
-        "step_roofline_frac": round(step_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "step_gb": round(step_bytes_b / 1e9, 4),
+        "step_roofline_frac": round(step_bytes_b / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "step_gb_batch1": round(step_bytes1 / 1e9, 4),
         "step_roofline_frac_batch1": round(step_bytes1 / (ms1 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "config4_128_steps": {"tokens_per_s": round(tps4, 2), "ms_per_step": round(ms4, 4),
+                              "steps": CONFIG4_STEPS, "context_from": args.context,
+                              "step_gb": round(step_bytes4 / 1e9, 4),
+                              "step_roofline_frac": round(step_bytes4 / (ms4 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4)},
         "gemv": table,
     }
     result["roofline"] = {
@@ -702,6 +730,7 @@ def main():
         cps, cdt = cpu_baseline(region, lay, torch, cbatch, args.context, threads)
         result["cpu_baseline"] = {
             "value": round(cps, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "host_cores": os.cpu_count(), "host_cores_available": len(os.sched_getaffinity(0)),
             "sample": f"one oracle decode step, batch {cbatch}, context {args.context} "
                       f"({cdt:.1f} s on {threads} threads)"}
     print(json.dumps(result))
