@@ -29,6 +29,7 @@
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_mma(aotx_attn_args a)
 {
+    aotx_args_touch(a);
     aotx_attend_body<D, G, W, 1>(a, blockIdx.x);
 }
 
@@ -37,6 +38,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) void aotx_attend_piece(aotx_attn_args a)
 {
+    aotx_args_touch(a);
     aotx_attend_body<D, G, W, 16 / G>(a, blockIdx.x);
 }
 

@@ -31,4 +31,19 @@ static __device__ __forceinline__ void co_store2h(unsigned short *p, unsigned in
     *(unsigned int *)p = (lo & 0xffffu) | (hi << 16);
 }
 
+/* Load one word of every 64-byte line of a kernel's by-value argument block at entry and
+ * wait for them once. The compiler spreads the scalar loads of the fields over the
+ * prologue, separated by waits for the values it needs first; without this each of those
+ * rounds misses the scalar cache and waits for memory again. */
+template <typename T>
+static __device__ __forceinline__ void aotx_args_touch(const T &a)
+{
+    typedef const __attribute__((address_space(4))) unsigned int cword;
+    cword *p = (cword *)(const void *)&a;
+    unsigned int x = 0u;
+#pragma unroll
+    for (unsigned int i = 0; i < (sizeof(T) + 63u) / 64u; ++i) x ^= p[i * 16u];
+    asm volatile("" ::"s"(x));
+}
+
 #endif

@@ -68,11 +68,12 @@ void aotx_q8r_repack(const void *src, unsigned int n, unsigned int k, void *dst,
 
 /* ---- narrow batches ------------------------------------------------------------- */
 
-template <int MT, int RT, int PD, int NW>
+template <int MT, int RT, int PD, int NW, bool NORM>
 __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    rg_narrow<MT, RT, PD, NW>(a, blockIdx.x, blockIdx.y, lds);
+    aotx_args_touch(a);
+    rg_narrow<MT, RT, PD, NW, NORM>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 /* Wide batches (17..32 rows of fp16 x): a workgroup owns T 16-row tiles; its W = T * P
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     constexpr int PIECES = KC * 16;                          /* 16-byte pieces per row */
     constexpr int PPT = (MT * PIECES + NT - 1) / NT;          /* pieces per thread */
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    aotx_args_touch(a);
     const unsigned int tid = threadIdx.x;
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
@@ -281,6 +283,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
 template <int MB>
 __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
 {
+    aotx_args_touch(a0);
     constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
     constexpr int CB = MB / 16;                   /* column blocks per wave */
     constexpr int NT = 512;
@@ -582,12 +585,15 @@ static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
 {
     unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
     size_t lds = aotx_rgemv_lds(a, MT);
-    if (a.nw == 8u)
-        hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8>), dim3(a.groups * a.splits, ey), dim3(512),
-                           lds, s, a);
-    else
-        hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4>), dim3(a.groups * a.splits, ey), dim3(256),
-                           lds, s, a);
+    const dim3 grid(a.groups * a.splits, ey);
+    const bool norm = a.xmode == AOTX_X_NORM;
+    if (a.nw == 8u) {
+        if (norm) hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8, true>), grid, dim3(512), lds, s, a);
+        else hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8, false>), grid, dim3(512), lds, s, a);
+    } else {
+        if (norm) hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4, true>), grid, dim3(256), lds, s, a);
+        else hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4, false>), grid, dim3(256), lds, s, a);
+    }
     AOTX_LAUNCH_CHECK();
 }
 

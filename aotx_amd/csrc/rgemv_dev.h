@@ -133,12 +133,104 @@ static __device__ __forceinline__ unsigned int rg_vrow(const aotx_rgemv_args &a,
     return (group * rt + j) * 16u + rr;
 }
 
+/* ---- QKV epilogue (rope of queries and keys, keys and values into the paged cache) ---- */
+
+/* One output pair (rows 2pr, 2pr+1 of a tile) of one batch row, resolved before the
+ * product's sums exist: the destination (the query rows, or the cache page and the byte
+ * offset in it; the page's load stays in flight until the store uses it) and the rope
+ * rotation. mode 0: nothing to write; 1 query, 2 key, 3 value. */
+struct rg_qkv_pre {
+    unsigned long long base;        /* query rows, or the page (0: absent) */
+    unsigned long long off;         /* bytes from base */
+    float cs, sn;
+    unsigned int mode;
+    unsigned int count_fault;       /* a key's dimension 0 counts an absent page */
+};
+
+/* The rope frequency factor of the pair (1 without factors): a load that does not depend on
+ * the batch, so it can go out with the first loads of the kernel. */
+static __device__ __forceinline__ float rg_qkv_factor(const aotx_rgemv_args &a, unsigned int group,
+                                                      unsigned int rt, unsigned int pr)
+{
+    const aotx_qkv_epi &e = a.qkv;
+    if (e.factor == nullptr) return 1.0f;
+    const unsigned int row = 2u * pr;
+    const unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+    unsigned int begin;
+    rg_seg(a, v, begin);
+    /* unconditional (a value row, or a row past n, reads a factor it does not use) */
+    const unsigned int dim = (v - begin) % e.head_dim;
+    return e.factor[dim >> 1];
+}
+
+static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep(const aotx_rgemv_args &a, unsigned int group,
+                                                         unsigned int rt, unsigned int pr,
+                                                         unsigned int mm, unsigned int position,
+                                                         unsigned int agent, float fac, bool live)
+{
+    rg_qkv_pre p = {0ull, 0ull, 1.0f, 0.0f, 0u, 0u};
+    const aotx_qkv_epi &e = a.qkv;
+    const unsigned int row = 2u * pr;
+    const unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+    if (!live || v >= a.n) return p;
+    unsigned int begin;
+    const unsigned int sg = rg_seg(a, v, begin);
+    const unsigned int d = e.head_dim;
+    const unsigned int local = v - begin;
+    const unsigned int head = local / d;
+    const unsigned int dim = local - head * d;
+    if (sg <= 1u) {
+        const float step = powf(e.theta, -2.0f / (float)d);
+        float angle = (float)position * powf(step, (float)(dim >> 1));
+        if (e.factor != nullptr) angle = angle / fac;
+        sincosf(angle, &p.sn, &p.cs);
+    }
+    if (sg == 0u) {
+        p.mode = 1u;
+        p.base = (unsigned long long)e.qh;
+        p.off = 2ull * ((unsigned long long)(a.m0 + mm) * e.heads * d + local);
+        return p;
+    }
+    /* the block of aotx_kvl_block, with the page word kept apart from the offset */
+    p.mode = sg == 1u ? 2u : 3u;
+    p.count_fault = sg == 1u && dim == 0u ? 1u : 0u;
+    const aotx_kvl_shape &s = e.shape;
+    if (s.blocks_page == 0u || agent >= AOTX_SLOTS) return p;
+    const unsigned int block = (position / AOTX_KVL_BLOCK) * s.layers + e.layer;
+    const unsigned int index = block / s.blocks_page;
+    if (index >= AOTX_KV_PAGES_EACH) return p;
+    p.base = e.state->kv.page[agent][index];
+    const unsigned int krow = (sg == 1u ? head : e.kv_heads + head) * AOTX_KVL_BLOCK
+                            + position % AOTX_KVL_BLOCK;
+    p.off = AOTX_KVL_HEADER + (unsigned long long)(block % s.blocks_page) * s.block_bytes
+          + 2ull * ((unsigned long long)krow * d + dim);
+    return p;
+}
+
+template <int MT>
+static __device__ __forceinline__ void rg_qkv_store(const aotx_rgemv_args &a, const float *out,
+                                                    const rg_qkv_pre &p, unsigned int row,
+                                                    unsigned int mm)
+{
+    if (p.mode == 0u) return;
+    if (p.base == 0ull) {
+        if (p.count_fault != 0u) atomicAdd(&a.qkv.state->faults, 1u);
+        return;
+    }
+    const float a0 = out[row * MT + mm];
+    const float a1 = out[(row + 1u) * MT + mm];
+    unsigned short *dst = (unsigned short *)(p.base + p.off);
+    if (p.mode == 3u) co_store2h(dst, aotx_f2h(a0), aotx_f2h(a1));
+    else co_store2h(dst, aotx_f2h(a0 * p.cs - a1 * p.sn), aotx_f2h(a0 * p.sn + a1 * p.cs));
+}
+
 /* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. */
 template <int MT, int NT>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
                                                    unsigned int mrows, const unsigned int *list,
-                                                   const float *rpre = nullptr)
+                                                   const float *rpre = nullptr,
+                                                   const rg_qkv_pre *qp = nullptr)
 {
     const unsigned int tid = threadIdx.x;
     const unsigned int gr = rt * 16u;
@@ -205,48 +297,19 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             else dst[0] = (unsigned short)h[0];            /* odd n */
         }
     } else if (a.epi == AOTX_EPI_QKV) {
-        const aotx_qkv_epi &e = a.qkv;
-        const unsigned int d = e.head_dim;
-        const float step = powf(e.theta, -2.0f / (float)d);
-        for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += NT) {
-            unsigned int pr = idx % (gr / 2u), mm = idx / (gr / 2u);
-            unsigned int row = 2u * pr;
-            unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
-            if (mm >= mrows || v >= a.n) continue;
-            unsigned int begin;
-            const unsigned int sg = rg_seg(a, v, begin);
-            unsigned int local = v - begin;
-            unsigned int t = a.m0 + mm;
-            float a0 = out[row * MT + mm];
-            float a1 = out[(row + 1u) * MT + mm];
-            unsigned int head = local / d;
-            unsigned int dim = local - head * d;
-            unsigned int position = e.pos[t];
-            if (sg == 0u) {
-                float angle = (float)position * powf(step, (float)(dim >> 1));
-                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
-                float sn, cs;
-                sincosf(angle, &sn, &cs);
-                unsigned short *dst = e.qh + (unsigned long long)t * e.heads * d + local;
-                co_store2h(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
-                continue;
-            }
-            unsigned char *blk = aotx_kvl_block(e.shape, &e.state->kv, e.agent[t], e.layer, position);
-            if (blk == nullptr) {
-                if (dim == 0u && sg == 1u) atomicAdd(&e.state->faults, 1u);
-                continue;
-            }
-            unsigned int krow = (sg == 1u ? head : e.kv_heads + head) * AOTX_KVL_BLOCK
-                              + position % AOTX_KVL_BLOCK;
-            unsigned short *dst = (unsigned short *)blk + (unsigned long long)krow * d + dim;
-            if (sg == 1u) {
-                float angle = (float)position * powf(step, (float)(dim >> 1));
-                if (e.factor != nullptr) angle = angle / e.factor[dim >> 1];
-                float sn, cs;
-                sincosf(angle, &sn, &cs);
-                co_store2h(dst, aotx_f2h(a0 * cs - a1 * sn), aotx_f2h(a0 * sn + a1 * cs));
-            } else {
-                co_store2h(dst, aotx_f2h(a0), aotx_f2h(a1));
+        if (qp != nullptr) {
+            /* prepared before the weight stream: one unit per thread */
+            if (tid < (gr / 2u) * MT) rg_qkv_store<MT>(a, out, *qp, 2u * (tid % (gr / 2u)), tid / (gr / 2u));
+        } else {
+            for (unsigned int idx = tid; idx < (gr / 2u) * MT; idx += NT) {
+                const unsigned int pr = idx % (gr / 2u), mm = idx / (gr / 2u);
+                const bool live = mm < mrows;
+                const unsigned int t = a.m0 + mm;
+                const unsigned int position = live ? a.qkv.pos[t] : 0u;
+                const unsigned int agent = live ? a.qkv.agent[t] : 0u;
+                const float fac = rg_qkv_factor(a, group, rt, pr);
+                const rg_qkv_pre p = rg_qkv_prep(a, group, rt, pr, mm, position, agent, fac, live);
+                rg_qkv_store<MT>(a, out, p, 2u * pr, mm);
             }
         }
     }
@@ -380,7 +443,7 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
  * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
  * few tiles, so that each wave's share of the dequantisation is short). */
-template <int MT, int RT, int PD, int NW>
+template <int MT, int RT, int PD, int NW, bool NORM>
 static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsigned int bx,
                                                  unsigned int expert, unsigned char *lds)
 {
@@ -495,7 +558,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     constexpr int RG_PRE = 2;
     const bool direct = list == nullptr && a.xrow == nullptr;
     const bool early = direct;
-    const bool norm = a.xmode == AOTX_X_NORM;
+    const bool norm = NORM;
     const bool resid_pre = early && a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
     const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
     const unsigned int kbeg = q0 * 128u;
@@ -505,33 +568,50 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     rg_u4 pre[RG_PRE][4];
     float ssp[16];
     float rold[(RT * 16 * MT + 64 * NW - 1) / (64 * NW)];
+    /* Every early load is issued unconditionally, from an address clamped into the
+     * operand (a piece out of range reads the row m0 at kbeg; kbeg + 8 <= k as k is a
+     * multiple of 32), and masked where it is used: a load under a condition would be
+     * waited for where its branch joins, before the weight stream goes out. */
     if (early) {
 #pragma unroll
         for (int i = 0; i < RG_PRE; ++i) {
             const unsigned int idx = tid + (unsigned int)i * NT;
-            const unsigned int mm = idx / pieces, p = idx - mm * pieces;
-            const unsigned int kk = kbeg + p * 8u;
-            pre[i][0] = pre[i][1] = pre[i][2] = pre[i][3] = (rg_u4){0u, 0u, 0u, 0u};
-            if (mm < cap && kk + 8u <= a.k) {
-                if (norm) {
-                    const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
-                    pre[i][0] = co_load4(rrow);
-                    pre[i][1] = co_load4(rrow + 4);
-                    pre[i][2] = *(const rg_u4 *)(a.norm_w + kk);
-                    pre[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
-                } else {
-                    pre[i][0] = co_load4(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
-                }
+            unsigned int mm = idx / pieces, p = idx - mm * pieces;
+            unsigned int kk = kbeg + p * 8u;
+            if (!(mm < cap && kk + 8u <= a.k)) { mm = 0u; kk = kbeg; }
+            if (NORM) {
+                const float *rrow = a.resid + (unsigned long long)(a.m0 + mm) * a.k + kk;
+                pre[i][0] = co_load4(rrow);
+                pre[i][1] = co_load4(rrow + 4);
+                pre[i][2] = *(const rg_u4 *)(a.norm_w + kk);
+                pre[i][3] = *(const rg_u4 *)(a.norm_w + kk + 4u);
+            } else {
+                pre[i][0] = co_load4(a.x + (unsigned long long)(a.m0 + mm) * a.ldx + kk);
             }
         }
-        if (norm) {
+        if (NORM) {
             const unsigned int mm = tid >> 4, l = tid & 15u;
+            const unsigned int mc = mm < cap ? mm : 0u;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const unsigned int at = l + 16u * (unsigned int)i;
-                ssp[i] = mm < cap && at < nss ? co_loadf(a.sumsq + (unsigned long long)(a.m0 + mm) * nss + at) : 0.0f;
+                ssp[i] = co_loadf(a.sumsq + (unsigned long long)(a.m0 + mc) * nss + (at < nss ? at : 0u));
             }
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    /* the QKV epilogue's batch words (position, slot) and rope factor go out with them: its
+     * destinations and rotations are resolved while the weights stream */
+    constexpr unsigned int QU = RT * 8u * MT;          /* output pairs of the workgroup */
+    const bool qkv_pre = a.epi == AOTX_EPI_QKV && QU <= NT;
+    unsigned int q_pos = 0u, q_agent = 0u;
+    float q_fac = 1.0f;
+    if (qkv_pre && tid < QU) {
+        const unsigned int mm = tid / (RT * 8u);
+        const unsigned int mc = mm < cap ? mm : 0u;      /* unconditional, as above */
+        q_pos = a.qkv.pos[a.m0 + mc];
+        q_agent = a.qkv.agent[a.m0 + mc];
+        q_fac = rg_qkv_factor(a, group, RT, tid % (RT * 8u));
     }
     constexpr unsigned int RPT = (RT * 16u * MT + NT - 1u) / NT;   /* residual values per thread */
     if (resid_pre) {
@@ -541,17 +621,24 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
             const unsigned int rr = idx & 15u, rest = idx >> 4;
             const unsigned int j = rest % RT, mm = rest / RT;
             const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
-            rold[it] = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n
-                ? co_loadf((const float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr) : 0.0f;
+            const bool ok = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n;
+            rold[it] = co_loadf((const float *)a.y + (ok ? (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr
+                                                         : (unsigned long long)a.m0 * a.ldy));
         }
     }
 
+    __builtin_amdgcn_sched_barrier(0);
     /* with one tile per workgroup only the first buffer goes out before the staging, so
      * every workgroup's x requests queue behind less of the grid's weight stream (measured
      * faster for every one-tile shape; a gate/up pair keeps both buffers ahead) */
     const bool both_first = RT > 1;
     RG_LOAD(0, wq0);
     if (both_first) RG_LOAD(1, wq0 + PD);
+    /* nothing that uses an early load may be scheduled above the weight stream's issue: the
+     * sums start from a zero the compiler cannot see through, made after it */
+    __builtin_amdgcn_sched_barrier(0);
+    float zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
     if (a.expert_stride == 0ull && a.m_dev != nullptr) {
         unsigned int total = rg_scalar(a.m_dev);
         mrows = total > a.m0 ? total - a.m0 : 0u;
@@ -570,10 +657,10 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                 src = list != nullptr ? list[mm] / a.xrow_div : a.xrow[a.m0 + mm];
             if (l == 0u && mm < mrows) xsrc[mm] = src;
             if (norm) {
-                float sum = 0.0f;
+                float sum = zero;
                 if (early) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) sum += ssp[i];
+                    for (int i = 0; i < 16; ++i) sum += l + 16u * (unsigned int)i < nss ? ssp[i] : 0.0f;
                     if (mm < mrows)
                         for (unsigned int i = l + 256u; i < nss; i += 16u)
                             sum += co_loadf(a.sumsq + (unsigned long long)src * nss + i);
@@ -594,7 +681,11 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
             for (int it = 0; it < (int)RPT; ++it) {
                 const unsigned int idx = tid + (unsigned int)it * NT;
                 const unsigned int rr = idx & 15u, rest = idx >> 4;
-                if (idx < RT * 16u * MT) rres[((rest % RT) * 16u + rr) * MT + rest / RT] = rold[it];
+                if (idx < RT * 16u * MT) {
+                    const unsigned int j = rest % RT, mm = rest / RT;
+                    const bool ok = mm < cap && rg_vrow(a, group, j, 0u, RT) + rr < a.n;
+                    rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+                }
             }
         }
         rg_sync_lds();
@@ -624,6 +715,10 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
 
     /* each buffer is refilled right after its quads are computed, two steps ahead */
     if (!both_first) RG_LOAD(1, wq0 + PD);
+    rg_qkv_pre qpre = {0ull, 0ull, 1.0f, 0.0f, 0u, 0u};
+    if (qkv_pre && tid < QU)
+        qpre = rg_qkv_prep(a, group, RT, tid % (RT * 8u), tid / (RT * 8u), q_pos, q_agent, q_fac,
+                           tid / (RT * 8u) < mrows);
     if (wq0 < wq1) {
         unsigned int q = wq0;
         for (;;) {
@@ -666,7 +761,8 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
         __shared__ unsigned int last;
         if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
-    rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr);
+    rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr,
+                        qkv_pre ? &qpre : nullptr);
 }
 
 
