@@ -112,6 +112,22 @@ static inline __device__ unsigned char *aotx_kvl_block(const aotx_kvl_shape &s,
                              + (unsigned long long)(block % s.blocks_page) * s.block_bytes);
 }
 
+/* ---- the fragment layout of a product's x (5..32 batch rows of a dense model) ----
+ * The B operand of v_mfma_f32_16x16x32_f16 in the order a product's wave loads it, so every
+ * 16-byte load of a wave reads one contiguous kilobyte. Batch row m (< 32) and column k of
+ * a row whose width is a multiple of 128 sit at
+ *   [quad k/128][row block m/16][step (k%32)/8][lane (m%16) + 16 ((k%128)/32)][k%8]
+ * (halves): 32 rows per quad whatever the batch, 8 KB per quad. Lane (r, g) of step s then
+ * holds rows 16t + r, columns 128q + 32g + 8s .. +7, the k order of the repacked weights'
+ * A operand (lane (r, g) dequantises block 4q + g, values 8s .. 8s + 7 at step s). */
+static inline __host__ __device__ unsigned long long aotx_xfrag_at(unsigned int m, unsigned int k)
+{
+    const unsigned int q = k >> 7, g = (k >> 5) & 3u, st = (k >> 3) & 3u;
+    const unsigned int lane = (m & 15u) + 16u * g;
+    return ((((unsigned long long)q * 2u + (m >> 4)) * 4u + st) * 64u + lane) * 8u + (k & 7u);
+}
+#define AOTX_XFRAG_ROWS 32u
+
 /* fp16 <-> fp32 on raw bits */
 static inline __device__ float aotx_h2f(unsigned short h)
 {

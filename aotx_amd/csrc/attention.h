@@ -21,7 +21,8 @@ int aotx_attend_plan(aotx_attn_args *args, const unsigned short *q, unsigned sho
                      unsigned int kv_heads, unsigned int head_dim, unsigned int layer,
                      unsigned int layers, unsigned int max_context, float *partial,
                      unsigned int *count);
-/* q/out fp16 [tokens][heads][d]; m_dev = device token count (or null); partial = the
+/* q/out fp16 [tokens][heads][d] (out_frag: out in the fragment layout of aotx_xfrag_at,
+ * for at most 32 tokens of decode rows); m_dev = device token count (or null); partial = the
  * caller's chunk buffer and count its [tokens * kv_heads] arrival counters, zeroed once
  * at allocation and left at zero by every launch (either null for the library scratch). */
 int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsigned int *pos,
@@ -29,6 +30,6 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
                        unsigned int tokens, unsigned int heads, unsigned int kv_heads,
                        unsigned int head_dim, unsigned int layer, unsigned int layers,
                        unsigned int max_context, float *partial, unsigned int *count,
-                       hipStream_t stream);
+                       hipStream_t stream, unsigned int out_frag = 0u);
 
 #endif

@@ -96,6 +96,7 @@ int aotx_attend_plan(aotx_attn_args *out_args, const unsigned short *q, unsigned
     a.layer = layer;
     a.splits = aotx_attn_splits(tokens, kv_heads, max_context);
     a.chunk_max = max_context;
+    a.out_frag = 0u;
     a.shape = aotx_kvl_make(layers, kv_heads, head_dim);
     a.state = aotx_state_device();
     a.partial = partial != nullptr
@@ -116,12 +117,14 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
                        unsigned int tokens, unsigned int heads, unsigned int kv_heads,
                        unsigned int head_dim, unsigned int layer, unsigned int layers,
                        unsigned int max_context, float *partial, unsigned int *count,
-                       hipStream_t stream)
+                       hipStream_t stream, unsigned int out_frag)
 {
     aotx_attn_args a;
     if (aotx_attend_plan(&a, q, out, pos, agent, m_dev, tokens, heads, kv_heads, head_dim,
                          layer, layers, max_context, partial, count) != 0)
         return 1;
+    if (out_frag != 0u && (tokens > AOTX_XFRAG_ROWS || (heads * head_dim) % 128u != 0u)) return 1;
+    a.out_frag = out_frag;
     const unsigned int g = heads / kv_heads;
     if (tokens >= AOTX_ATTN_PIECE_TOKENS) {
         /* more tokens than sequence slots: a batch with prompt pieces. One workgroup per

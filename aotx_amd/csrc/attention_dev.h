@@ -27,7 +27,16 @@ struct aotx_attn_args {
     aotx_state *state;
     float *partial;               /* [tokens*kv_heads][splits][G*(d+2)] */
     unsigned int *count;          /* [tokens*kv_heads] chunk arrivals, zero between launches */
+    unsigned int out_frag;        /* out in the fragment layout (aotx_xfrag_at) */
 };
+
+/* Half index of out for query row t, head h, dimension e. */
+static __device__ __forceinline__ unsigned long long aotx_attn_out_at(const aotx_attn_args &a,
+                                                                    unsigned int t, unsigned int h,
+                                                                    unsigned int e, unsigned int d)
+{
+    return a.out_frag ? aotx_xfrag_at(t, h * d + e) : ((unsigned long long)t * a.heads + h) * d + e;
+}
 
 #define ATTN_CHUNK_ALIGN 64u   /* a chunk is a whole number of 16-position blocks per wave */
 #define ATTN_MAX_SPLITS 32u
@@ -299,7 +308,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         }
         if (st == 1u) {
             float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-            co_store2h(a.out + ((unsigned long long)(t + qj) * a.heads + kh * G + hj) * D + e,
+            co_store2h(a.out + aotx_attn_out_at(a, t + qj, kh * G + hj, e, D),
                            aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
         } else {
             aotx_attn_put(mine + j * (D + 2) + 2 + e, osum[0]);
@@ -353,7 +362,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
             }
         }
         const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-        co_store2h(a.out + ((unsigned long long)t * a.heads + kh * G + j) * D + e,
+        co_store2h(a.out + aotx_attn_out_at(a, t, kh * G + j, e, D),
                        aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
     }
 }

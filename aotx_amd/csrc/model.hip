@@ -249,7 +249,10 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
         mt = gemm ? (cap - m0 < AOTX_RGEMM_ROWS ? cap - m0 : AOTX_RGEMM_ROWS)
                   : (cap - m0 < 32u ? cap - m0 : 32u);
         aotx_rgemv_args a;
-        if (aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt) != 0) {
+        const int refused = tmpl.xmode == AOTX_X_FRAG
+            ? aotx_rgemv_plan_frag(&a, w, rows, nseg, k, epi, mt)
+            : aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt);
+        if (refused != 0) {
             fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);
             exit(1);
         }
@@ -292,6 +295,7 @@ static void aotx_roperands(aotx_rgemv_args *p, const aotx_rgemv_args &tmpl)
         a.sumsq_out = tmpl.sumsq_out;
         a.xg_out = tmpl.xg_out;
         a.xg_w = tmpl.xg_w;
+        a.out_frag = tmpl.out_frag;
         a.row_ss = tmpl.row_ss;
         a.row_eps = tmpl.row_eps;
         a.qkv = tmpl.qkv;
@@ -326,6 +330,20 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
      * x = half(resid * w) for the next norm's weights w, and the next product multiplies its
      * outputs by the rows' RMSNorm scale, so no norm kernel runs between them */
     const bool scaled_x = !fused_norm && !experts;
+    /* and up to 32 rows, when every width is a multiple of 128: the x of QKV (the first
+     * norm's and the down products' output) and of O (the attention's) are written in the
+     * fragment layout and read by the fragment product, whose waves load their MFMA
+     * operands straight from it; gate/up and down keep the wide kernel, measured faster
+     * there (AOTX_FRAG=0 keeps the row layout everywhere, for comparison) */
+    static const bool frag_on = [] {
+        const char *v = getenv("AOTX_FRAG");
+        return !(v != nullptr && v[0] == '0');
+    }();
+    const bool frag_dims = d->hidden % 128u == 0u && wide % 128u == 0u && d->ffn % 128u == 0u;
+    const bool frag = frag_on && scaled_x && T <= AOTX_XFRAG_ROWS && frag_dims;
+    const bool head_frag = frag_on && d->hidden % 128u == 0u && R > AOTX_NARROW_ROWS
+                        && R <= AOTX_XFRAG_ROWS;
+    const int xmode_in = frag ? AOTX_X_FRAG : AOTX_X_F16;
 
     if (tk != nullptr) {
         /* the tick: the plan packs the batch on the device and the call block points at it */
@@ -350,6 +368,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     nrm.eps = d->rms_eps;
     nrm.hidden = d->hidden;
     nrm.x = h->x;
+    nrm.x_frag = frag ? 1u : 0u;
 
     for (unsigned int l = 0; l < d->layers; ++l) {
         const aotx_model_layer *L = &d->layer[l];
@@ -374,7 +393,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
                 x_in.row_ss = h->sumsq;          /* x = half(resid * attn_w) from the down product */
                 x_in.row_eps = d->rms_eps;
             }
-            x_in.xmode = AOTX_X_F16;
+            x_in.xmode = xmode_in;
             x_in.x = h->x;
             x_in.ldx = d->hidden;
         }
@@ -427,21 +446,21 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
         }
         if (aotx_attend_launch(h->qh, h->att, h->pos, h->tagent, m_tokens, T, d->heads,
                                d->kv_heads, hd, l, d->layers, max_context, h->attn_partial,
-                               h->attn_count, s) != 0) {
+                               h->attn_count, s, frag ? 1u : 0u) != 0) {
             fprintf(stderr, "aotx: attention refused the shape\n");
             exit(1);
         }
         {
             aotx_rgemv_args t;
             memset(&t, 0, sizeof t);
-            t.xmode = AOTX_X_F16;
+            t.xmode = xmode_in;              /* the attention's output */
             t.x = h->att;
             t.ldx = wide;
             t.y = h->resid;
             t.ldy = d->hidden;
             t.sumsq_out = h->sumsq;
             if (scaled_x) {
-                t.xg_out = h->x;
+                t.xg_out = h->x;                 /* gate/up's x: row layout */
                 t.xg_w = ffn_w;
             }
             const void *o_w[1] = {RL->o};
@@ -528,6 +547,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             if (scaled_x && l + 1u < d->layers) {
                 u.xg_out = h->x;
                 u.xg_w = (const float *)aotx_tensor(d->layer[l + 1u].offset[AOTX_SLOT_ATTN_NORM]);
+                u.out_frag = frag ? 1u : 0u;
             }
             const void *dn_w[1] = {RL->down};
             unsigned int dn_rows[1] = {d->hidden};
@@ -545,11 +565,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             aotx_norm_args on = nrm;
             on.norm_w = out_w;
             on.x = nullptr;
+            on.x_frag = 0u;
             on.sel = h->sel;
+            on.sel_frag = head_frag ? 1u : 0u;
             on.last = h->last;
             on.step = h->step;
             aotx_launch_norm(on, T, s);
-            t.xmode = AOTX_X_F16;
+            t.xmode = head_frag ? AOTX_X_FRAG : AOTX_X_F16;
             t.x = h->sel;
             t.ldx = d->hidden;
         }
@@ -623,10 +645,12 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
     const size_t wide = (size_t)d->heads * hd, narrow = (size_t)d->kv_heads * hd;
     h->resid = (float *)aotx_take(h, T * d->hidden * 4u);
     h->sumsq = (float *)aotx_take(h, T * ((d->hidden + 15u) / 16u) * 4u);
-    h->x = (unsigned short *)aotx_take(h, T * d->hidden * 2u);
+    /* x, att and act hold 32 rows at least: the fragment layout of 5..32-row buckets */
+    const size_t TF = T > AOTX_XFRAG_ROWS ? T : AOTX_XFRAG_ROWS;
+    h->x = (unsigned short *)aotx_take(h, TF * d->hidden * 2u);
     h->qh = (unsigned short *)aotx_take(h, T * wide * 2u);
-    h->att = (unsigned short *)aotx_take(h, T * wide * 2u);
-    h->act = (unsigned short *)aotx_take(h, T * d->ffn * 2u);
+    h->att = (unsigned short *)aotx_take(h, TF * wide * 2u);
+    h->act = (unsigned short *)aotx_take(h, TF * d->ffn * 2u);
     h->sel = (unsigned short *)aotx_take(h, R * d->hidden * 2u);
     h->qkv = (float *)aotx_take(h, T * (wide + 2u * narrow) * 4u);
     h->logits = (float *)aotx_take(h, R * d->vocab * 4u);
@@ -704,6 +728,17 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
             }
             unsigned int rv[1] = {d->vocab};
             if (aotx_rgemv_plan(&a, w1, rv, 1u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            /* the fragment products of the same shapes */
+            if (aotx_rgemv_plan_frag(&a, w3, r3, 3u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan_frag(&a, w1, r1, 1u, (unsigned int)wide, AOTX_EPI_RESID, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan_frag(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan_frag(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan_frag(&a, w1, rv, 1u, d->hidden, AOTX_EPI_F32, mt) == 0)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
         }
     }
@@ -1000,6 +1035,7 @@ extern "C" unsigned long long aotx_model_buffer(unsigned int role, unsigned int 
     if (role >= AOTX_MODEL_ROLES || !aotx_holds[role].ready) return 0ull;
     const aotx_hold *h = &aotx_holds[role];
     switch (which) {
+    /* x and sel of a 5..32-row bucket are in the fragment layout (aotx_xfrag_at) */
     case 0: return (unsigned long long)h->x;        /* last norm output, fp16 */
     case 1: return (unsigned long long)h->resid;    /* residual stream, fp32 */
     case 2: return (unsigned long long)h->logits;   /* head rows, fp32 */

@@ -36,7 +36,8 @@ void aotx_q8r_repack(const void *src, unsigned int n, unsigned int k, void *dst,
 /* How the batch rows of x reach the product. */
 enum {
     AOTX_X_F16 = 0,       /* x fp16 [rows][ldx] in device memory */
-    AOTX_X_NORM = 1       /* x = half(rsqrt(ss/h + eps) * resid * w) computed per workgroup */
+    AOTX_X_NORM = 1,      /* x = half(rsqrt(ss/h + eps) * resid * w) computed per workgroup */
+    AOTX_X_FRAG = 2       /* x fp16 in the fragment layout (aotx_xfrag_at), 32 rows, m0 = 0 */
 };
 
 struct aotx_rgemv_args {
@@ -49,6 +50,7 @@ struct aotx_rgemv_args {
     unsigned int rt;              /* 16-row tiles per workgroup */
     unsigned int wide;            /* 1: the tile-split wide-batch kernel (fp16 x only) */
     unsigned int gemm;            /* 1: the GEMM of 33..512 rows (fp16 x, direct rows) */
+    unsigned int frag;            /* 1: the fragment-layout product (AOTX_X_FRAG, 5..32 rows) */
     unsigned int pd;              /* quads loaded ahead per wave (narrow kernel) */
     unsigned int nw;              /* waves per workgroup (narrow kernel: 4 or 8) */
     unsigned int groups;          /* workgroups along n */
@@ -74,6 +76,7 @@ struct aotx_rgemv_args {
     unsigned int *count;          /* splits > 1: [experts][groups] arrivals, zero between launches */
     float *sumsq_out;             /* AOTX_EPI_RESID: [rows][n/16] sums of squares */
     unsigned short *xg_out;       /* AOTX_EPI_RESID, optional: fp16 resid * xg_w, [rows][n] */
+    unsigned int out_frag;        /* xg_out, and SWIGLU's y, in the fragment layout */
     const float *xg_w;            /* the next norm's weights [n] */
     const float *row_ss;          /* optional (wide batches, direct rows): the rows' partial
                                      sums of squares [rows][k/16]; outputs are multiplied by
@@ -97,6 +100,11 @@ struct aotx_rgemv_args {
 #define AOTX_RGEMM_ROWS 512u
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                     unsigned int nseg, unsigned int k, int epi, unsigned int mt);
+/* Plan a product whose x is in the fragment layout (AOTX_X_FRAG): a dense product of at
+ * most 32 rows (one pass, m0 = 0) over tensors whose k is a multiple of 128; 1 when
+ * refused. */
+int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                         unsigned int nseg, unsigned int k, int epi, unsigned int mt);
 /* Launch one pass (<= 32 rows) and, with splits > 1, the kernel that adds the partials
  * and applies the epilogue. */
 void aotx_rgemv_launch(const aotx_rgemv_args &a, hipStream_t stream);

@@ -105,17 +105,15 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     const unsigned int expert = blockIdx.y;
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
+    const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
     if (a.expert_stride != 0ull) {
+        /* an expert no row chose streams nothing: its row count comes first */
         unsigned int total = rg_scalar(a.list_count + expert);
         mrows = total > a.m0 ? total - a.m0 : 0u;
         list = a.list + (unsigned long long)expert * a.list_cap + a.m0;
-    } else if (a.m_dev != nullptr) {
-        unsigned int total = rg_scalar(a.m_dev);
-        mrows = total > a.m0 ? total - a.m0 : 0u;
+        if (mrows > cap) mrows = cap;
+        if (mrows == 0u) return;
     }
-    if (mrows > a.m) mrows = a.m;
-    if (mrows > (unsigned int)MT) mrows = MT;
-    if (mrows == 0u) return;
 
     const unsigned int group = blockIdx.x / a.splits;
     const unsigned int split = blockIdx.x % a.splits;
@@ -176,16 +174,27 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     /* x chunk c: rows past mrows and k past a.k are zeros. A thread's pieces keep their
      * batch row from chunk to chunk, so the source rows are looked up once, here, before
      * any weight load (a lookup after them would wait for all of them). */
+    /* Batch rows of x are loaded for the pass capacity (rows past the count are stale rows
+     * of the x buffer: a batch column only feeds its own output column, which is never
+     * written), so no load waits for the device row count. Every x load is unconditional,
+     * from an address clamped into x, and k past a.k is zeroed where it is stored (the
+     * weights there are zero, and zero times a stale infinity would not be): a load under
+     * a condition would be waited for where its branch joins, before the weight stream. */
     rg_u4 xr[PPT];
     unsigned int xsrcv[PPT];
+    if (list == nullptr && a.xrow == nullptr) {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-        const unsigned int idx = tid + (unsigned int)i * NT;
-        const unsigned int mm = idx / PIECES;
-        xsrcv[i] = 0xFFFFFFFFu;
-        if (idx < (unsigned int)(MT * PIECES) && mm < mrows)
-            xsrcv[i] = list != nullptr ? list[mm] / a.xrow_div
-                     : (a.xrow != nullptr ? a.xrow[a.m0 + mm] : a.m0 + mm);
+        for (int i = 0; i < PPT; ++i) {
+            const unsigned int mm = (tid + (unsigned int)i * NT) / PIECES;
+            xsrcv[i] = a.m0 + (mm < cap ? mm : 0u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const unsigned int mm = (tid + (unsigned int)i * NT) / PIECES;
+            const unsigned int mc = mm < mrows ? mm : 0u;
+            xsrcv[i] = list != nullptr ? list[mc] / a.xrow_div : a.xrow[a.m0 + mc];
+        }
     }
 #define RGW_XLOAD(C)                                                                     \
     do {                                                                                 \
@@ -193,9 +202,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
             unsigned int idx = tid + (unsigned int)i * NT;                               \
             unsigned int p = idx % PIECES;                                               \
             unsigned int kk = (q0 + (C) * KC) * 128u + p * 8u;                           \
-            xr[i] = (rg_u4){0u, 0u, 0u, 0u};                                             \
-            if (xsrcv[i] != 0xFFFFFFFFu && kk < q1 * 128u && kk < a.k)                   \
-                xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)xsrcv[i] * a.ldx + kk); \
+            if (!(kk < q1 * 128u && kk < a.k)) kk = 0u;                                  \
+            xr[i] = *(const rg_u4 *)(a.x + (unsigned long long)xsrcv[i] * a.ldx + kk);   \
         }                                                                                \
     } while (0)
 #define RGW_XSTORE(C)                                                                    \
@@ -204,8 +212,10 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                \
             unsigned int idx = tid + (unsigned int)i * NT;                               \
             unsigned int mm = idx / PIECES, p = idx % PIECES;                            \
+            unsigned int kk = (q0 + (C) * KC) * 128u + p * 8u;                           \
+            const rg_u4 v = kk < q1 * 128u && kk < a.k ? xr[i] : (rg_u4){0u, 0u, 0u, 0u}; \
             if (idx < (unsigned int)(MT * PIECES))                                       \
-                *(rg_u4 *)(xb + mm * XS + p * 8u) = xr[i];                               \
+                *(rg_u4 *)(xb + mm * XS + p * 8u) = v;                                   \
         }                                                                                \
     } while (0)
 
@@ -216,6 +226,13 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     RGW_XLOAD(0u);
     RGW_LOAD(0, 0u);
     RGW_LOAD(1, (unsigned int)PDQ);
+    __builtin_amdgcn_sched_barrier(0);
+    if (list == nullptr && a.m_dev != nullptr) {
+        /* the device row count, after the weight stream went out */
+        unsigned int total = rg_scalar(a.m_dev);
+        mrows = total > a.m0 ? total - a.m0 : 0u;
+    }
+    if (mrows > cap) mrows = cap;
     RGW_XSTORE(0u);
     rg_sync_lds();
     for (unsigned int c = 0; c < nch; ++c) {
@@ -268,6 +285,213 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
     }
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
+}
+
+/* Wide batches (5..32 rows) of a dense model with x in the fragment layout (aotx_xfrag_at):
+ * a workgroup owns RT 16-row tiles of one k split, and its NW waves take consecutive runs
+ * of that split's quads. Every wave loads, per quad, the tiles' weights (two 1 KB loads per
+ * tile) and the quad's 32 x rows as eight B operands (eight 1 KB loads, shared by the RT
+ * tiles), PD quads per buffer, two buffers ahead of the MFMAs: no LDS for x and no barrier
+ * until the waves' sums are added in wave order. Split partials, the RMSNorm row scale and
+ * the epilogues are those of the other products; SS loads the row scale's partial sums
+ * with the first loads. */
+template <int RT, int NW, int PD, bool SS>
+__global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
+{
+    constexpr int MT = 32;
+    constexpr unsigned int NT = 64u * NW;
+    __shared__ float part[NW * RT * 16 * MT];           /* the waves' sums, then out */
+    __shared__ float rres[RT * 16 * MT];                /* the epilogue's residual values */
+    aotx_args_touch(a);
+    const unsigned int tid = threadIdx.x;
+    const unsigned int lane = tid & 63u;
+    const unsigned int wave = tid >> 6;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+    const unsigned int group = blockIdx.x / a.splits;
+    const unsigned int split = blockIdx.x % a.splits;
+    const unsigned int q0 = split * a.qps;
+    const unsigned int q1 = q0 + a.qps < a.qn ? q0 + a.qps : a.qn;
+    const unsigned int nq = q1 - q0;
+    const unsigned int per = (nq + NW - 1u) / NW;
+    const unsigned int wq0 = q0 + wave * per < q1 ? q0 + wave * per : q1;
+    const unsigned int wq1 = wq0 + per < q1 ? wq0 + per : q1;
+    const unsigned int qlast = wq0 < wq1 ? wq1 - 1u : q0;
+    const unsigned int cap = a.m < (unsigned int)MT ? a.m : (unsigned int)MT;
+
+    const unsigned char *qb[RT];
+    const unsigned short *sb[RT];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+        unsigned int dummy = 0u;
+        qb[j] = rg_tile(a, group, (unsigned int)j, RT, 0u, dummy) + lane * 16u;
+        sb[j] = rg_scales(a, group, (unsigned int)j, RT, 0u) + lane;
+    }
+    const rg_u4 *xf = (const rg_u4 *)a.x + lane;
+
+    /* ---- loads that do not depend on the weights go out first, unconditionally (from
+     * clamped addresses; masked where used): the QKV epilogue's batch words and rope
+     * factor, and the residual values the residual epilogue adds to ---- */
+    constexpr unsigned int QU = RT * 8u * MT;
+    const bool qkv_pre = a.epi == AOTX_EPI_QKV && QU <= NT;
+    unsigned int q_pos = 0u, q_agent = 0u;
+    float q_fac = 1.0f;
+    if (qkv_pre && tid < QU) {
+        const unsigned int mm = tid / (RT * 8u);
+        const unsigned int mc = mm < cap ? mm : 0u;
+        q_pos = a.qkv.pos[mc];
+        q_agent = a.qkv.agent[mc];
+        q_fac = rg_qkv_factor(a, group, RT, tid % (RT * 8u));
+    }
+    const bool resid_pre = a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr && a.splits == 1u;
+    constexpr unsigned int RPT = (RT * 16u * MT + NT - 1u) / NT;
+    float rold[RPT];
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % RT, mm = rest / RT;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, RT);
+            const bool ok = idx < RT * 16u * MT && mm < cap && v0 + rr < a.n;
+            rold[it] = co_loadf((const float *)a.y + (ok ? (unsigned long long)mm * a.ldy + v0 + rr : 0ull));
+        }
+    }
+    rg_ss_pre<MT, NT> ssp;
+    const bool ss_pre = SS && rg_row_ss_load<MT, NT>(a, cap, ssp);
+    __builtin_amdgcn_sched_barrier(0);
+
+    rg_f4 acc[RT][2];
+#pragma unroll
+    for (int j = 0; j < RT; ++j) acc[j][0] = acc[j][1] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+    rg_u4 wa[2][PD][RT][2];
+    unsigned int ws[2][PD][RT];
+    rg_u4 xb[2][PD][2][4];
+    /* quads past the wave's range reload its last quad (a cache hit) and are not added */
+#define RGF_LOAD(BUF, QS)                                                                 \
+    do {                                                                                  \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                               \
+            unsigned int qq = (QS) + (unsigned int)qi;                                    \
+            if (qq > qlast) qq = qlast;                                                   \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                              \
+                const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
+                wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                      \
+                wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                 \
+                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                   \
+            }                                                                             \
+            _Pragma("unroll") for (int t = 0; t < 2; ++t)                                 \
+                _Pragma("unroll") for (int st = 0; st < 4; ++st)                          \
+                    xb[BUF][qi][t][st] = xf[(((unsigned long long)qq * 2u + t) * 4u + st) * 64u]; \
+        }                                                                                 \
+    } while (0)
+#define RGF_COMPUTE(BUF, QS)                                                              \
+    do {                                                                                  \
+        _Pragma("unroll") for (int qi = 0; qi < PD; ++qi) {                               \
+            const unsigned int qq = (QS) + (unsigned int)qi;                              \
+            _Pragma("unroll") for (int j = 0; j < RT; ++j) {                              \
+                const unsigned int sbits = qq < wq1 ? ws[BUF][qi][j] : 0u;                \
+                rg_h2 s2 = __builtin_bit_cast(rg_h2, sbits | (sbits << 16));              \
+                const rg_u4 q0v = wa[BUF][qi][j][0], q1v = wa[BUF][qi][j][1];             \
+                unsigned int qd[8] = {q0v[0], q0v[1], q0v[2], q0v[3],                     \
+                                      q1v[0], q1v[1], q1v[2], q1v[3]};                    \
+                _Pragma("unroll") for (int st = 0; st < 4; ++st) {                        \
+                    unsigned int d0, d1, d2, d3;                                          \
+                    rg_dequant4(qd[2 * st], s2, d0, d1);                                  \
+                    rg_dequant4(qd[2 * st + 1], s2, d2, d3);                              \
+                    rg_u4 av = {d0, d1, d2, d3};                                          \
+                    rg_h8 A = __builtin_bit_cast(rg_h8, av);                              \
+                    _Pragma("unroll") for (int t = 0; t < 2; ++t)                         \
+                        acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(                \
+                            A, __builtin_bit_cast(rg_h8, xb[BUF][qi][t][st]), acc[j][t], 0, 0, 0); \
+                }                                                                         \
+            }                                                                             \
+        }                                                                                 \
+    } while (0)
+
+    RGF_LOAD(0, wq0);
+    RGF_LOAD(1, wq0 + PD);
+    __builtin_amdgcn_sched_barrier(0);
+    unsigned int mrows = cap;
+    if (a.m_dev != nullptr) {
+        /* the device row count, after the weight stream went out */
+        const unsigned int total = rg_scalar(a.m_dev);
+        mrows = total < cap ? total : cap;
+    }
+    rg_qkv_pre qpre = {0ull, 0ull, 1.0f, 0.0f, 0u, 0u};
+    if (qkv_pre && tid < QU)
+        qpre = rg_qkv_prep(a, group, RT, tid % (RT * 8u), tid / (RT * 8u), q_pos, q_agent, q_fac,
+                           tid / (RT * 8u) < mrows);
+    __shared__ float rs[MT];
+    if (ss_pre) rg_row_ss_sum<MT, NT>(a, mrows, rs, ssp);
+    if (wq0 < wq1) {
+        unsigned int q = wq0;
+        for (;;) {
+            RGF_COMPUTE(0, q);
+            q += PD;
+            if (q >= wq1) break;
+            RGF_LOAD(0, q + PD);
+            RGF_COMPUTE(1, q);
+            q += PD;
+            if (q >= wq1) break;
+            RGF_LOAD(1, q + PD);
+        }
+    }
+#undef RGF_LOAD
+#undef RGF_COMPUTE
+
+    /* ---- the waves' sums in wave order ---- */
+    constexpr unsigned int GR = RT * 16u;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                part[(wave * GR + (unsigned int)j * 16u + 4u * g + (unsigned int)i) * MT
+                     + (unsigned int)t * 16u + r] = acc[j][t][i];
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            if (idx < RT * 16u * MT) {
+                const unsigned int j = rest % RT, mm = rest / RT;
+                const bool ok = mm < cap && rg_vrow(a, group, j, 0u, RT) + rr < a.n;
+                rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+            }
+        }
+    }
+    __syncthreads();
+    float sums[(GR * MT + NT - 1u) / NT];
+#pragma unroll
+    for (unsigned int i = 0; i < (GR * MT + NT - 1u) / NT; ++i) {
+        const unsigned int idx = tid + i * NT;
+        float sum = 0.0f;
+        if (idx < GR * MT) {
+            sum = part[idx];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * GR * MT + idx];
+        }
+        sums[i] = sum;
+    }
+    __syncthreads();
+    float *out = part;
+#pragma unroll
+    for (unsigned int i = 0; i < (GR * MT + NT - 1u) / NT; ++i)
+        if (tid + i * NT < GR * MT) out[tid + i * NT] = sums[i];
+    __syncthreads();
+    if (a.splits > 1u) {
+        __shared__ unsigned int last;
+        if (!rg_split_merge<NT>(a, out, GR * MT, 0u, group, split, &last)) return;
+    }
+    if (ss_pre) {
+        /* rs was written before the loop; the barriers since have published it */
+        for (unsigned int idx = tid; idx < GR * MT; idx += NT) out[idx] *= rs[idx % MT];
+        __syncthreads();
+    } else if (a.row_ss != nullptr) {
+        rg_row_scale<MT, NT>(a, out, GR, mrows, rs);
+    }
+    rg_epilogue<MT, NT>(a, out, group, RT, mrows, nullptr, resid_pre ? rres : nullptr,
+                        qkv_pre ? &qpre : nullptr);
 }
 
 /* Many batch rows (prefill): a GEMM. A workgroup takes 256 weight rows (16 tiles; for
@@ -574,6 +798,45 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
     return 0;
 }
 
+/* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
+ * shapes with 32 rows: one tile per workgroup up to 256 tiles (O, down), two up to 512
+ * (QKV), four beyond (gate/up pairs, the head); 8 waves below 256 workgroups; two quads per
+ * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd" overrides them for measurement
+ * sweeps. */
+int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                         unsigned int nseg, unsigned int k, int epi, unsigned int mt)
+{
+    if (k % 128u != 0u || mt == 0u || mt > AOTX_XFRAG_ROWS) return 1;
+    if (aotx_rgemv_plan(a, w, rows, nseg, k, epi, mt) != 0) return 1;
+    static const unsigned int *tv = [] {
+        static unsigned int v[3] = {0u, 0u, 0u};
+        const char *e = getenv("AOTX_FRAG_TUNE");
+        if (e != nullptr) sscanf(e, "%u,%u,%u", &v[0], &v[1], &v[2]);
+        return v;
+    }();
+    const unsigned int tiles = epi == AOTX_EPI_SWIGLU ? 2u * (unsigned int)aotx_q8r_tiles(a->n)
+                                                      : (a->n + 15u) / 16u;
+    unsigned int rt = epi == AOTX_EPI_SWIGLU ? 4u : (tiles <= 256u ? 1u : (tiles <= 512u ? 2u : 4u));
+    if (tv[0] == 1u || tv[0] == 2u || tv[0] == 4u) rt = tv[0];
+    if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
+    a->wide = 0u;
+    a->gemm = 0u;
+    a->frag = 1u;
+    a->rt = rt;
+    a->groups = epi == AOTX_EPI_SWIGLU ? ((unsigned int)aotx_q8r_tiles(a->n) + rt / 2u - 1u) / (rt / 2u)
+                                       : (tiles + rt - 1u) / rt;
+    unsigned int s = 1u;
+    while (a->groups * s < 192u && a->qn / (s + 1u) >= 8u) s += 1u;
+    a->qps = (a->qn + s - 1u) / s;
+    a->splits = (a->qn + a->qps - 1u) / a->qps;
+    a->nw = a->groups * a->splits < 256u ? 8u : 4u;
+    if (tv[1] == 4u || tv[1] == 8u) a->nw = tv[1];
+    a->pd = a->qps >= 64u ? 2u : 1u;
+    if (tv[2] == 1u || tv[2] == 2u) a->pd = tv[2];
+    if (rt > 1u) a->pd = 1u;
+    return 0;
+}
+
 size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
 {
     size_t e = a.expert_stride != 0ull ? a.experts : 1u;
@@ -619,6 +882,35 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), grid, dim3(512), lds, s, a);
         AOTX_LAUNCH_CHECK();
         return;
+    }
+    if (a.frag) {
+        if (a.xmode != AOTX_X_FRAG || a.expert_stride != 0ull || a.list != nullptr
+            || a.xrow != nullptr || a.m0 != 0u || a.m > AOTX_XFRAG_ROWS) {
+            fprintf(stderr, "aotx: the fragment product takes fragment-layout x of one pass\n");
+            exit(1);
+        }
+        const dim3 grid(a.groups * a.splits);
+        const bool ss = a.row_ss != nullptr && a.k <= 4096u;
+#define RGF_GO(RT, NW, PD)                                                                 \
+        do {                                                                               \
+            if (ss) hipLaunchKernelGGL((aotx_rgemv_frag<RT, NW, PD, true>), grid, dim3(64 * NW), 0, s, a); \
+            else hipLaunchKernelGGL((aotx_rgemv_frag<RT, NW, PD, false>), grid, dim3(64 * NW), 0, s, a); \
+        } while (0)
+        if (a.rt == 1u) {
+            if (a.nw == 8u) { if (a.pd == 2u) RGF_GO(1, 8, 2); else RGF_GO(1, 8, 1); }
+            else { if (a.pd == 2u) RGF_GO(1, 4, 2); else RGF_GO(1, 4, 1); }
+        } else if (a.rt == 2u) {          /* one quad per buffer (two would spill) */
+            if (a.nw == 8u) RGF_GO(2, 8, 1); else RGF_GO(2, 4, 1);
+        } else {
+            if (a.nw == 8u) RGF_GO(4, 8, 1); else RGF_GO(4, 4, 1);
+        }
+#undef RGF_GO
+        AOTX_LAUNCH_CHECK();
+        return;
+    }
+    if (a.xmode == AOTX_X_FRAG) {
+        fprintf(stderr, "aotx: fragment-layout x needs the fragment product's plan\n");
+        exit(1);
     }
     if (a.row_ss != nullptr && (!a.wide || a.list != nullptr || a.xrow != nullptr)) {
         fprintf(stderr, "aotx: the row-scaled product takes wide batches of direct rows only\n");

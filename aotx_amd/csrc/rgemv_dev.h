@@ -257,7 +257,8 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                 co_storef(p, v);
             }
             if (a.xg_out != nullptr && col_ok)
-                a.xg_out[(unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
+                a.xg_out[a.out_frag ? aotx_xfrag_at(RG_YROW(mm), v0 + rr)
+                                    : (unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
             float sq = v * v;
             sq += __shfl_xor(sq, 1, 64);
             sq += __shfl_xor(sq, 2, 64);
@@ -292,7 +293,9 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                 float unit = gate / (1.0f + expf(-gate));
                 h[e] = aotx_f2h(unit * up);
             }
-            unsigned short *dst = (unsigned short *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v;
+            unsigned short *dst = (unsigned short *)a.y
+                                + (a.out_frag ? aotx_xfrag_at(RG_YROW(mm), v)
+                                              : (unsigned long long)RG_YROW(mm) * a.ldy + v);
             if (v + 1u < a.n) co_store2h(dst, h[0], h[1]);
             else dst[0] = (unsigned short)h[0];            /* odd n */
         }
@@ -351,6 +354,62 @@ static __device__ __forceinline__ void rg_row_scale(const aotx_rgemv_args &a, fl
     __syncthreads();
     for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
     __syncthreads();
+}
+
+/* The row scale of rg_row_scale with the partial sums loaded early, before the weight
+ * stream, and added as soon as they arrive, before the product's loop (rows of at most 256
+ * partials, k <= 4096): the same 16 threads per batch row and the same order of adds, so the
+ * scale is bit-identical, and no register holds them through the loop. The loads are
+ * unconditional (rows past cap read row 0, partials past the row read its first), masked
+ * where they are added. */
+template <int MT, int NT>
+struct rg_ss_pre {
+    float v[(MT * 16 + NT - 1) / NT][16];
+};
+
+template <int MT, int NT>
+static __device__ __forceinline__ bool rg_row_ss_load(const aotx_rgemv_args &a, unsigned int cap,
+                                                      rg_ss_pre<MT, NT> &p)
+{
+    const unsigned int nss = (a.k + 15u) / 16u;
+    if (a.row_ss == nullptr || nss > 256u) return false;
+    const unsigned int tid = threadIdx.x, l = tid & 15u;
+#pragma unroll
+    for (int sl = 0; sl < (MT * 16 + NT - 1) / NT; ++sl) {
+        const unsigned int mm = ((unsigned int)sl * NT + tid) >> 4;
+        const unsigned int mc = mm < cap ? mm : 0u;
+        const float *ss = a.row_ss + (unsigned long long)(a.m0 + mc) * nss;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const unsigned int i = l + 16u * (unsigned int)u;
+            p.v[sl][u] = ss[i < nss ? i : 0u];
+        }
+    }
+    return true;
+}
+
+/* The row scales from the early partial sums into rs[MT] (LDS); the caller's later
+ * barrier publishes them. */
+template <int MT, int NT>
+static __device__ __forceinline__ void rg_row_ss_sum(const aotx_rgemv_args &a, unsigned int mrows,
+                                                     float *rs, const rg_ss_pre<MT, NT> &p)
+{
+    const unsigned int tid = threadIdx.x, l = tid & 15u;
+    const unsigned int nss = (a.k + 15u) / 16u;
+#pragma unroll
+    for (int sl = 0; sl < (MT * 16 + NT - 1) / NT; ++sl) {
+        const unsigned int mm = ((unsigned int)sl * NT + tid) >> 4;
+        float sum = 0.0f;
+        if (mm < mrows) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) sum += l + 16u * (unsigned int)u < nss ? p.v[sl][u] : 0.0f;
+        }
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        sum += __shfl_xor(sum, 8, 64);
+        if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
+    }
 }
 
 /* Eight fp16 values x = half(scale * r * w) of the fused norm (cuda/model/norm.cu:49-77),
