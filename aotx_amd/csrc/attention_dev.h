@@ -100,17 +100,32 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
     const unsigned int r = lane & 15u, g = lane >> 4;
-    unsigned int tokens = a.m_dev ? aotx_attn_scalar(a.m_dev) : a.tokens;
-    if (tokens > a.tokens) tokens = a.tokens;
+    /* one unconditional scalar load (of the device count, or of a word of the positions
+     * when there is none, then not used): a load under a condition would be waited for
+     * where the paths join. (Not the address of an argument: that would point at a private
+     * copy of the arguments, which a scalar load cannot read.) */
+    const unsigned int counted = aotx_attn_scalar(a.m_dev != nullptr ? a.m_dev : a.pos);
+    unsigned int tokens = a.m_dev != nullptr ? counted : a.tokens;
     unsigned int S, c, kh, t, n, st, p0, p1, nq = 1u, plim;
+    unsigned int agent;
     if constexpr (QT == 1) {
         S = a.splits;
         c = bx % S;
         const unsigned int rest = bx / S;
         kh = rest % a.kv_heads;
         t = rest / a.kv_heads;
-        if (t >= tokens) return;
-        n = a.pos[t] + 1u;
+        /* the token's position and slot are read before its row count is known (t is below
+         * the launch's token capacity, so both words exist): one memory round trip for all
+         * three, where a load after the count's test would wait for the count first */
+        const unsigned int pos_t = a.pos[t];
+        agent = a.agent[t];
+        __builtin_amdgcn_sched_barrier(0);
+        if (tokens > a.tokens) tokens = a.tokens;
+        /* the test reads both words, so neither load is sunk past it (a position of all
+         * ones, which no sequence reaches, would end the workgroup as a token past the
+         * count does) */
+        if (t >= tokens || (pos_t & agent) == 0xFFFFFFFFu) return;
+        n = pos_t + 1u;
         const unsigned int chunk = aotx_attn_chunk(n, S);
         st = (n + chunk - 1u) / chunk;
         if (c >= st) return;
@@ -121,6 +136,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         /* a prompt piece: the workgroup of token t leads when t starts its sequence's run
          * in the batch or sits at a multiple of QT, and takes the next tokens of the same
          * sequence up to the next multiple; every query reads the keys once */
+        if (tokens > a.tokens) tokens = a.tokens;
         S = 1u;
         c = 0u;
         st = 1u;
@@ -133,6 +149,7 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
                && a.pos[t + nq] % QT != 0u)
             ++nq;
         n = a.pos[t + nq - 1u] + 1u;
+        agent = agent0;
         p0 = 0u;
         p1 = n;
         /* this lane's column: query r / G; a column with no query sees position 0 only */
@@ -143,7 +160,6 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const unsigned int b0 = p0 / 16u + wave * per;
     unsigned int b1 = b0 + per;
     if (b1 > (p1 + 15u) / 16u) b1 = (p1 + 15u) / 16u;
-    const unsigned int agent = a.agent[t];
     const aotx_kv_table *kv = &a.state->kv;
     const float scale = 1.4426950408889634f / sqrtf((float)D);
 

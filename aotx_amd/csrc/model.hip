@@ -344,6 +344,11 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
     const bool head_frag = frag_on && d->hidden % 128u == 0u && R > AOTX_NARROW_ROWS
                         && R <= AOTX_XFRAG_ROWS;
     const int xmode_in = frag ? AOTX_X_FRAG : AOTX_X_F16;
+    static const bool frag_down_on = [] {
+        const char *v = getenv("AOTX_FRAG_DOWN");
+        return v != nullptr && v[0] == '1';
+    }();
+    const bool frag_down = frag && frag_down_on;
 
     if (tk != nullptr) {
         /* the tick: the plan packs the batch on the device and the call block points at it */
@@ -533,12 +538,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             }
             t.y = h->act;
             t.ldy = d->ffn;
+            t.out_frag = frag_down ? 1u : 0u;
             const void *gu_w[2] = {RL->gate, RL->up};
             unsigned int gu_rows[2] = {d->ffn, d->ffn};
             aotx_rproduct(h, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, m_tokens, t);
             aotx_rgemv_args u;
             memset(&u, 0, sizeof u);
-            u.xmode = AOTX_X_F16;
+            u.xmode = frag_down ? AOTX_X_FRAG : AOTX_X_F16;
             u.x = h->act;
             u.ldx = d->ffn;
             u.y = h->resid;

@@ -223,6 +223,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
      * is refilled right after its quad is computed, two quads ahead. x chunk c + 1 is
      * requested before chunk c's later weight loads, so storing it waits for nothing
      * issued after it. */
+    rg_ss_pre<MT, NT> ssp;
+    const bool ss_pre = list == nullptr && rg_row_ss_load<MT, NT>(a, cap, ssp);
     RGW_XLOAD(0u);
     RGW_LOAD(0, 0u);
     RGW_LOAD(1, (unsigned int)PDQ);
@@ -233,6 +235,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         mrows = total > a.m0 ? total - a.m0 : 0u;
     }
     if (mrows > cap) mrows = cap;
+    __shared__ float rs[MT];
+    if (ss_pre) rg_row_ss_sum<MT, NT>(a, mrows, rs, ssp);
     RGW_XSTORE(0u);
     rg_sync_lds();
     for (unsigned int c = 0; c < nch; ++c) {
@@ -280,8 +284,11 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
         __shared__ unsigned int last;
         if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
-    if (a.row_ss != nullptr) {
-        __shared__ float rs[MT];
+    if (ss_pre) {
+        /* rs was written before the loop; the barriers since have published it */
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
+        __syncthreads();
+    } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
     }
     rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
@@ -801,19 +808,21 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
 /* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
  * shapes with 32 rows: one tile per workgroup up to 256 tiles (O, down), two up to 512
  * (QKV), four beyond (gate/up pairs, the head); 8 waves below 256 workgroups; two quads per
- * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd" overrides them for measurement
- * sweeps. */
+ * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k]" overrides them for measurement
+ * sweeps (with k given, only for products of that k). */
 int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                          unsigned int nseg, unsigned int k, int epi, unsigned int mt)
 {
     if (k % 128u != 0u || mt == 0u || mt > AOTX_XFRAG_ROWS) return 1;
     if (aotx_rgemv_plan(a, w, rows, nseg, k, epi, mt) != 0) return 1;
-    static const unsigned int *tv = [] {
-        static unsigned int v[3] = {0u, 0u, 0u};
+    static const unsigned int *tv0 = [] {
+        static unsigned int v[4] = {0u, 0u, 0u, 0u};
         const char *e = getenv("AOTX_FRAG_TUNE");
-        if (e != nullptr) sscanf(e, "%u,%u,%u", &v[0], &v[1], &v[2]);
+        if (e != nullptr) sscanf(e, "%u,%u,%u,%u", &v[0], &v[1], &v[2], &v[3]);
         return v;
     }();
+    static const unsigned int none[4] = {0u, 0u, 0u, 0u};
+    const unsigned int *tv = tv0[3] == 0u || tv0[3] == k ? tv0 : none;
     const unsigned int tiles = epi == AOTX_EPI_SWIGLU ? 2u * (unsigned int)aotx_q8r_tiles(a->n)
                                                       : (a->n + 15u) / 16u;
     unsigned int rt = epi == AOTX_EPI_SWIGLU ? 4u : (tiles <= 256u ? 1u : (tiles <= 512u ? 2u : 4u));
