@@ -808,21 +808,24 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
 /* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
  * shapes with 32 rows: one tile per workgroup up to 256 tiles (O, down), two up to 512
  * (QKV), four beyond (gate/up pairs, the head); 8 waves below 256 workgroups; two quads per
- * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k]" overrides them for measurement
- * sweeps (with k given, only for products of that k). */
+ * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k[,n]]" overrides them for
+ * measurement sweeps (with k, and n the rows of all segments, given: only for those). */
 int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                          unsigned int nseg, unsigned int k, int epi, unsigned int mt)
 {
     if (k % 128u != 0u || mt == 0u || mt > AOTX_XFRAG_ROWS) return 1;
     if (aotx_rgemv_plan(a, w, rows, nseg, k, epi, mt) != 0) return 1;
     static const unsigned int *tv0 = [] {
-        static unsigned int v[4] = {0u, 0u, 0u, 0u};
+        static unsigned int v[5] = {0u, 0u, 0u, 0u, 0u};
         const char *e = getenv("AOTX_FRAG_TUNE");
-        if (e != nullptr) sscanf(e, "%u,%u,%u,%u", &v[0], &v[1], &v[2], &v[3]);
+        if (e != nullptr) sscanf(e, "%u,%u,%u,%u,%u", &v[0], &v[1], &v[2], &v[3], &v[4]);
         return v;
     }();
-    static const unsigned int none[4] = {0u, 0u, 0u, 0u};
-    const unsigned int *tv = tv0[3] == 0u || tv0[3] == k ? tv0 : none;
+    static const unsigned int none[5] = {0u, 0u, 0u, 0u, 0u};
+    unsigned int rows_all = 0u;
+    for (unsigned int sg = 0; sg < nseg; ++sg) rows_all += rows[sg];
+    const unsigned int *tv = (tv0[3] == 0u || tv0[3] == k) && (tv0[4] == 0u || tv0[4] == rows_all)
+                           ? tv0 : none;
     const unsigned int tiles = epi == AOTX_EPI_SWIGLU ? 2u * (unsigned int)aotx_q8r_tiles(a->n)
                                                       : (a->n + 15u) / 16u;
     unsigned int rt = epi == AOTX_EPI_SWIGLU ? 4u : (tiles <= 256u ? 1u : (tiles <= 512u ? 2u : 4u));
