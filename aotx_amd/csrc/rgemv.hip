@@ -765,7 +765,7 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         else a->groups = (tiles + a->rt - 1u) / a->rt;
         const unsigned int wtarget = tw.target != 0u ? tw.target : 256u;
         unsigned int s = 1u;
-        if (a->groups < 192u && a->qn > 32u)
+        if (a->groups < 192u && a->qn >= 32u)
             while (a->groups * s < wtarget && a->qn / (s + 1u) >= kc) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
