@@ -752,7 +752,7 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
         /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
          * tiles (gate/up pair, head), 4 x 2 for a 14336-row matrix, 2 x 4 for few (QKV, O,
          * down), measured best at the 8B shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
-         * no second launch) unless they have fewer than 192 workgroups and a long k (down):
+         * no second launch) unless they have fewer than 192 workgroups and k of 32 quads or more (down, a 4096-row O):
          * those split k towards 256 workgroups while a split keeps a whole chunk, and the
          * last split of a group to finish adds the partials. */
         a->wide = 1u;
