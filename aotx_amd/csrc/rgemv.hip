@@ -68,12 +68,12 @@ void aotx_q8r_repack(const void *src, unsigned int n, unsigned int k, void *dst,
 
 /* ---- narrow batches ------------------------------------------------------------- */
 
-template <int MT, int RT, int PD, int NW, bool NORM>
+template <int MT, int RT, int PD, int NW, bool NORM, bool DIRECT>
 __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
 {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     aotx_args_touch(a);
-    rg_narrow<MT, RT, PD, NW, NORM>(a, blockIdx.x, blockIdx.y, lds);
+    rg_narrow<MT, RT, PD, NW, NORM, DIRECT>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 /* Wide batches (17..32 rows of fp16 x): a workgroup owns T 16-row tiles; its W = T * P
@@ -862,13 +862,18 @@ static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
     size_t lds = aotx_rgemv_lds(a, MT);
     const dim3 grid(a.groups * a.splits, ey);
     const bool norm = a.xmode == AOTX_X_NORM;
+    const bool direct = a.expert_stride == 0ull && a.list == nullptr && a.xrow == nullptr;
+#define RGN_GO(NW, NORM)                                                                   \
+    do {                                                                                   \
+        if (direct) hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, NW, NORM, true>), grid, dim3(64 * NW), lds, s, a); \
+        else hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, NW, NORM, false>), grid, dim3(64 * NW), lds, s, a); \
+    } while (0)
     if (a.nw == 8u) {
-        if (norm) hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8, true>), grid, dim3(512), lds, s, a);
-        else hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 8, false>), grid, dim3(512), lds, s, a);
+        if (norm) RGN_GO(8, true); else RGN_GO(8, false);
     } else {
-        if (norm) hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4, true>), grid, dim3(256), lds, s, a);
-        else hipLaunchKernelGGL((aotx_rgemv<MT, RT, PD, 4, false>), grid, dim3(256), lds, s, a);
+        if (norm) RGN_GO(4, true); else RGN_GO(4, false);
     }
+#undef RGN_GO
     AOTX_LAUNCH_CHECK();
 }
 

@@ -502,17 +502,19 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
 /* MT: batch columns of the MFMA (16 or 32); RT: 16-row tiles per workgroup; PD: quads
  * loaded ahead per wave; NW: waves per workgroup, splitting the k range (8 for products of
  * few tiles, so that each wave's share of the dequantisation is short). */
-template <int MT, int RT, int PD, int NW, bool NORM>
+template <int MT, int RT, int PD, int NW, bool NORM, bool DIRECT>
 static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsigned int bx,
-                                                 unsigned int expert, unsigned char *lds)
+                                                 unsigned int expert_in, unsigned char *lds)
 {
+    /* DIRECT: batch row i is row m0 + i (no expert list, no row map), known when compiled */
+    const unsigned int expert = DIRECT ? 0u : expert_in;
     constexpr unsigned int NT = 64u * NW;
     const unsigned int tid = threadIdx.x;
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
     const unsigned int *list = nullptr;
     unsigned int mrows = a.m;
-    if (a.expert_stride != 0ull) {
+    if (!DIRECT && a.expert_stride != 0ull) {
         /* an expert no row chose streams nothing */
         unsigned int total = rg_scalar(a.list_count + expert);
         mrows = total > a.m0 ? total - a.m0 : 0u;
@@ -615,7 +617,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
      * may hold. vmcnt counts in issue order, so these must precede the weight stream to
      * be waited for without it. ---- */
     constexpr int RG_PRE = 2;
-    const bool direct = list == nullptr && a.xrow == nullptr;
+    const bool direct = DIRECT || (list == nullptr && a.xrow == nullptr);
     const bool early = direct;
     const bool norm = NORM;
     const bool resid_pre = early && a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
@@ -698,7 +700,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     __builtin_amdgcn_sched_barrier(0);
     float zero;
     asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-    if (a.expert_stride == 0ull && a.m_dev != nullptr) {
+    if ((DIRECT || a.expert_stride == 0ull) && a.m_dev != nullptr) {
         unsigned int total = rg_scalar(a.m_dev);
         mrows = total > a.m0 ? total - a.m0 : 0u;
     }
