@@ -235,12 +235,13 @@ def _device_model(torch, shape, seed):
     return region_dev, region_dev.cpu().numpy(), lay
 
 
-@pytest.mark.parametrize("rows", [32, 20])
+@pytest.mark.parametrize("rows", [32, 20, 12, 6])
 def test_8b_width_wide_batch_vs_oracle(torch, orc, rows):
-    """8B-width layer (d_model 4096, FFN 14336, 32/8 heads x 128) at 17..32 batch rows: the
-    QKV (rotary + page write), O and down (residual add + sums of squares) products take the
-    one-tile-per-workgroup wide kernel; a prompt pass of 4 tokens per slot, then a decode
-    step of one token per slot, logits vs the oracle."""
+    """8B-width layer (d_model 4096, FFN 14336, 32/8 heads x 128) at 5..32 batch rows (token
+    buckets 8, 16 and 32): QKV (rotary + page write) and O (residual add + sums of squares)
+    take the fragment-layout product, with x written in that layout by the norm, the down
+    epilogue and the attention; gate/up and down take the wide kernel. A prompt pass of 4
+    tokens per slot, then a decode step of one token per slot, logits vs the oracle."""
     shape = Shape(layers=1, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
                   vocab=1024)
     region_dev, region, lay = _device_model(torch, shape, 5)
