@@ -27,7 +27,7 @@
 #define PICK_THREADS 256u
 #define PICK_BUCKETS 256u
 #define PICK_PASSES 2u
-#define PICK_CHUNKS 16u   /* workgroups per row of the largest-logit search */
+#define PICK_CHUNKS 64u   /* workgroups per row of the largest-logit search */
 #define PICK_EXP_WGS 32u  /* workgroups per row of the exponentials and first histogram */
 
 #pragma clang fp contract(off)
@@ -104,19 +104,26 @@ static __device__ __forceinline__ bool aotx_pick_ahead(float v, unsigned int i, 
     return v > bv || (v == bv && ((i & 255u) < (bi & 255u) || ((i & 255u) == (bi & 255u) && i < bi)));
 }
 
-/* The row's largest logit from the slices of aotx_argmax_kernel (reference order). */
+/* The row's largest logit from the slices of aotx_argmax_kernel (reference order): one
+ * slice per lane, merged across the wave; every lane of a full wave gets the winner. */
+static_assert(PICK_CHUNKS <= 64u, "one slice per lane");
 static __device__ __forceinline__ void aotx_pick_top(const aotx_pick_args &a, unsigned int r,
                                                      float &best, unsigned int &at)
 {
     const unsigned int *cand = a.best + (unsigned long long)r * PICK_CHUNKS * 2u;
+    const unsigned int lane = threadIdx.x & 63u;
     best = -INFINITY;
     at = 0u;
-    for (unsigned int c = 0u; c < PICK_CHUNKS; ++c) {
-        float v = __uint_as_float(cand[2u * c]);
-        unsigned int i = cand[2u * c + 1u];
-        if (aotx_pick_ahead(v, i, best, at)) {
-            best = v;
-            at = i;
+    if (lane < PICK_CHUNKS) {
+        best = __uint_as_float(cand[2u * lane]);
+        at = cand[2u * lane + 1u];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const unsigned int oi = __shfl_xor(at, off, 64);
+        if (aotx_pick_ahead(ov, oi, best, at)) {
+            best = ov;
+            at = oi;
         }
     }
 }
@@ -145,6 +152,12 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_argmax_kernel(aotx_pick_arg
     int *token_out = run ? run->token : a.token;
     if (r >= rows || token_out == nullptr) return;
     if (run && run->select != AOTX_MODEL_ROWS_LAST) return;
+    /* the row's histogram starts at zero for the exponential pass that follows (its place
+     * in the sampler's buffer depends on the call's row count, so an earlier call with
+     * another count may have left other words there) */
+    if (c == 0u)
+        for (unsigned int i = tid; i < PICK_BUCKETS; i += PICK_THREADS)
+            a.hist[(unsigned long long)r * PICK_BUCKETS + i] = 0u;
     const float *row = a.logits + (unsigned long long)r * a.ld;
     const unsigned int span = (a.vocab + PICK_CHUNKS - 1u) / PICK_CHUNKS;
     const unsigned int lo = c * span;
@@ -266,14 +279,16 @@ __global__ __launch_bounds__(PICK_THREADS) void aotx_pick_kernel(aotx_pick_args 
     }
 
     /* largest logit and its place, from the slices of aotx_argmax_kernel */
-    if (tid == 0u) {
+    if (tid < 64u) {
         float best;
         unsigned int at;
         aotx_pick_top(a, r, best, at);
-        s_top = best;
-        mark[0] = at;
-        s_position = atomicAdd(&a.state->draw[agent], 1u);
-        if (draw_out != nullptr) draw_out[r] = s_position;
+        if (tid == 0u) {
+            s_top = best;
+            mark[0] = at;
+            s_position = atomicAdd(&a.state->draw[agent], 1u);
+            if (draw_out != nullptr) draw_out[r] = s_position;
+        }
     }
     __syncthreads();
     const float top = s_top;
