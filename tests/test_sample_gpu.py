@@ -127,3 +127,25 @@ def test_pick_distribution_chi_square(torch, lib, orc):
             used += 1
     dof = max(used - 1, 1)
     assert chi <= dof + 4 * np.sqrt(2 * dof) + 10
+
+
+def test_pick_alternating_row_counts(torch, lib, orc):
+    """Sampled picks whose calls alternate between row counts (the sampler's buffer is carved
+    by the call's row count, so each row's histogram must start at zero whatever an earlier
+    call left there): every token matches the oracle's on the same logits and draw."""
+    rng = np.random.default_rng(17)
+    lib.aotx_model_restream()
+    draws = {}
+    for rows, vocab in ((8, 4096), (3, 2048), (8, 4096), (5, 3000), (3, 2048)):
+        logits = rng.normal(0, 2, (rows, vocab)).astype(np.float32)
+        agent = np.arange(rows, dtype=np.uint32) + 10
+        tok = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        assert lib.aotx_pick(p(dev(logits, torch)), rows, vocab, p(dev(agent, torch)), None, 40, 0.9,
+                             0.8, 77, p(tok), None, None) == 0
+        torch.cuda.synchronize()
+        got = tok.cpu().numpy()
+        for i in range(rows):
+            a = int(agent[i])
+            want = orc.pick(logits[i], 40, 0.9, 0.0, 0.8, 77, a, draws.get(a, 0))[0]
+            draws[a] = draws.get(a, 0) + 1
+            assert got[i] == want, (rows, vocab, i)
