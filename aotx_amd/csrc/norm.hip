@@ -115,20 +115,30 @@ __global__ __launch_bounds__(256) void aotx_gather_kernel(const aotx_step *step,
     float *r = resid + (unsigned long long)t * hidden;
     const unsigned int tiles = (hidden + 15u) / 16u;
     for (unsigned int tile = threadIdx.x; tile < tiles; tile += blockDim.x) {
-        float sum = 0.0f;
-        for (unsigned int d = tile * 16u; d < tile * 16u + 16u && d < hidden; ++d) {
-            float v;
+        /* the tile's 16 values are loaded together (unrolled), then added in column order */
+        float v[16];
+#pragma unroll
+        for (unsigned int e = 0; e < 16u; ++e) {
+            const unsigned int d = tile * 16u + e;
+            const unsigned int dc = d < hidden ? d : hidden - 1u;
             if (embd_type == AOTX_WEIGHT_Q8_0) {
-                const unsigned char *blk = table + ((unsigned long long)row * (hidden / 32u) + d / 32u) * 34ull;
-                float scale = aotx_h2f((unsigned short)(blk[0] | (blk[1] << 8)));
-                v = scale * (float)(int)(signed char)blk[2u + d % 32u];
+                const unsigned char *blk = table + ((unsigned long long)row * (hidden / 32u) + dc / 32u) * 34ull;
+                const float scale = aotx_h2f((unsigned short)(blk[0] | (blk[1] << 8)));
+                v[e] = scale * (float)(int)(signed char)blk[2u + dc % 32u];
             } else if (embd_type == AOTX_WEIGHT_F16) {
-                v = aotx_h2f(((const unsigned short *)table)[(unsigned long long)row * hidden + d]);
+                v[e] = aotx_h2f(((const unsigned short *)table)[(unsigned long long)row * hidden + dc]);
             } else {
-                v = ((const float *)table)[(unsigned long long)row * hidden + d];
+                v[e] = ((const float *)table)[(unsigned long long)row * hidden + dc];
             }
-            r[d] = v;
-            sum += v * v;
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (unsigned int e = 0; e < 16u; ++e) {
+            const unsigned int d = tile * 16u + e;
+            if (d < hidden) {
+                r[d] = v[e];
+                sum += v[e] * v[e];
+            }
         }
         sumsq[(unsigned long long)t * tiles + tile] = sum;
     }
