@@ -226,6 +226,30 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     rg_ss_pre<MT, NT> ssp;
     const bool ss_pre = list == nullptr && rg_row_ss_load<MT, NT>(a, cap, ssp);
     RGW_XLOAD(0u);
+    /* the residual epilogue's residual values and next norm weights of few-tile products
+     * (down), for direct rows: read with the first loads, unconditionally (from clamped
+     * addresses; masked where used), instead of in dependent rounds after the split merge */
+    constexpr bool RP = T <= 2;
+    constexpr unsigned int RPT = (T * 16u * MT + NT - 1u) / NT;
+    __shared__ float rres[RP ? T * 16 * MT : 1];
+    __shared__ float rgw[RP ? T * 16 : 1];
+    const bool resid_pre = RP && list == nullptr && a.xrow == nullptr && a.epi == AOTX_EPI_RESID
+                        && a.sumsq_out != nullptr;
+    float rold[RPT];
+    float gwv = 0.0f;
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            const unsigned int j = rest % T, mm = rest / T;
+            const unsigned int v0 = rg_vrow(a, group, j, 0u, T);
+            const bool ok = idx < T * 16u * MT && mm < cap && v0 + rr < a.n;
+            rold[it] = co_loadf((const float *)a.y + (ok ? (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr
+                                                         : (unsigned long long)a.m0 * a.ldy));
+        }
+        gwv = rg_gw_load(a, group, T, tid);
+    }
     RGW_LOAD(0, 0u);
     RGW_LOAD(1, (unsigned int)PDQ);
     __builtin_amdgcn_sched_barrier(0);
@@ -238,6 +262,19 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     __shared__ float rs[MT];
     if (ss_pre) rg_row_ss_sum<MT, NT>(a, mrows, rs, ssp);
     RGW_XSTORE(0u);
+    if (resid_pre) {
+#pragma unroll
+        for (int it = 0; it < (int)RPT; ++it) {
+            const unsigned int idx = tid + (unsigned int)it * NT;
+            const unsigned int rr = idx & 15u, rest = idx >> 4;
+            if (idx < T * 16u * MT) {
+                const unsigned int j = rest % T, mm = rest / T;
+                const bool ok = mm < cap && rg_vrow(a, group, j, 0u, T) + rr < a.n;
+                rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+            }
+        }
+        if (tid < T * 16u) rgw[tid] = gwv;
+    }
     rg_sync_lds();
     for (unsigned int c = 0; c < nch; ++c) {
         const unsigned short *xb = xl + (c & 1u) * (unsigned int)(MT * XS);
@@ -291,7 +328,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
     }
-    rg_epilogue<MT, NT>(a, out, group, T, mrows, list);
+    rg_epilogue<MT, NT>(a, out, group, T, mrows, list, resid_pre ? rres : nullptr, nullptr,
+                        resid_pre ? rgw : nullptr);
 }
 
 /* Wide batches (5..32 rows) of a dense model with x in the fragment layout (aotx_xfrag_at):
@@ -363,6 +401,8 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
             rold[it] = co_loadf((const float *)a.y + (ok ? (unsigned long long)mm * a.ldy + v0 + rr : 0ull));
         }
     }
+    __shared__ float rgw[RT * 16];
+    const float gwv = resid_pre ? rg_gw_load(a, group, RT, tid) : 0.0f;
     rg_ss_pre<MT, NT> ssp;
     const bool ss_pre = SS && rg_row_ss_load<MT, NT>(a, cap, ssp);
     __builtin_amdgcn_sched_barrier(0);
@@ -466,6 +506,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
                 rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
             }
         }
+        if (tid < GR) rgw[tid] = gwv;
     }
     __syncthreads();
     float sums[(GR * MT + NT - 1u) / NT];
@@ -498,7 +539,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
         rg_row_scale<MT, NT>(a, out, GR, mrows, rs);
     }
     rg_epilogue<MT, NT>(a, out, group, RT, mrows, nullptr, resid_pre ? rres : nullptr,
-                        qkv_pre ? &qpre : nullptr);
+                        qkv_pre ? &qpre : nullptr, resid_pre ? rgw : nullptr);
 }
 
 /* Many batch rows (prefill): a GEMM. A workgroup takes 256 weight rows (16 tiles; for

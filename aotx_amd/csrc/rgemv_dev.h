@@ -224,13 +224,29 @@ static __device__ __forceinline__ void rg_qkv_store(const aotx_rgemv_args &a, co
     else co_store2h(dst, aotx_f2h(a0 * p.cs - a1 * p.sn), aotx_f2h(a0 * p.sn + a1 * p.cs));
 }
 
-/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. */
+/* The next norm's weight of the workgroup's output row tid (tid < rt * 16; the residual
+ * epilogue's xg_w), for a load issued before the weight stream: unconditional, from an
+ * address clamped into xg_w (or into y when there is no next norm), masked where used. */
+static __device__ __forceinline__ float rg_gw_load(const aotx_rgemv_args &a, unsigned int group,
+                                                   unsigned int rt, unsigned int tid)
+{
+    const unsigned int j = tid / 16u;
+    const unsigned int v = rg_vrow(a, group, j < rt ? j : 0u, tid % 16u, rt);
+    const bool ok = a.xg_w != nullptr && j < rt && v < a.n;
+    const float *src = a.xg_w != nullptr ? a.xg_w : (const float *)a.y;
+    return src[ok ? v : 0u];
+}
+
+/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. rpre and
+ * gpre, when given, hold the residual values out[] adds to and the next norm's weights of
+ * the rows (gpre[row]), read while the weights streamed. */
 template <int MT, int NT>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
                                                    unsigned int mrows, const unsigned int *list,
                                                    const float *rpre = nullptr,
-                                                   const rg_qkv_pre *qp = nullptr)
+                                                   const rg_qkv_pre *qp = nullptr,
+                                                   const float *gpre = nullptr)
 {
     const unsigned int tid = threadIdx.x;
     const unsigned int gr = rt * 16u;
@@ -248,7 +264,8 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             const bool row_ok = idx < total && mm < mrows && v0 < a.n;
             const bool col_ok = row_ok && v0 + rr < a.n;
             /* the next norm's weight is read alongside the residual, not after it */
-            const float gw = a.xg_out != nullptr && col_ok ? a.xg_w[v0 + rr] : 0.0f;
+            const float gw = a.xg_out != nullptr && col_ok
+                           ? (gpre != nullptr ? gpre[j * 16u + rr] : a.xg_w[v0 + rr]) : 0.0f;
             float v = 0.0f;
             if (col_ok) {
                 float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
@@ -626,6 +643,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     const unsigned int pieces = (q1 - q0) * 16u;       /* 16-byte pieces (8 values) per row */
     const unsigned int nss = (a.k + 15u) / 16u;
     __shared__ float rres[RT * 16 * MT];               /* the epilogue's residual values */
+    __shared__ float rgw[RT * 16];                     /* and the next norm's weights */
     rg_u4 pre[RG_PRE][4];
     float ssp[16];
     float rold[(RT * 16 * MT + 64 * NW - 1) / (64 * NW)];
@@ -687,6 +705,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                                                          : (unsigned long long)a.m0 * a.ldy));
         }
     }
+    const float gwv = resid_pre ? rg_gw_load(a, group, RT, tid) : 0.0f;
 
     __builtin_amdgcn_sched_barrier(0);
     /* with one tile per workgroup only the first buffer goes out before the staging, so
@@ -748,6 +767,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                     rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
                 }
             }
+            if (tid < RT * 16u) rgw[tid] = gwv;
         }
         rg_sync_lds();
         const unsigned int total = mrows * pieces;
@@ -823,7 +843,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
         if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
     }
     rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr,
-                        qkv_pre ? &qpre : nullptr);
+                        qkv_pre ? &qpre : nullptr, resid_pre ? rgw : nullptr);
 }
 
 
