@@ -352,34 +352,38 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     __syncthreads();
     if (last == 0u) return;
     const float *all = a.partial + (unsigned long long)unit * S * stride;
-    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D / 2); idx += 64u * W) {
-        const unsigned int j = idx / (D / 2), e = 2u * (idx - j * (D / 2));
+    /* One output value per lane: a wave's 64 lanes lie in one head (D is 64 or 128). Lane
+     * c < st reads chunk c's max and mass and the wave shares them (uniform-index
+     * shuffles), so a lane issues st + 2 loads, all in flight together, and the sums run
+     * in chunk order as before. */
+    for (unsigned int idx = threadIdx.x; idx < (unsigned int)(G * D); idx += 64u * W) {
+        const unsigned int j = idx / D, e = idx % D;
         const float *col = all + j * (D + 2);
-        float mc[ATTN_MAX_SPLITS], lc[ATTN_MAX_SPLITS], oc[ATTN_MAX_SPLITS], od[ATTN_MAX_SPLITS];
+        const unsigned int cl = lane < st ? lane : 0u;
+        const float m_l = aotx_attn_get(col + cl * stride);
+        const float l_l = aotx_attn_get(col + cl * stride + 1u);
+        float oc[ATTN_MAX_SPLITS];
 #pragma unroll
-        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
-            const bool live = cc < st;
-            mc[cc] = live ? aotx_attn_get(col + cc * stride) : -INFINITY;
-            lc[cc] = live ? aotx_attn_get(col + cc * stride + 1u) : 0.0f;
-            oc[cc] = live ? aotx_attn_get(col + cc * stride + 2u + e) : 0.0f;
-            od[cc] = live ? aotx_attn_get(col + cc * stride + 3u + e) : 0.0f;
-        }
-        float top = -INFINITY;
+        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc)
+            oc[cc] = cc < st ? aotx_attn_get(col + cc * stride + 2u + e) : 0.0f;
+        float top = lane < st ? m_l : -INFINITY;
 #pragma unroll
-        for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) top = fmaxf(top, mc[cc]);
-        float msum = 0.0f, osum[2] = {0.0f, 0.0f};
+        for (int sh = 1; sh < 64; sh <<= 1) top = fmaxf(top, __shfl_xor(top, sh, 64));
+        const float f_l = lane < st && m_l != -INFINITY ? aotx_exp2(m_l - top) : 0.0f;
+        float msum = 0.0f, osum = 0.0f;
 #pragma unroll
         for (unsigned int cc = 0; cc < ATTN_MAX_SPLITS; ++cc) {
             if (cc < st) {
-                const float f = mc[cc] == -INFINITY ? 0.0f : aotx_exp2(mc[cc] - top);
-                msum += lc[cc] * f;
-                osum[0] += oc[cc] * f;
-                osum[1] += od[cc] * f;
+                const float f = __shfl(f_l, (int)cc, 64);
+                msum += __shfl(l_l, (int)cc, 64) * f;
+                osum += oc[cc] * f;
             }
         }
         const float back = msum > 0.0f ? 1.0f / msum : 0.0f;
-        co_store2h(a.out + aotx_attn_out_at(a, t, kh * G + j, e, D),
-                       aotx_f2h(osum[0] * back), aotx_f2h(osum[1] * back));
+        const float v = osum * back;
+        const float v1 = __shfl_down(v, 1, 64);
+        if ((e & 1u) == 0u)
+            co_store2h(a.out + aotx_attn_out_at(a, t, kh * G + j, e, D), aotx_f2h(v), aotx_f2h(v1));
     }
 }
 

@@ -848,8 +848,8 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
 
 /* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
  * shapes with 32 rows: one tile per workgroup up to 256 tiles (O, down), two up to 512
- * (QKV), four beyond (gate/up pairs, the head); 8 waves below 256 workgroups; two quads per
- * buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k[,n]]" overrides them for
+ * (QKV), four beyond (gate/up pairs, the head); 8 waves up to 256 workgroups (O: 10.1
+ * against 10.7 us with 4); two quads per buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k[,n]]" overrides them for
  * measurement sweeps (with k, and n the rows of all segments, given: only for those). */
 int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                          unsigned int nseg, unsigned int k, int epi, unsigned int mt)
@@ -882,7 +882,7 @@ int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigne
     while (a->groups * s < 192u && a->qn / (s + 1u) >= 8u) s += 1u;
     a->qps = (a->qn + s - 1u) / s;
     a->splits = (a->qn + a->qps - 1u) / a->qps;
-    a->nw = a->groups * a->splits < 256u ? 8u : 4u;
+    a->nw = a->groups * a->splits <= 256u ? 8u : 4u;
     if (tv[1] == 4u || tv[1] == 8u) a->nw = tv[1];
     a->pd = a->qps >= 64u ? 2u : 1u;
     if (tv[2] == 1u || tv[2] == 2u) a->pd = tv[2];
