@@ -58,6 +58,18 @@ enum {
 
 static inline hipStream_t aotx_stream(void *s) { return (hipStream_t)s; }
 
+/* Wait for a stream's work by polling it. The calls a decode loop makes every step (page
+ * requests, serve, the offsets read-back, the step) each wait for the device; a blocking
+ * wait is woken tens of microseconds after the work ends, a poll within about one. */
+static inline void aotx_wait(hipStream_t s)
+{
+    for (;;) {
+        const hipError_t e = hipStreamQuery(s);
+        if (e == hipSuccess) return;
+        if (e != hipErrorNotReady) AOTX_CHECK(e);
+    }
+}
+
 /* ---- paged layout (cuda/model/kv_layout.cuh:37-163), one layer kind: every layer owns
  * KV pages. ---- */
 struct aotx_kvl_shape {

@@ -88,7 +88,7 @@ extern "C" int aotx_kv_serve(aotx_kv_map *map, void *stream)
     unsigned int *marks = (unsigned int *)aotx_pinned();
     AOTX_CHECK(hipMemcpyAsync(marks, (unsigned char *)&state->kv + offsetof(aotx_kv_table, made),
                               2u * sizeof *marks, hipMemcpyDeviceToHost, s));
-    AOTX_CHECK(hipStreamSynchronize(s));
+    aotx_wait(s);
     if (marks[0] == marks[1]) return 0;
     static aotx_kv_table table;
     AOTX_CHECK(hipMemcpy(&table, &state->kv, sizeof table, hipMemcpyDeviceToHost));
@@ -132,7 +132,7 @@ extern "C" int aotx_kv_serve(aotx_kv_map *map, void *stream)
     hipLaunchKernelGGL(aotx_kv_stamp_kernel, dim3(AOTX_SLOTS, (AOTX_KV_PAGES_EACH + 255u) / 256u),
                        dim3(256), 0, s, state);
     AOTX_LAUNCH_CHECK();
-    AOTX_CHECK(hipStreamSynchronize(s));
+    aotx_wait(s);
     return (int)done;
 }
 

@@ -849,7 +849,7 @@ extern "C" int aotx_model_pages(unsigned int role, const unsigned int *offset, u
     const aotx_model_desc *d = &h->desc;
     aotx_launch_request(offset, agent, seqs, aotx_kvl_make(d->layers, d->kv_heads, d->head_dim),
                         h->stream);
-    AOTX_CHECK(hipStreamSynchronize(h->stream));
+    aotx_wait(h->stream);
     return 0;
 }
 
@@ -890,7 +890,7 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
                                   (size_t)set->rows * h->desc.vocab * sizeof(float),
                                   hipMemcpyDeviceToDevice, h->stream));
     }
-    AOTX_CHECK(hipStreamSynchronize(h->stream));
+    aotx_wait(h->stream);
     return 0;
 }
 
@@ -948,7 +948,7 @@ extern "C" int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *t
         h->tick_setup[bt] = tk;
     }
     AOTX_CHECK(hipGraphLaunch(exec, h->stream));
-    AOTX_CHECK(hipStreamSynchronize(h->stream));
+    aotx_wait(h->stream);
     return 0;
 }
 
@@ -965,7 +965,7 @@ static int aotx_call_set(aotx_model_run *set, const int *ids, const unsigned int
     }
     AOTX_CHECK(hipMemcpyAsync(rows, offset, (seqs + 1u) * sizeof *rows, hipMemcpyDeviceToHost,
                               nullptr));
-    AOTX_CHECK(hipStreamSynchronize(nullptr));
+    aotx_wait(nullptr);
     for (unsigned int s = 0u; s < seqs; ++s) {
         if (rows[s + 1u] <= rows[s]) {
             fprintf(stderr, "the sequence %u of the pass holds no token\n", s);
