@@ -745,8 +745,10 @@ static unsigned int tune_nw_limit()
     return v;
 }
 
-int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
-                    unsigned int nseg, unsigned int k, int epi, unsigned int mt)
+/* narrow_max: the most batch rows that take the streaming (narrow) kernel. */
+static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                             unsigned int nseg, unsigned int k, int epi, unsigned int mt,
+                             unsigned int narrow_max)
 {
     memset(a, 0, sizeof *a);
     if (k == 0u || k % 32u != 0u || nseg == 0u || nseg > 3u || mt == 0u || mt > AOTX_RGEMM_ROWS)
@@ -788,7 +790,7 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
      * work below 32 rows, but the matrix cores are not what bounds these products: at 8
      * rows it streams the config-2 shapes 1.0-1.5x faster than the streaming kernel, whose
      * per-workgroup x staging grows with the rows; at 2 rows the streaming kernel wins. */
-    if (mt > AOTX_NARROW_ROWS) {
+    if (mt > narrow_max) {
         const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
         /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
          * tiles (gate/up pair, head), 4 x 2 for a 14336-row matrix, 2 x 4 for few (QKV, O,
@@ -844,6 +846,13 @@ int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int
      * the quads to dequantise after its data arrives), 4 otherwise */
     a->nw = a->groups * a->splits <= tune_nw_limit() ? 8u : 4u;
     return 0;
+}
+
+/* Up to AOTX_NARROW_ROWS batch rows take the streaming kernel. */
+int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                    unsigned int nseg, unsigned int k, int epi, unsigned int mt)
+{
+    return aotx_rgemv_plan_n(a, w, rows, nseg, k, epi, mt, AOTX_NARROW_ROWS);
 }
 
 /* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
@@ -1033,7 +1042,19 @@ static int aotx_q8r_gemv_any(const void *wr, unsigned int n, unsigned int k, con
         /* more than 32 rows: GEMM passes of up to AOTX_RGEMM_ROWS */
         mt = m - m0 > 32u ? (m - m0 < AOTX_RGEMM_ROWS ? m - m0 : AOTX_RGEMM_ROWS) : m - m0;
         aotx_rgemv_args a;
-        if (aotx_rgemv_plan(&a, ws, rows, 1u, k, epi, mt) != 0) return 1;
+        /* up to 8 rows of a product of at most 256 tiles and k <= 4096 (4096 square) stream
+         * faster through the narrow kernel: 9.0 against 9.8 us at 8 rows, where the wide
+         * kernel splits k to fill the chip; larger products keep the wide kernel from 5 rows
+         * (measured on the four 8B shapes; AOTX_NARROW_MAX, 1..16, overrides the choice for
+         * measurement sweeps) */
+        static const unsigned int forced = [] {
+            const char *e = getenv("AOTX_NARROW_MAX");
+            const unsigned int v = e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 0u;
+            return v <= 16u ? v : 0u;
+        }();
+        const unsigned int narrow_max = forced != 0u ? forced
+                                      : ((n + 15u) / 16u <= 256u && k <= 4096u ? 8u : AOTX_NARROW_ROWS);
+        if (aotx_rgemv_plan_n(&a, ws, rows, 1u, k, epi, mt, narrow_max) != 0) return 1;
         a.xmode = AOTX_X_F16;
         a.x = (const unsigned short *)x;
         a.ldx = k;

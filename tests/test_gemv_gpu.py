@@ -109,7 +109,7 @@ def repack(torch, lib, w, n, k):
 
 @pytest.mark.parametrize("n,k", [(64, 256), (128, 704), (80, 128), (1000, 4096), (256, 14336),
                                  (17, 96)])
-@pytest.mark.parametrize("m", [1, 3, 8, 16, 17, 32, 40, 33, 128, 300])
+@pytest.mark.parametrize("m", [1, 3, 6, 8, 16, 17, 32, 40, 33, 128, 300])
 def test_repacked_gemv_small_full(torch, lib, orc, n, k, m):
     """The streaming product over repacked weights (the model path) vs the oracle."""
     w = make(torch, lib, n, k, 11 + n + k)
