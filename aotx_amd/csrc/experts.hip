@@ -17,14 +17,25 @@
  */
 #include "aotx_internal.h"
 #include "experts.h"
+#include "coherent.h"
 #include "gemv.h"
 
-#define ROUTE_THREADS 256u
+#define ROUTE_THREADS 512u
+#define ROUTE_VEC 16u            /* 16-byte router loads in flight per lane per step */
+#define ROUTE_HIDDEN_LDS 16384u  /* largest hidden staged in LDS (64 KB of floats) */
 
+/* The router of one token (one workgroup). VEC: x staged once in LDS as floats (16-byte
+ * loads), then wave w takes experts w, w + 8, ...: a lane adds the products of its 4-value
+ * pieces (piece p = lane + 64 i, in i order), with ROUTE_VEC 16-byte router loads issued
+ * before their adds, so a row costs one memory round trip, and the wave adds the lanes'
+ * sums; for rows or x not 16-byte aligned, or a hidden past ROUTE_HIDDEN_LDS, lanes take
+ * single values straight from memory. Then the softmax over every expert and the rank. */
+template <bool VEC>
 __global__ __launch_bounds__(ROUTE_THREADS) void aotx_route_kernel(
     const float *router, const unsigned short *x, const unsigned int *m_dev, unsigned int tokens,
     unsigned int hidden, unsigned int experts, unsigned int used, float *prob, unsigned int *ids)
 {
+    extern __shared__ float xs[];
     __shared__ float logit[AOTX_LAYER_EXPERTS_MAX];
     __shared__ float red[ROUTE_THREADS];
     unsigned int count = m_dev ? *m_dev : tokens;
@@ -33,10 +44,49 @@ __global__ __launch_bounds__(ROUTE_THREADS) void aotx_route_kernel(
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
     const unsigned short *xr = x + (unsigned long long)t * hidden;
+    if constexpr (VEC) {
+        const unsigned int pieces8 = hidden / 8u;
+#pragma unroll 4
+        for (unsigned int p = threadIdx.x; p < pieces8; p += ROUTE_THREADS) {
+            const aotx_u4 v = *(const aotx_u4 *)(xr + 8u * p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xs[8u * p + 2u * (unsigned int)i] = aotx_h2f((unsigned short)(v[i] & 0xffffu));
+                xs[8u * p + 2u * (unsigned int)i + 1u] = aotx_h2f((unsigned short)(v[i] >> 16));
+            }
+        }
+        __syncthreads();
+    }
     for (unsigned int e = wave; e < experts; e += ROUTE_THREADS / 64u) {
         const float *row = router + (unsigned long long)e * hidden;
         float dot = 0.0f;
-        for (unsigned int d = lane; d < hidden; d += 64u) dot += row[d] * aotx_h2f(xr[d]);
+        if constexpr (VEC) {
+            const unsigned int pieces = hidden / 4u;
+            const aotx_u4 *r4 = (const aotx_u4 *)row;
+            for (unsigned int base = 0; base < pieces; base += 64u * ROUTE_VEC) {
+                aotx_u4 rv[ROUTE_VEC];
+#pragma unroll
+                for (unsigned int i = 0; i < ROUTE_VEC; ++i) {
+                    const unsigned int pc = base + lane + 64u * i;
+                    rv[i] = r4[pc < pieces ? pc : 0u];      /* unconditional; masked below */
+                }
+#pragma unroll
+                for (unsigned int i = 0; i < ROUTE_VEC; ++i) {
+                    const unsigned int pc = base + lane + 64u * i;
+                    if (pc < pieces) {
+                        const float *xv = xs + 4u * pc;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const unsigned int w = rv[i][j];   /* a bit cast of the element
+                                                                * itself reads element 0 */
+                            dot += __uint_as_float(w) * xv[j];
+                        }
+                    }
+                }
+            }
+        } else {
+            for (unsigned int d = lane; d < hidden; d += 64u) dot += row[d] * aotx_h2f(xr[d]);
+        }
         for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
         if (lane == 0u) logit[e] = dot;
     }
@@ -75,19 +125,45 @@ __global__ __launch_bounds__(ROUTE_THREADS) void aotx_route_kernel(
     }
 }
 
-/* Slots (token * used + rank) of each expert, in slot order; one thread per expert. */
-__global__ void aotx_group_kernel(const unsigned int *ids, const unsigned int *m_dev,
-                                  unsigned int tokens, unsigned int used, unsigned int experts,
-                                  unsigned int *list, unsigned int *count, unsigned int cap)
+#define GROUP_THREADS 256u
+#define GROUP_CHUNK 4096u
+
+/* Routed (token, rank) slots grouped per expert, in slot order, the first `cap` of each
+ * expert kept and counted (one workgroup): the slots' expert ids come into LDS a chunk at a
+ * time with one round of loads, then wave w takes experts w, w + 4, ... and places 64 slots
+ * per step with a ballot and a prefix count. */
+__global__ __launch_bounds__(GROUP_THREADS) void aotx_group_kernel(
+    const unsigned int *ids, const unsigned int *m_dev, unsigned int tokens, unsigned int used,
+    unsigned int experts, unsigned int *list, unsigned int *count, unsigned int cap)
 {
-    unsigned int e = blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= experts) return;
-    unsigned int n = m_dev ? *m_dev : tokens;
-    unsigned int c = 0u;
-    for (unsigned int s = 0; s < n * used; ++s) {
-        if (ids[s] == e && c < cap) list[(unsigned long long)e * cap + c++] = s;
+    __shared__ unsigned int sid[GROUP_CHUNK];
+    __shared__ unsigned int cnt[AOTX_LAYER_EXPERTS_MAX];
+    const unsigned int n = (m_dev ? *m_dev : tokens) * used;
+    const unsigned int lane = threadIdx.x & 63u;
+    const unsigned int wave = threadIdx.x >> 6;
+    for (unsigned int e = threadIdx.x; e < experts; e += GROUP_THREADS) cnt[e] = 0u;
+    for (unsigned int base = 0u; base < n; base += GROUP_CHUNK) {
+        const unsigned int len = n - base < GROUP_CHUNK ? n - base : GROUP_CHUNK;
+        __syncthreads();
+#pragma unroll 4
+        for (unsigned int i = threadIdx.x; i < len; i += GROUP_THREADS) sid[i] = ids[base + i];
+        __syncthreads();
+        for (unsigned int e = wave; e < experts; e += GROUP_THREADS / 64u) {
+            unsigned int c = cnt[e];
+            for (unsigned int off = 0u; off < len; off += 64u) {
+                const unsigned int s = off + lane;
+                const bool match = s < len && sid[s] == e;
+                const unsigned long long mask = __ballot(match);
+                const unsigned int pos = c + (unsigned int)__popcll(mask & ((1ull << lane) - 1ull));
+                if (match && pos < cap) list[(unsigned long long)e * cap + pos] = base + s;
+                c += (unsigned int)__popcll(mask);
+            }
+            if (lane == 0u) cnt[e] = c;
+        }
     }
-    count[e] = c;
+    __syncthreads();
+    for (unsigned int e = threadIdx.x; e < experts; e += GROUP_THREADS)
+        count[e] = cnt[e] < cap ? cnt[e] : cap;
 }
 
 /* out[t][d] = sum over rank of prob * y, rank by rank, each product rounded first. */
@@ -113,7 +189,7 @@ void aotx_launch_group(const unsigned int *ids, const unsigned int *m_dev, unsig
                        unsigned int used, unsigned int experts, unsigned int *list,
                        unsigned int *count, unsigned int cap, hipStream_t s)
 {
-    hipLaunchKernelGGL(aotx_group_kernel, dim3((experts + 255u) / 256u), dim3(256), 0, s, ids, m_dev,
+    hipLaunchKernelGGL(aotx_group_kernel, dim3(1), dim3(GROUP_THREADS), 0, s, ids, m_dev,
                        tokens, used, experts, list, count, cap);
     AOTX_LAUNCH_CHECK();
 }
@@ -122,8 +198,15 @@ void aotx_launch_route(const float *router, const unsigned short *x, const unsig
                        unsigned int tokens, unsigned int hidden, unsigned int experts,
                        unsigned int used, float *prob, unsigned int *ids, hipStream_t s)
 {
-    hipLaunchKernelGGL(aotx_route_kernel, dim3(tokens), dim3(ROUTE_THREADS), 0, s, router, x,
-                       m_dev, tokens, hidden, experts, used, prob, ids);
+    const bool vec = ((unsigned long long)router & 15ull) == 0ull && ((unsigned long long)x & 15ull) == 0ull
+                  && hidden % 8u == 0u && hidden <= ROUTE_HIDDEN_LDS;
+    if (vec)
+        hipLaunchKernelGGL(aotx_route_kernel<true>, dim3(tokens), dim3(ROUTE_THREADS),
+                           (size_t)hidden * sizeof(float), s, router, x, m_dev, tokens, hidden,
+                           experts, used, prob, ids);
+    else
+        hipLaunchKernelGGL(aotx_route_kernel<false>, dim3(tokens), dim3(ROUTE_THREADS), 0, s, router,
+                           x, m_dev, tokens, hidden, experts, used, prob, ids);
     AOTX_LAUNCH_CHECK();
 }
 
@@ -131,7 +214,7 @@ int aotx_launch_expert_ffn(const aotx_expert_plan &p, const unsigned short *x,
                            const unsigned int *m_dev, unsigned int tokens,
                            const unsigned int *ids, unsigned short *act, float *y, hipStream_t s)
 {
-    hipLaunchKernelGGL(aotx_group_kernel, dim3((p.experts + 255u) / 256u), dim3(256), 0, s, ids,
+    hipLaunchKernelGGL(aotx_group_kernel, dim3(1), dim3(GROUP_THREADS), 0, s, ids,
                        m_dev, tokens, p.used, p.experts, p.list, p.count, p.cap);
     AOTX_LAUNCH_CHECK();
     /* gate + up with the gated unit, per expert; passes of 32 routed rows */

@@ -1046,6 +1046,9 @@ extern "C" unsigned long long aotx_model_buffer(unsigned int role, unsigned int 
     case 1: return (unsigned long long)h->resid;    /* residual stream, fp32 */
     case 2: return (unsigned long long)h->logits;   /* head rows, fp32 */
     case 3: return (unsigned long long)h->sel;      /* head input rows, fp16 */
+    /* routed experts, the last layer of the last pass (null without experts) */
+    case 4: return (unsigned long long)h->ecount;   /* rows per expert, u32 [experts] */
+    case 5: return (unsigned long long)h->ids;      /* experts of each token, u32 [T][used] */
     default: return 0ull;
     }
 }

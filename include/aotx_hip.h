@@ -284,8 +284,12 @@ int aotx_model_probe(unsigned int role, const int *ids, const unsigned int *offs
  * write a slot's KV pages out of band (restore from a copy, benchmarks that seat a
  * prefilled context) and then continue decoding at `position`. Returns 1 for a bad slot. */
 int aotx_model_seat(unsigned int agent, unsigned int position);
-/* Address of a role's hidden-state rows after the last norm (half [max_tokens][hidden]),
- * for checks. */
+/* Device address of one of a role's step buffers, for checks; no counterpart in the
+ * reference. which: 0 the rows after the last norm (half [max_tokens][hidden]; a 5..32-row
+ * pass in the fragment layout), 1 the residual stream (float), 2 the head's rows (float
+ * [rows][vocab]), 3 the head's input rows (half), 4 the routed rows per expert of the last
+ * layer run (u32 [experts]), 5 the experts each token chose there (u32 [tokens][used]).
+ * 0 for an unknown buffer or one the role does not have. */
 unsigned long long aotx_model_buffer(unsigned int role, unsigned int which);
 
 /* ---------------------------------------------------------------------------------------

@@ -17,9 +17,9 @@ def torch():
 
 
 @pytest.mark.parametrize("experts,used,tokens", [(8, 2, 64), (1, 1, 3), (3, 1, 7), (7, 7, 5), (64, 8, 33)])
-def test_route_vs_oracle(torch, lib, orc, experts, used, tokens):
+@pytest.mark.parametrize("hidden", [512, 100])   # 16-byte router loads; single values (hidden % 8)
+def test_route_vs_oracle(torch, lib, orc, experts, used, tokens, hidden):
     rng = np.random.default_rng(experts * 13 + tokens)
-    hidden = 512
     router = rng.normal(0, 0.05, (experts, hidden)).astype(np.float32)
     x = rng.normal(0, 1, (tokens, hidden)).astype(np.float16)
     prob = torch.zeros(tokens * experts, dtype=torch.float32, device="cuda")
@@ -52,7 +52,8 @@ def _ffn_oracle(orc, gate, up, down, E, H, F, x, prob, ids):
     return out
 
 
-@pytest.mark.parametrize("E,used,tokens", [(8, 2, 64), (4, 2, 5), (8, 2, 1)])
+# (16, 16, 300): 4800 routed slots, grouped in two chunks
+@pytest.mark.parametrize("E,used,tokens", [(8, 2, 64), (4, 2, 5), (8, 2, 1), (16, 16, 300)])
 def test_expert_ffn_vs_oracle(torch, lib, orc, E, used, tokens):
     rng = np.random.default_rng(E + tokens)
     H, F = 256, 512
