@@ -110,8 +110,11 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     unsigned int agent;
     if constexpr (QT == 1) {
         S = a.splits;
-        c = bx % S;
-        const unsigned int rest = bx / S;
+        /* chunk-major: the workgroups of one chunk index are consecutive, so they spread
+         * over every XCD whichever chunks are empty (dispatch goes round the XCDs) */
+        const unsigned int units = a.tokens * a.kv_heads;
+        c = bx / units;
+        const unsigned int rest = bx - c * units;
         kh = rest % a.kv_heads;
         t = rest / a.kv_heads;
         /* the token's position and slot are read before its row count is known (t is below
