@@ -552,8 +552,12 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
  * results pass through LDS to the same epilogues. */
 #define RGM_MB 64
 #define RGM_RT 16
-template <int MB>
-__global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
+/* XCD: the grid is one-dimensional, ordered so that the row blocks of a weight group run
+ * together on one XCD (dispatch goes round the 8 XCDs by workgroup index): they read each
+ * weight quad at about the same time, and the XCD's L2 serves all but the first read.
+ * NTL: the weights are read with nontemporal loads. */
+template <int MB, bool XCD, bool NTL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void aotx_rgemm(aotx_rgemv_args a0, unsigned int ny)
 {
     aotx_args_touch(a0);
     constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
@@ -568,10 +572,16 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
     const unsigned int r = lane & 15u, g = lane >> 4;
-    const unsigned int group = blockIdx.x;
+    unsigned int group = blockIdx.x, yb = blockIdx.y;
+    if (XCD) {
+        const unsigned int seq = blockIdx.x >> 3;           /* index on its XCD */
+        yb = seq % ny;
+        group = (seq / ny) * 8u + (blockIdx.x & 7u);
+        if (group >= a0.groups) return;
+    }
 
     aotx_rgemv_args a = a0;
-    a.m0 = a0.m0 + blockIdx.y * (unsigned int)MB;
+    a.m0 = a0.m0 + yb * (unsigned int)MB;
     unsigned int total = a0.m;
     if (a0.m_dev != nullptr) {
         const unsigned int live = rg_scalar(a0.m_dev);
@@ -615,40 +625,46 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
         const unsigned int qq_ = (Q) < qn ? (Q) : qn - 1u;                               \
         _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                  \
             const rg_u4 *src = (const rg_u4 *)(qb[t] + (unsigned long long)qq_ * 2048ull); \
-            wa[BUF][t][0] = __builtin_nontemporal_load(src);                            \
-            wa[BUF][t][1] = __builtin_nontemporal_load(src + 64);                        \
+            if (NTL) {                                                                   \
+                wa[BUF][t][0] = __builtin_nontemporal_load(src);                        \
+                wa[BUF][t][1] = __builtin_nontemporal_load(src + 64);                    \
+            } else {                                                                     \
+                wa[BUF][t][0] = src[0];                                                  \
+                wa[BUF][t][1] = src[64];                                                 \
+            }                                                                            \
             ws[BUF][t] = sb[t][(unsigned long long)qq_ * 64ull];                         \
         }                                                                                \
     } while (0)
     /* x pieces of quad Q (k is a whole number of quads: a quad past k repeats the last) */
-    rg_u4 xr[PPT];
-#define RGM_XLOAD(Q)                                                                     \
+    rg_u4 xr[2][PPT];                             /* register buffer XB = Q & 1 holds quad Q */
+#define RGM_XLOAD(XB, Q)                                                                 \
     do {                                                                                 \
         const unsigned int qx_ = ((Q) < qn ? (Q) : qn - 1u) * 128u;                      \
         _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
-            xr[i] = *(const rg_u4 *)(a.x + xoff[i] + qx_);                               \
+            xr[XB][i] = *(const rg_u4 *)(a.x + xoff[i] + qx_);                           \
     } while (0)
-#define RGM_XSTORE(Q)                                                                    \
+#define RGM_XSTORE(XB, Q)                                                                \
     do {                                                                                 \
         unsigned short *xb_ = xl + ((Q) & 1u) * (unsigned int)(MB * XS) + xrow0 * XS + xpc * 8u; \
         _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
             *(rg_u4 *)(xb_ + (unsigned int)i * RSTEP * XS) =                             \
-                xrow0 + (unsigned int)i * RSTEP < mrows ? xr[i] : (rg_u4){0u, 0u, 0u, 0u}; \
+                xrow0 + (unsigned int)i * RSTEP < mrows ? xr[XB][i] : (rg_u4){0u, 0u, 0u, 0u}; \
     } while (0)
 
     /* Quad q is computed from LDS x buffer q & 1 and weight buffer q & 1. Its step first
-     * requests quad q + 1's x and quad q + 2's weights (x first: the store of x then waits
-     * for nothing issued after it), computes, and stores quad q + 1's x. */
-    RGM_XLOAD(0u);
+     * requests quad q + 2's x (into the registers quad q's x left) and, after the MFMAs,
+     * quad q + 2's weights, then stores quad q + 1's x, requested a whole step earlier. */
+    RGM_XLOAD(0, 0u);
+    RGM_XLOAD(1, 1u);
     RGM_WLOAD(0, 0u);
     RGM_WLOAD(1, 1u);
-    RGM_XSTORE(0u);
+    RGM_XSTORE(0, 0u);
     rg_sync_lds();
     for (unsigned int q = 0; q < qn; q += 2u) {
 #define RGM_STEP(BUF, QQ)                                                                \
     do {                                                                                 \
         const unsigned int qc_ = (QQ);                                                   \
-        RGM_XLOAD(qc_ + 1u);                                                             \
+        RGM_XLOAD(BUF, qc_ + 2u);                                                        \
         __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */ \
         const unsigned short *xb = xl + (qc_ & 1u) * (unsigned int)(MB * XS);           \
         const unsigned int sq_ = qc_ < qn ? 0xffffffffu : 0u;                            \
@@ -677,7 +693,7 @@ __global__ __launch_bounds__(512) void aotx_rgemm(aotx_rgemv_args a0)
         __builtin_amdgcn_sched_barrier(0);     /* the MFMAs before the new loads */      \
         RGM_WLOAD(BUF, qc_ + 2u);                                                        \
         __builtin_amdgcn_sched_barrier(0);                                               \
-        RGM_XSTORE(qc_ + 1u);                                                            \
+        RGM_XSTORE(BUF ^ 1, qc_ + 1u);                                                   \
         rg_sync_lds();                                                                   \
     } while (0)
         RGM_STEP(0, q);
@@ -943,10 +959,22 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             fprintf(stderr, "aotx: the GEMM takes fp16 x of direct rows only\n");
             exit(1);
         }
-        const dim3 grid(a.groups, (a.m + RGM_MB - 1u) / RGM_MB);
+        const unsigned int ny = (a.m + RGM_MB - 1u) / RGM_MB;
         const size_t x = 2u * RGM_MB * (128u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
         const size_t lds = x > res ? x : res;
-        hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), grid, dim3(512), lds, s, a);
+        static const int mode = [] {
+            /* measurement sweeps (AOTX_GEMM_MODE): bit 1 the XCD order, bit 0 plain weight
+             * loads; the default 3 measured fastest (512 rows: 19.87 ms per step at 0) */
+            const char *e = getenv("AOTX_GEMM_MODE");
+            return e != nullptr ? atoi(e) & 3 : 3;
+        }();
+        const dim3 g2(a.groups, ny), g1(((a.groups + 7u) / 8u) * 8u * ny);
+        switch (mode) {
+        case 0: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, true>), g2, dim3(512), lds, s, a, ny); break;
+        case 1: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, false>), g2, dim3(512), lds, s, a, ny); break;
+        case 2: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, true>), g1, dim3(512), lds, s, a, ny); break;
+        default: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false>), g1, dim3(512), lds, s, a, ny); break;
+        }
         AOTX_LAUNCH_CHECK();
         return;
     }
