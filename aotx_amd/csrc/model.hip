@@ -251,7 +251,8 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
         aotx_rgemv_args a;
         const int refused = tmpl.xmode == AOTX_X_FRAG
             ? aotx_rgemv_plan_frag(&a, w, rows, nseg, k, epi, mt)
-            : aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt);
+            : tmpl.expert_stride != 0ull ? aotx_rgemv_plan_routed(&a, w, rows, nseg, k, epi, mt)
+                                         : aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt);
         if (refused != 0) {
             fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);
             exit(1);
@@ -721,13 +722,15 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
             unsigned int r1[1] = {d->hidden};
             if (aotx_rgemv_plan(&a, w1, r1, 1u, (unsigned int)wide, AOTX_EPI_RESID, mt) == 0)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
-            if (aotx_rgemv_plan(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt) == 0) {
+            if ((d->expert_count != 0u ? aotx_rgemv_plan_routed(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt)
+                                       : aotx_rgemv_plan(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt)) == 0) {
                 a.expert_stride = d->expert_count != 0u ? 1ull : 0ull;
                 a.experts = E;
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
             }
             unsigned int r2[2] = {d->ffn, d->ffn};
-            if (aotx_rgemv_plan(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt) == 0) {
+            if ((d->expert_count != 0u ? aotx_rgemv_plan_routed(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt)
+                                       : aotx_rgemv_plan(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt)) == 0) {
                 a.expert_stride = d->expert_count != 0u ? 1ull : 0ull;
                 a.experts = E;
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);

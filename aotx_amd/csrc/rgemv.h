@@ -100,6 +100,10 @@ struct aotx_rgemv_args {
 #define AOTX_RGEMM_ROWS 512u
 int aotx_rgemv_plan(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                     unsigned int nseg, unsigned int k, int epi, unsigned int mt);
+/* The same for a routed-expert product (one workgroup row per expert, x rows through the
+ * expert's row list): its wide passes may take larger tile groups. */
+int aotx_rgemv_plan_routed(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
+                           unsigned int nseg, unsigned int k, int epi, unsigned int mt);
 /* Plan a product whose x is in the fragment layout (AOTX_X_FRAG): a dense product of at
  * most 32 rows (one pass, m0 = 0) over tensors whose k is a multiple of 128; 1 when
  * refused. */
