@@ -146,17 +146,31 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
         kh = bx % a.kv_heads;
         t = bx / a.kv_heads;
         if (t >= tokens) return;
-        const unsigned int agent0 = a.agent[t], pos0 = a.pos[t];
-        if (t != 0u && a.agent[t - 1u] == agent0 && pos0 % QT != 0u) return;
-        while (nq < (unsigned int)QT && t + nq < tokens && a.agent[t + nq] == agent0
-               && a.pos[t + nq] % QT != 0u)
-            ++nq;
-        n = a.pos[t + nq - 1u] + 1u;
+        /* one round trip for every word the test needs: lane i holds the slot and position
+         * of token t - 1 + i (i <= QT; lane 0 a token before the batch, or one past it, holds
+         * no slot: all ones) */
+        const unsigned int ti = t + lane - 1u;
+        unsigned int ag = 0xFFFFFFFFu, ps = 0u;
+        if (lane <= (unsigned int)QT && (lane != 0u || t != 0u) && ti < tokens) {
+            ag = a.agent[ti];
+            ps = a.pos[ti];
+        }
+        const unsigned int agent0 = (unsigned int)__shfl((int)ag, 1, 64);
+        const unsigned int pos0 = (unsigned int)__shfl((int)ps, 1, 64);
+        const unsigned int agent_prev = (unsigned int)__shfl((int)ag, 0, 64);
+        if (t != 0u && agent_prev == agent0 && pos0 % QT != 0u) return;
+        /* the run: tokens t + 1 .. of the same slot off a multiple of QT (lanes 2 ..) */
+        const bool more = lane >= 2u && lane <= (unsigned int)QT && ag == agent0 && ps % QT != 0u;
+        const unsigned long long run = (unsigned long long)__ballot(more) >> 2;
+        nq = 1u + (unsigned int)__builtin_ctzll(~run);
+        if (nq > (unsigned int)QT) nq = QT;
+        n = (unsigned int)__shfl((int)ps, (int)nq, 64) + 1u;
         agent = agent0;
         p0 = 0u;
         p1 = n;
         /* this lane's column: query r / G; a column with no query sees position 0 only */
-        plim = r / (unsigned int)G < nq ? a.pos[t + r / (unsigned int)G] + 1u : 1u;
+        const unsigned int qpos = (unsigned int)__shfl((int)ps, (int)(r / (unsigned int)G) + 1, 64);
+        plim = r / (unsigned int)G < nq ? qpos + 1u : 1u;
     }
     const unsigned int nblk = (p1 - p0 + 15u) / 16u;
     const unsigned int per = (nblk + W - 1u) / W;
