@@ -42,6 +42,14 @@ __global__ __launch_bounds__(64 * W) void aotx_attend_piece(aotx_attn_args a)
     aotx_attend_body<D, G, W, 16 / G>(a, blockIdx.x);
 }
 
+/* Prompt pieces one wave each (aotx_attend_runs). */
+template <int D, int G, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_run(aotx_attn_args a)
+{
+    aotx_args_touch(a);
+    aotx_attend_runs<D, G, W>(a, blockIdx.x);
+}
+
 /* ---------------------------------------------------------------------------------------
  * Host side
  * ------------------------------------------------------------------------------------- */
@@ -130,10 +138,17 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
         /* more tokens than sequence slots: a batch with prompt pieces. One workgroup per
          * token and KV head; the ones that lead a run of queries compute it. */
         a.splits = 1u;
+        /* AOTX_ATTN_RUNS=0: the piece per workgroup, for comparison */
+        static const bool runs = [] {
+            const char *v = getenv("AOTX_ATTN_RUNS");
+            return !(v != nullptr && v[0] == '0');
+        }();
         dim3 grid(tokens * kv_heads);
+        const dim3 rgrid((tokens + AOTX_RUN_RANGE - 1u) / AOTX_RUN_RANGE * kv_heads);
 #define AOTX_PIECE_GO(DD, GG)                                                              \
         do {                                                                               \
-            hipLaunchKernelGGL((aotx_attend_piece<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
+            if (runs) hipLaunchKernelGGL((aotx_attend_run<DD, GG, 4>), rgrid, dim3(256), 0, stream, a); \
+            else hipLaunchKernelGGL((aotx_attend_piece<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
             AOTX_LAUNCH_CHECK();                                                           \
         } while (0)
         if (head_dim == 128u) {

@@ -72,6 +72,85 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
     return (chunk + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN * ATTN_CHUNK_ALIGN;
 }
 
+/* The block loop shared by the attention bodies. They expect, in scope: a, kv, agent, b1,
+ * lane, r, g, kbyte, vbyte, wbase, pages, kr, vr, absent, CPOL, KK, VP, NS, VS, D, qb, o,
+ * mrun, lrun, missing, scale, p0, plim and vw (this wave's LDS value slot).
+ * MMA_WINDOW(B0): the page addresses of blocks B0 .. B0 + 63 (one per lane).
+ * MMA_LOAD(BUF, B): block B's keys and values into register buffer BUF.
+ * MMA_COMPUTE(BUF, B): block B's scores, online softmax and P . V. */
+#define MMA_WINDOW(B0)                                                                      \
+    do {                                                                                    \
+        wbase = (B0);                                                                       \
+        unsigned int bl = wbase + lane;                                                     \
+        pages = bl < b1 ? (unsigned long long)aotx_kvl_block(a.shape, kv, agent, a.layer, bl * 16u) \
+                        : 0ull;                                                             \
+    } while (0)
+#define MMA_LOAD(BUF, B)                                                                    \
+    do {                                                                                    \
+        if ((B) - wbase >= 64u) MMA_WINDOW(B);                                              \
+        unsigned long long pb = __shfl(pages, (int)((B) - wbase), 64);                     \
+        pb = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb >> 32)) << 32) \
+           | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb); \
+        absent[BUF] = pb == 0ull;                                                           \
+        __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
+            (void *)pb, (short)0, absent[BUF] ? 0 : (int)a.shape.block_bytes, 0x00020000);  \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            kr[BUF][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + kk * 64, 0, CPOL); \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u)                                      \
+            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * 1024, 0, CPOL); \
+    } while (0)
+
+#define MMA_COMPUTE(BUF, B)                                                                 \
+    do {                                                                                    \
+        if (absent[BUF]) missing = 1;                                                       \
+        aotx_f4a sc = {0.0f, 0.0f, 0.0f, 0.0f};                                             \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                    \
+                __builtin_bit_cast(aotx_h8a, kr[BUF][kk]), qb[kk], sc, 0, 0, 0);             \
+        /* the block's values into this wave's LDS slot (row-major, padded rows) */         \
+        _Pragma("unroll") for (int u = 0; u < VP; ++u) {                                    \
+            const unsigned int piece = (unsigned int)u * 64u + lane;                        \
+            *(aotx_u4a *)(vw + (piece / (D / 8)) * VS + (piece % (D / 8)) * 8u) = vr[BUF][u]; \
+        }                                                                                   \
+        float pr[4];                                                                        \
+        float mb = -INFINITY;                                                               \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
+            const bool ok = p >= p0 && p < plim && !absent[BUF];                            \
+            pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
+            mb = fmaxf(mb, pr[i]);                                                          \
+        }                                                                                   \
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
+        const float mnew = fmaxf(mrun, mb);                                                 \
+        /* 0 from -inf; a column with no position yet keeps its (empty) sums */           \
+        const float shift = mnew == -INFINITY ? 1.0f : aotx_exp2(mrun - mnew);              \
+        mrun = mnew;                                                                        \
+        aotx_h4a pa;                                                                        \
+        float mass = 0.0f;                                                                  \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const _Float16 ph = mnew == -INFINITY ? (_Float16)0.0f                          \
+                              : (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
+            pa[i] = ph;                                                                     \
+            mass += (float)ph;                                                              \
+        }                                                                                   \
+        lrun = lrun * shift + mass;                                                         \
+        /* the accumulators of heads 4g + i take those heads' shifts */                     \
+        if (__any(shift != 1.0f)) {                                                         \
+            float sh[4];                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) sh[i] = __shfl(shift, (int)(4u * g) + i, 64); \
+            _Pragma("unroll") for (int cc = 0; cc < NS; ++cc)                               \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
+        }                                                                                   \
+        _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
+            const unsigned short *col = vw + (4u * g) * VS + 16u * (unsigned int)cc + r;    \
+            aotx_h4a vb;                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                   \
+                vb[i] = __builtin_bit_cast(_Float16, col[(unsigned int)i * VS]);            \
+            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[cc], 0, 0, 0);          \
+        }                                                                                   \
+    } while (0)
+
 /* One workgroup = W waves = one (token, KV head, context chunk); each wave takes a
  * contiguous run of 16-position layout blocks. Per wave and block, on the matrix cores:
  *   - scores S[pos][head] = K . q^T: one v_mfma_f32_16x16x32_f16 per 32 of d, keys as the A
@@ -204,79 +283,6 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     bool absent[2];
     unsigned long long pages = 0ull;
     unsigned int wbase = b0;
-#define MMA_WINDOW(B0)                                                                      \
-    do {                                                                                    \
-        wbase = (B0);                                                                       \
-        unsigned int bl = wbase + lane;                                                     \
-        pages = bl < b1 ? (unsigned long long)aotx_kvl_block(a.shape, kv, agent, a.layer, bl * 16u) \
-                        : 0ull;                                                             \
-    } while (0)
-#define MMA_LOAD(BUF, B)                                                                    \
-    do {                                                                                    \
-        if ((B) - wbase >= 64u) MMA_WINDOW(B);                                              \
-        unsigned long long pb = __shfl(pages, (int)((B) - wbase), 64);                     \
-        pb = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb >> 32)) << 32) \
-           | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb); \
-        absent[BUF] = pb == 0ull;                                                           \
-        __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(                      \
-            (void *)pb, (short)0, absent[BUF] ? 0 : (int)a.shape.block_bytes, 0x00020000);  \
-        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
-            kr[BUF][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs, kbyte + kk * 64, 0, CPOL); \
-        _Pragma("unroll") for (int u = 0; u < VP; ++u)                                      \
-            vr[BUF][u] = __builtin_amdgcn_raw_buffer_load_b128(rs, vbyte + u * 1024, 0, CPOL); \
-    } while (0)
-
-#define MMA_COMPUTE(BUF, B)                                                                 \
-    do {                                                                                    \
-        if (absent[BUF]) missing = 1;                                                       \
-        aotx_f4a sc = {0.0f, 0.0f, 0.0f, 0.0f};                                             \
-        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                    \
-                __builtin_bit_cast(aotx_h8a, kr[BUF][kk]), qb[kk], sc, 0, 0, 0);             \
-        /* the block's values into this wave's LDS slot (row-major, padded rows) */         \
-        _Pragma("unroll") for (int u = 0; u < VP; ++u) {                                    \
-            const unsigned int piece = (unsigned int)u * 64u + lane;                        \
-            *(aotx_u4a *)(vw + (piece / (D / 8)) * VS + (piece % (D / 8)) * 8u) = vr[BUF][u]; \
-        }                                                                                   \
-        float pr[4];                                                                        \
-        float mb = -INFINITY;                                                               \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
-            const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
-            const bool ok = p >= p0 && p < plim && !absent[BUF];                            \
-            pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
-            mb = fmaxf(mb, pr[i]);                                                          \
-        }                                                                                   \
-        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
-        const float mnew = fmaxf(mrun, mb);                                                 \
-        /* 0 from -inf; a column with no position yet keeps its (empty) sums */           \
-        const float shift = mnew == -INFINITY ? 1.0f : aotx_exp2(mrun - mnew);              \
-        mrun = mnew;                                                                        \
-        aotx_h4a pa;                                                                        \
-        float mass = 0.0f;                                                                  \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
-            const _Float16 ph = mnew == -INFINITY ? (_Float16)0.0f                          \
-                              : (_Float16)aotx_exp2(pr[i] - mnew);   /* 0 when masked */    \
-            pa[i] = ph;                                                                     \
-            mass += (float)ph;                                                              \
-        }                                                                                   \
-        lrun = lrun * shift + mass;                                                         \
-        /* the accumulators of heads 4g + i take those heads' shifts */                     \
-        if (__any(shift != 1.0f)) {                                                         \
-            float sh[4];                                                                    \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i) sh[i] = __shfl(shift, (int)(4u * g) + i, 64); \
-            _Pragma("unroll") for (int cc = 0; cc < NS; ++cc)                               \
-                _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
-        }                                                                                   \
-        _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
-            const unsigned short *col = vw + (4u * g) * VS + 16u * (unsigned int)cc + r;    \
-            aotx_h4a vb;                                                                    \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                   \
-                vb[i] = __builtin_bit_cast(_Float16, col[(unsigned int)i * VS]);            \
-            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[cc], 0, 0, 0);          \
-        }                                                                                   \
-    } while (0)
-
     /* The next block's loads are issued on every step: past the wave's last block the page
      * address is zero and the loads go through a zero-size resource (they return zeros
      * and touch no memory; that buffer is never computed). With a load on one path only,
@@ -297,10 +303,6 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
             if (b >= b1) break;
         }
     }
-#undef MMA_WINDOW
-#undef MMA_LOAD
-#undef MMA_COMPUTE
-
     /* a head's mass over its 4 lane groups */
     lrun += __shfl_xor(lrun, 16, 64);
     lrun += __shfl_xor(lrun, 32, 64);
@@ -403,5 +405,137 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
             co_store2h(a.out + aotx_attn_out_at(a, t, kh * G + j, e, D), aotx_f2h(v), aotx_f2h(v1));
     }
 }
+
+/* Prompt pieces one wave each: a workgroup of W waves takes the pieces led inside its
+ * range of AOTX_RUN_RANGE tokens (a piece: up to QT = 16 / G consecutive queries of one
+ * sequence, led by a token that starts its sequence's run in the batch or sits at a
+ * multiple of QT, as in the decode body's prompt pieces), in rank order, wave k taking
+ * pieces k, k + W, ... A wave runs one ordered pass of online softmax over every block its
+ * queries see (the reference's single pass per query, cuda/model/attention.cu:22-154) and
+ * writes their outputs: no merge. The waves of one sequence read the same blocks at about
+ * the same time, which the caches serve. */
+#define AOTX_RUN_RANGE 16u
+template <int D, int G, int W>
+static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a, unsigned int bx)
+{
+    constexpr int QT = 16 / G;
+    constexpr int KK = D / 32;
+    constexpr int VP = D / 32;
+    constexpr int NS = D / 16;
+    constexpr int VS = D + 8;
+    constexpr unsigned int RANGE = AOTX_RUN_RANGE;
+    static_assert(RANGE + QT <= 64u, "one lane per token word");
+    __shared__ __attribute__((aligned(16))) unsigned short vl[W][16 * VS];
+
+    const unsigned int lane = threadIdx.x & 63u;
+    const unsigned int wave = threadIdx.x >> 6;
+    const unsigned int r = lane & 15u, g = lane >> 4;
+    const unsigned int counted = aotx_attn_scalar(a.m_dev != nullptr ? a.m_dev : a.pos);
+    unsigned int tokens = a.m_dev != nullptr ? counted : a.tokens;
+    if (tokens > a.tokens) tokens = a.tokens;
+    const unsigned int kh = bx % a.kv_heads;
+    const unsigned int r0 = (bx / a.kv_heads) * RANGE;
+    if (r0 >= tokens) return;
+    /* one round trip: lane i holds the slot and position of token r0 - 1 + i (a token
+     * before the batch or past it holds no slot: all ones) */
+    const unsigned int ti = r0 + lane - 1u;
+    unsigned int ag = 0xFFFFFFFFu, ps = 0u;
+    if (lane < RANGE + (unsigned int)QT && (lane != 0u || r0 != 0u) && ti < tokens) {
+        ag = a.agent[ti];
+        ps = a.pos[ti];
+    }
+    const unsigned int ag_prev = (unsigned int)__shfl((int)ag, (int)((lane - 1u) & 63u), 64);
+    const bool lead = lane >= 1u && lane <= RANGE && ti < tokens
+                   && (ag != ag_prev || ps % (unsigned int)QT == 0u);
+    unsigned long long leaders = (unsigned long long)__ballot(lead) >> 1;   /* bit j: token r0 + j */
+
+    const aotx_kv_table *kv = &a.state->kv;
+    const float scale = 1.4426950408889634f / sqrtf((float)D);
+    const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + r) * D + 8u * g) * 2u;
+    const unsigned int vbyte = ((a.kv_heads + kh) * AOTX_KVL_BLOCK * D + lane * 8u) * 2u;
+    unsigned short *vw = vl[wave];
+    constexpr int CPOL = 0;
+
+    for (unsigned int rank = 0; leaders != 0ull; ++rank) {
+        const unsigned int j = (unsigned int)__builtin_ctzll(leaders);
+        leaders &= leaders - 1ull;
+        if (rank % (unsigned int)W != wave) continue;
+        /* the piece led by token t = r0 + j (lane j + 1): the next tokens of its slot off a
+         * multiple of QT, up to QT in all */
+        const unsigned int lead_lane = j + 1u;
+        const unsigned int t = r0 + j;
+        const unsigned int agent = (unsigned int)__shfl((int)ag, (int)lead_lane, 64);
+        const bool cont = lane > lead_lane && lane < lead_lane + (unsigned int)QT && ag == agent
+                       && ps % (unsigned int)QT != 0u;
+        const unsigned long long cm = (unsigned long long)__ballot(cont) >> (lead_lane + 1u);
+        unsigned int nq = 1u + (unsigned int)__builtin_ctzll(~cm);
+        if (nq > (unsigned int)QT) nq = QT;
+        const unsigned int n = (unsigned int)__shfl((int)ps, (int)(lead_lane + nq - 1u), 64) + 1u;
+        /* this lane's column: query r / G; a column with no query sees position 0 only */
+        const unsigned int qpos = (unsigned int)__shfl((int)ps, (int)(lead_lane + r / (unsigned int)G), 64);
+        const unsigned int plim = r / (unsigned int)G < nq ? qpos + 1u : 1u;
+        const unsigned int p0 = 0u;
+        const unsigned int b0 = 0u, b1 = (n + 15u) / 16u;
+
+        aotx_h8a qb[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            aotx_u4a w = {0u, 0u, 0u, 0u};
+            const unsigned int qi = r / (unsigned int)G, hh = r % (unsigned int)G;
+            if (qi < nq)
+                w = co_load4(a.q + ((unsigned long long)(t + qi) * a.heads + kh * G + hh) * D
+                                 + 32 * kk + 8 * g);
+            qb[kk] = __builtin_bit_cast(aotx_h8a, w);
+        }
+        float mrun = -INFINITY, lrun = 0.0f;
+        aotx_f4a o[NS];
+#pragma unroll
+        for (int cc = 0; cc < NS; ++cc) o[cc] = (aotx_f4a){0.0f, 0.0f, 0.0f, 0.0f};
+        int missing = 0;
+        aotx_u4a kr[2][KK], vr[2][VP];
+        bool absent[2];
+        unsigned long long pages = 0ull;
+        unsigned int wbase = b0;
+        {
+            unsigned int b = b0;
+            MMA_WINDOW(b0);
+            MMA_LOAD(0, b);
+            for (;;) {
+                MMA_LOAD(1, b + 1u);
+                MMA_COMPUTE(0, b);
+                b += 1u;
+                if (b >= b1) break;
+                MMA_LOAD(0, b + 1u);
+                MMA_COMPUTE(1, b);
+                b += 1u;
+                if (b >= b1) break;
+            }
+        }
+        /* a head's mass over its 4 lane groups; column c's mass sits in lane c */
+        lrun += __shfl_xor(lrun, 16, 64);
+        lrun += __shfl_xor(lrun, 32, 64);
+        missing = __any(missing);
+        if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned int col = 4u * g + (unsigned int)i;
+            const float l = __shfl(lrun, (int)col, 64);
+            const float back = !missing && l > 0.0f ? 1.0f / l : 0.0f;
+            const unsigned int qc = col / (unsigned int)G, hc = col % (unsigned int)G;
+#pragma unroll
+            for (int cc = 0; cc < NS; ++cc) {
+                const float v = o[cc][i] * back;
+                const float v1 = __shfl_down(v, 1, 64);
+                if (qc < nq && (r & 1u) == 0u)
+                    co_store2h(a.out + aotx_attn_out_at(a, t + qc, kh * G + hc, 16u * cc + r, D),
+                               aotx_f2h(v), aotx_f2h(v1));
+            }
+        }
+    }
+}
+
+#undef MMA_WINDOW
+#undef MMA_LOAD
+#undef MMA_COMPUTE
 
 #endif

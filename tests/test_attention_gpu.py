@@ -186,17 +186,25 @@ def test_kv_release_and_reuse(torch, lib):
         lib.aotx_kv_close(ctypes.byref(m))
 
 
+# (slot, cached positions before the piece, piece length)
+_PIECES = [(3, 0, 57), (9, 13, 30), (21, 0, 1), (40, 301, 49), (5, 7, 3), (63, 1000, 1)]
+# 20 decode rows side by side (a 16-token range of the launch leads 16 pieces, so each
+# wave takes several), then a prompt
+_SINGLES = [(10 + i, 5 * i + 2, 1) for i in range(20)] + [(50, 3, 117)]
+
+
+@pytest.mark.parametrize("layout", ["pieces", "singles"])
 @pytest.mark.parametrize("heads,kvh,d", [(32, 8, 128), (16, 2, 64), (8, 8, 64)])
-def test_attend_prompt_pieces_vs_oracle(torch, lib, orc, heads, kvh, d):
+def test_attend_prompt_pieces_vs_oracle(torch, lib, orc, heads, kvh, d, layout):
     """A launch of 128 tokens or more (prompt pieces: more tokens than sequence slots) runs
-    the piece kernel, whose workgroups take 16 / G consecutive queries of one sequence on a
-    single read of their keys: pieces that start mid-cache at positions that are not
-    multiples of 16 / G, a run cut by the next sequence, single decode rows, causal limits
-    per query; every (token, head) vs the oracle's online softmax at its own position."""
+    the piece kernel, where one wave takes up to 16 / G consecutive queries of one sequence
+    on a single pass over their keys: pieces that start mid-cache at positions that are
+    not multiples of 16 / G, a run cut by the next sequence, single decode rows (many in
+    one workgroup's range), causal limits per query; every (token, head) vs the oracle's
+    online softmax at its own position."""
     layers, layer = 2, 0
     rng = np.random.default_rng(heads + kvh + d)
-    # (slot, cached positions before the piece, piece length)
-    pieces = [(3, 0, 57), (9, 13, 30), (21, 0, 1), (40, 301, 49), (5, 7, 3), (63, 1000, 1)]
+    pieces = _PIECES if layout == "pieces" else _SINGLES
     contexts = [c + n for _, c, n in pieces]
     slots = [s for s, _, _ in pieces]
     m = _open_pool(lib, 256)
