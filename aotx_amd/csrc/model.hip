@@ -267,8 +267,7 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
                 exit(1);
             }
             a.partial = h->gemv_partial;
-            const unsigned int e = a.expert_stride != 0ull ? a.experts : 1u;
-            if (e * a.groups > AOTX_GEMV_COUNTS) {
+            if (aotx_rgemv_count_words(a) > AOTX_GEMV_COUNTS) {
                 fprintf(stderr, "aotx: split counters exceed the planned buffer\n");
                 exit(1);
             }
@@ -748,6 +747,21 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
             if (aotx_rgemv_plan_frag(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt) == 0)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
             if (aotx_rgemv_plan_frag(&a, w1, rv, 1u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+        }
+        /* the GEMM passes (256 rows and more) of the dense products */
+        for (unsigned int mt = 256u; mt <= AOTX_RGEMM_ROWS && mt <= cap; mt += 64u) {
+            aotx_rgemv_args a;
+            unsigned int r3[3] = {(unsigned int)wide, (unsigned int)narrow, (unsigned int)narrow};
+            unsigned int r1[1] = {d->hidden};
+            unsigned int r2[2] = {d->ffn, d->ffn};
+            if (aotx_rgemv_plan(&a, w3, r3, 3u, d->hidden, AOTX_EPI_F32, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan(&a, w1, r1, 1u, (unsigned int)wide, AOTX_EPI_RESID, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan(&a, w1, r1, 1u, d->ffn, AOTX_EPI_RESID, mt) == 0)
+                gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
+            if (aotx_rgemv_plan(&a, w2, r2, 2u, d->hidden, AOTX_EPI_SWIGLU, mt) == 0)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
         }
     }

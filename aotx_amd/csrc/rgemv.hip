@@ -572,11 +572,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
     const unsigned int r = lane & 15u, g = lane >> 4;
-    unsigned int group = blockIdx.x, yb = blockIdx.y;
+    /* the row block runs fastest, then the k split, then the weight group */
+    unsigned int group = blockIdx.x, yb = blockIdx.y % ny, split = blockIdx.y / ny;
     if (XCD) {
         const unsigned int seq = blockIdx.x >> 3;           /* index on its XCD */
         yb = seq % ny;
-        group = (seq / ny) * 8u + (blockIdx.x & 7u);
+        const unsigned int rest = seq / ny;
+        split = rest % a0.splits;
+        group = (rest / a0.splits) * 8u + (blockIdx.x & 7u);
         if (group >= a0.groups) return;
     }
 
@@ -618,7 +621,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
 
     rg_u4 wa[2][2][2];
     unsigned int ws[2][2];
-    const unsigned int qn = a.qn;
+    /* this split's quads [qb0, qn) */
+    const unsigned int qb0 = split * a.qps;
+    const unsigned int qn = qb0 + a.qps < a.qn ? qb0 + a.qps : a.qn;
     /* every call issues the same loads (a quad past k repeats the last: never computed) */
 #define RGM_WLOAD(BUF, Q)                                                                \
     do {                                                                                 \
@@ -654,13 +659,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     /* Quad q is computed from LDS x buffer q & 1 and weight buffer q & 1. Its step first
      * requests quad q + 2's x (into the registers quad q's x left) and, after the MFMAs,
      * quad q + 2's weights, then stores quad q + 1's x, requested a whole step earlier. */
-    RGM_XLOAD(0, 0u);
-    RGM_XLOAD(1, 1u);
-    RGM_WLOAD(0, 0u);
-    RGM_WLOAD(1, 1u);
-    RGM_XSTORE(0, 0u);
+    RGM_XLOAD(0, qb0);
+    RGM_XLOAD(1, qb0 + 1u);
+    RGM_WLOAD(0, qb0);
+    RGM_WLOAD(1, qb0 + 1u);
+    RGM_XSTORE(0, qb0);
     rg_sync_lds();
-    for (unsigned int q = 0; q < qn; q += 2u) {
+    for (unsigned int q = qb0; q < qn; q += 2u) {
 #define RGM_STEP(BUF, QQ)                                                                \
     do {                                                                                 \
         const unsigned int qc_ = (QQ);                                                   \
@@ -716,11 +721,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
                 out[((wave * 2u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i) * MB
                     + (unsigned int)c * 16u + r] = acc[t][c][i];
     __syncthreads();
+    if (a.splits > 1u) {
+        /* the last split of (row block, group) to finish adds the splits in order */
+        __shared__ unsigned int last;
+        if (!rg_split_merge<NT>(a, out, RT * 16u * MB, yb, group, split, &last)) return;
+    }
     if (a.row_ss != nullptr) {
         __shared__ float rs[MB];
         rg_row_scale<MB, NT>(a, out, RT * 16u, mrows, rs);
     }
-    rg_epilogue<MB, NT>(a, out, group, RT, mrows, nullptr);
+    rg_epilogue<MB, NT, RT>(a, out, group, RT, mrows, nullptr);
 }
 
 /* ---- host ---------------------------------------------------------------------------- */
@@ -798,8 +808,20 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
         a->nw = 8u;
         a->groups = epi == AOTX_EPI_SWIGLU ? ((unsigned int)aotx_q8r_tiles(rows[0]) + 7u) / 8u
                                            : (tiles + 15u) / 16u;
-        a->splits = 1u;
-        a->qps = a->qn;
+        /* k split while the launch stays within one workgroup per CU and a split keeps 8
+         * quads: a workgroup's time is its k length, and a second workgroup on a CU shares
+         * its VALU and matrix cores (AOTX_GEMM_SPLIT caps the split for measurement sweeps) */
+        static const unsigned int split_cap = [] {
+            const char *e = getenv("AOTX_GEMM_SPLIT");
+            const unsigned int v = e != nullptr ? (unsigned int)atoi(e) : 0u;
+            return v != 0u ? v : 64u;
+        }();
+        const unsigned int ny = (mt + 63u) / 64u;
+        unsigned int sp = 1u;
+        while (sp * 2u <= split_cap && a->groups * ny * sp * 2u <= 256u && a->qn / (sp * 2u) >= 8u)
+            sp *= 2u;
+        a->qps = (a->qn + sp - 1u) / sp;
+        a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
     }
     /* 5 to 32 rows: the wide kernel. With 32 batch columns per MFMA it wastes matrix-core
@@ -928,8 +950,16 @@ int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigne
 
 size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
 {
+    if (a.splits <= 1u) return 0u;
+    if (a.gemm) return (size_t)aotx_rgemv_count_words(a) * a.splits * RGM_RT * 16u * RGM_MB * sizeof(float);
     size_t e = a.expert_stride != 0ull ? a.experts : 1u;
-    return a.splits > 1u ? e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float) : 0u;
+    return e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float);
+}
+
+unsigned int aotx_rgemv_count_words(const aotx_rgemv_args &a)
+{
+    if (a.gemm) return a.groups * ((a.m + RGM_MB - 1u) / RGM_MB);
+    return (a.expert_stride != 0ull ? a.experts : 1u) * a.groups;
 }
 
 template <int MT, int RT, int PD>
@@ -961,12 +991,12 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL, aotx_rgemv_partial_bytes(a));
     }
     if (a.splits > 1u && a.count == nullptr) {
-        const size_t e = a.expert_stride != 0ull ? a.experts : 1u;
-        a.count = (unsigned int *)aotx_scratch(AOTX_SCRATCH_GEMV_COUNT, e * a.groups * sizeof(unsigned int));
+        a.count = (unsigned int *)aotx_scratch(AOTX_SCRATCH_GEMV_COUNT,
+                                               (size_t)aotx_rgemv_count_words(a) * sizeof(unsigned int));
     }
     if (a.gemm) {
         if (a.xmode != AOTX_X_F16 || a.expert_stride != 0ull || a.list != nullptr
-            || a.xrow != nullptr || a.splits != 1u) {
+            || a.xrow != nullptr || (a.splits > 1u && (a.partial == nullptr || a.count == nullptr))) {
             fprintf(stderr, "aotx: the GEMM takes fp16 x of direct rows only\n");
             exit(1);
         }
@@ -979,7 +1009,7 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             const char *e = getenv("AOTX_GEMM_MODE");
             return e != nullptr ? atoi(e) & 3 : 3;
         }();
-        const dim3 g2(a.groups, ny), g1(((a.groups + 7u) / 8u) * 8u * ny);
+        const dim3 g2(a.groups, ny * a.splits), g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
         switch (mode) {
         case 0: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, true>), g2, dim3(512), lds, s, a, ny); break;
         case 1: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, false>), g2, dim3(512), lds, s, a, ny); break;

@@ -240,7 +240,7 @@ static __device__ __forceinline__ float rg_gw_load(const aotx_rgemv_args &a, uns
 /* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. rpre and
  * gpre, when given, hold the residual values out[] adds to and the next norm's weights of
  * the rows (gpre[row]), read while the weights streamed. */
-template <int MT, int NT>
+template <int MT, int NT, int RTC = 0>
 static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, const float *out,
                                                    unsigned int group, unsigned int rt,
                                                    unsigned int mrows, const unsigned int *list,
@@ -251,6 +251,57 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
     const unsigned int tid = threadIdx.x;
     const unsigned int gr = rt * 16u;
 #define RG_YROW(mm) (list != nullptr ? list[(mm)] : a.m0 + (mm))
+    if constexpr (RTC > 0) {
+        /* rt == RTC, known when compiled (the GEMM's tile): a thread's outputs in chunks of
+         * CH, every load of a chunk issued before its first store (a store to y may alias
+         * the next output's residual, so a plain loop waits a round trip per output) */
+        if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr && list == nullptr) {
+            constexpr unsigned int ITER = ((unsigned int)RTC * 16u * MT + NT - 1u) / NT;
+            constexpr unsigned int CH = ITER < 16u ? ITER : 16u;
+            static_assert(ITER % CH == 0u && (RTC * 16 * MT) % NT == 0, "whole chunks");
+            for (unsigned int c0 = 0; c0 < ITER; c0 += CH) {
+                float rv[CH], gv[CH];
+#pragma unroll
+                for (unsigned int i = 0; i < CH; ++i) {
+                    const unsigned int idx = (c0 + i) * NT + tid;
+                    const unsigned int rr = idx & 15u, rest = idx >> 4;
+                    const unsigned int j = rest % RTC, mm = rest / RTC;
+                    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
+                    const bool col_ok = mm < mrows && v0 + rr < a.n;
+                    /* unconditional, from an address clamped into the operand */
+                    const unsigned long long at = col_ok ? (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr
+                                                         : (unsigned long long)a.m0 * a.ldy;
+                    rv[i] = co_loadf((const float *)a.y + at);
+                    gv[i] = a.xg_out != nullptr ? a.xg_w[col_ok ? v0 + rr : 0u] : 0.0f;
+                }
+#pragma unroll
+                for (unsigned int i = 0; i < CH; ++i) {
+                    const unsigned int idx = (c0 + i) * NT + tid;
+                    const unsigned int rr = idx & 15u, rest = idx >> 4;
+                    const unsigned int j = rest % RTC, mm = rest / RTC;
+                    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
+                    const bool row_ok = mm < mrows && v0 < a.n;
+                    const bool col_ok = row_ok && v0 + rr < a.n;
+                    float v = 0.0f;
+                    if (col_ok) {
+                        v = rv[i] + out[(j * 16u + rr) * MT + mm];
+                        co_storef((float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr, v);
+                        if (a.xg_out != nullptr)
+                            a.xg_out[a.out_frag ? aotx_xfrag_at(a.m0 + mm, v0 + rr)
+                                                : (unsigned long long)(a.m0 + mm) * a.n + v0 + rr] = aotx_f2h(v * gv[i]);
+                    }
+                    float sq = v * v;
+                    sq += __shfl_xor(sq, 1, 64);
+                    sq += __shfl_xor(sq, 2, 64);
+                    sq += __shfl_xor(sq, 4, 64);
+                    sq += __shfl_xor(sq, 8, 64);
+                    if (row_ok && rr == 0u)
+                        co_storef(a.sumsq_out + (unsigned long long)(a.m0 + mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
+                }
+            }
+            return;
+        }
+    }
     if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr) {
         /* one thread per output: 16 consecutive threads hold the 16 rows of one tile for
          * one row of x, add them into the residual stream, and leave the tile's sum of
