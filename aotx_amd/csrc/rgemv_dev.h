@@ -207,6 +207,50 @@ static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep(const aotx_rgemv_args &
     return p;
 }
 
+/* rg_qkv_prep without branches around its loads: every field from selects, the page word
+ * read unconditionally from a clamped index, so that the preparations of several units
+ * have their page-table loads in flight together. Same result as rg_qkv_prep. */
+static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep_flat(const aotx_rgemv_args &a, unsigned int group,
+                                                              unsigned int rt, unsigned int pr,
+                                                              unsigned int mm, unsigned int position,
+                                                              unsigned int agent, float fac, bool live)
+{
+    rg_qkv_pre p;
+    const aotx_qkv_epi &e = a.qkv;
+    const unsigned int row = 2u * pr;
+    const unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
+    const bool ok = live && v < a.n;
+    unsigned int begin;
+    const unsigned int sg = rg_seg(a, v, begin);
+    const unsigned int d = e.head_dim;
+    const unsigned int local = v - begin;
+    const unsigned int head = local / d;
+    const unsigned int dim = local - head * d;
+    const aotx_kvl_shape &s = e.shape;
+    const unsigned int block = (position / AOTX_KVL_BLOCK) * s.layers + e.layer;
+    const unsigned int index = s.blocks_page != 0u ? block / s.blocks_page : 0u;
+    const bool page_ok = s.blocks_page != 0u && agent < AOTX_SLOTS && index < AOTX_KV_PAGES_EACH;
+    const unsigned long long word = e.state->kv.page[page_ok ? agent : 0u][page_ok ? index : 0u];
+    p.cs = 1.0f;
+    p.sn = 0.0f;
+    if (ok && sg <= 1u) {
+        const float step = powf(e.theta, -2.0f / (float)d);
+        float angle = (float)position * powf(step, (float)(dim >> 1));
+        if (e.factor != nullptr) angle = angle / fac;
+        sincosf(angle, &p.sn, &p.cs);
+    }
+    const unsigned int krow = (sg == 1u ? head : e.kv_heads + head) * AOTX_KVL_BLOCK
+                            + position % AOTX_KVL_BLOCK;
+    p.mode = !ok ? 0u : (sg == 0u ? 1u : (sg == 1u ? 2u : 3u));
+    p.count_fault = ok && sg == 1u && dim == 0u ? 1u : 0u;
+    p.base = sg == 0u ? (unsigned long long)e.qh : (page_ok ? word : 0ull);
+    p.off = sg == 0u ? 2ull * ((unsigned long long)(a.m0 + mm) * e.heads * d + local)
+                     : AOTX_KVL_HEADER + (unsigned long long)(s.blocks_page != 0u ? block % s.blocks_page : 0u)
+                                       * s.block_bytes
+                       + 2ull * ((unsigned long long)krow * d + dim);
+    return p;
+}
+
 template <int MT>
 static __device__ __forceinline__ void rg_qkv_store(const aotx_rgemv_args &a, const float *out,
                                                     const rg_qkv_pre &p, unsigned int row,
@@ -297,6 +341,39 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
                     sq += __shfl_xor(sq, 8, 64);
                     if (row_ok && rr == 0u)
                         co_storef(a.sumsq_out + (unsigned long long)(a.m0 + mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
+                }
+            }
+            return;
+        }
+        if (a.epi == AOTX_EPI_QKV && qp == nullptr && list == nullptr) {
+            constexpr unsigned int PAIRS = (unsigned int)RTC * 8u;     /* output pairs per batch row */
+            constexpr unsigned int ITER = PAIRS * MT / NT;
+            constexpr unsigned int CH = ITER < 8u ? ITER : 8u;
+            static_assert((PAIRS * MT) % NT == 0u && ITER % CH == 0u, "whole chunks");
+            for (unsigned int c0 = 0; c0 < ITER; c0 += CH) {
+                unsigned int posv[CH], agv[CH];
+                float facv[CH];
+#pragma unroll
+                for (unsigned int i = 0; i < CH; ++i) {
+                    const unsigned int idx = (c0 + i) * NT + tid;
+                    const unsigned int pr = idx % PAIRS, mm = idx / PAIRS;
+                    const unsigned int tc = a.m0 + (mm < mrows ? mm : 0u);   /* clamped */
+                    posv[i] = a.qkv.pos[tc];
+                    agv[i] = a.qkv.agent[tc];
+                    facv[i] = rg_qkv_factor(a, group, RTC, pr);
+                }
+                rg_qkv_pre pv[CH];
+#pragma unroll
+                for (unsigned int i = 0; i < CH; ++i) {
+                    const unsigned int idx = (c0 + i) * NT + tid;
+                    const unsigned int pr = idx % PAIRS, mm = idx / PAIRS;
+                    pv[i] = rg_qkv_prep_flat(a, group, RTC, pr, mm, posv[i], agv[i], facv[i], mm < mrows);
+                }
+#pragma unroll
+                for (unsigned int i = 0; i < CH; ++i) {
+                    const unsigned int idx = (c0 + i) * NT + tid;
+                    const unsigned int pr = idx % PAIRS, mm = idx / PAIRS;
+                    rg_qkv_store<MT>(a, out, pv[i], 2u * pr, mm);
                 }
             }
             return;
