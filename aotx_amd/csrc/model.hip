@@ -236,14 +236,20 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
                           unsigned int nseg, unsigned int k, int epi, unsigned int cap,
                           const unsigned int *m_dev, const aotx_rgemv_args &tmpl)
 {
-    /* 256 rows or more of a dense product: one GEMM pass (up to 512 rows; below 256 rows
-     * its few workgroups are slower than re-reading the weights per 32 rows); routed
-     * experts keep passes of 32 rows through their row lists */
+    /* 128 rows or more of a dense product: one GEMM pass (up to 512 rows; 128-token prompt
+     * 10.15 -> 8.49 ms against passes of 32 rows, while at 64 rows its few workgroups are
+     * slower than re-reading the weights per 32 rows: the Mixtral-shape step 17.2 -> 19.3
+     * ms); routed experts keep passes of 32 rows through their row lists */
     static const bool gemm_on = [] {
         const char *v = getenv("AOTX_GEMM");       /* 0: 32-row passes, for comparison */
         return !(v != nullptr && v[0] == '0');
     }();
-    const bool gemm = gemm_on && cap >= 256u && tmpl.expert_stride == 0ull && tmpl.list == nullptr
+    static const unsigned int gemm_min = [] {
+        const char *v = getenv("AOTX_GEMM_MIN");   /* the smallest pass for the GEMM (sweeps) */
+        const unsigned int m = v != nullptr ? (unsigned int)atoi(v) : 0u;
+        return m >= 33u && m <= AOTX_RGEMM_ROWS ? m : 128u;
+    }();
+    const bool gemm = gemm_on && cap >= gemm_min && tmpl.expert_stride == 0ull && tmpl.list == nullptr
                    && tmpl.xrow == nullptr && tmpl.xmode == AOTX_X_F16;
     for (unsigned int m0 = 0, mt = 0; m0 < cap; m0 += mt) {
         mt = gemm ? (cap - m0 < AOTX_RGEMM_ROWS ? cap - m0 : AOTX_RGEMM_ROWS)
@@ -750,7 +756,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
         }
         /* the GEMM passes (256 rows and more) of the dense products */
-        for (unsigned int mt = 256u; mt <= AOTX_RGEMM_ROWS && mt <= cap; mt += 64u) {
+        for (unsigned int mt = 64u; mt <= AOTX_RGEMM_ROWS && mt <= cap; mt += 64u) {
             aotx_rgemv_args a;
             unsigned int r3[3] = {(unsigned int)wide, (unsigned int)narrow, (unsigned int)narrow};
             unsigned int r1[1] = {d->hidden};

@@ -286,11 +286,12 @@ def test_8b_width_experts_wide_batch_vs_oracle(torch, orc):
         rt.close()
 
 
-@pytest.mark.parametrize("prompt", [300, 512])
+@pytest.mark.parametrize("prompt", [100, 300, 512])
 def test_8b_width_long_prompt_logits_vs_oracle(torch, orc, prompt):
-    """A prompt of 300 and of 512 tokens in one pass through aotx_model_prefill on an
-    8B-width model (2 layers: d_model 4096, FFN 14336, 32/8 heads x 128): the GEMM of 256
-    rows or more with its QKV rotary/page-write, residual and SwiGLU epilogues, and the
+    """A prompt of 100, 300 and 512 tokens in one pass through aotx_model_prefill on an
+    8B-width model (2 layers: d_model 4096, FFN 14336, 32/8 heads x 128): the GEMM of 128
+    rows or more (k split for the products of few workgroups) with its QKV rotary/page-write,
+    residual and SwiGLU epilogues, and the
     prompt-piece attention; the logits of tokens 1, 17, 130 and 257 and of the last vs the
     oracle
     (cuda/model/gemm.cuh:55-189, cuda/model/attention.cu:22-154)."""
@@ -308,6 +309,8 @@ def test_8b_width_long_prompt_logits_vs_oracle(torch, orc, prompt):
         want = ref.step(ids, [0, prompt], [3])
         assert rel_rms(lg[prompt - 1:prompt], want) < 1e-2
         for n in (1, 17, 130, 257):
+            if n >= prompt:
+                continue
             r2 = orc.Model(lay.desc, region, slots=4, max_context=prompt + 2, threads=8)
             w = r2.step(ids[:n], [0, n], [3])
             assert rel_rms(lg[n - 1:n], w) < 1e-2, n
