@@ -556,14 +556,15 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
  * together on one XCD (dispatch goes round the 8 XCDs by workgroup index): they read each
  * weight quad at about the same time, and the XCD's L2 serves all but the first read.
  * NTL: the weights are read with nontemporal loads. */
-template <int MB, bool XCD, bool NTL>
+template <int MB, bool XCD, bool NTL, bool PAIR = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void aotx_rgemm(aotx_rgemv_args a0, unsigned int ny)
 {
     aotx_args_touch(a0);
     constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
     constexpr int CB = MB / 16;                   /* column blocks per wave */
     constexpr int NT = 512;
-    constexpr int XS = 128 + 8;                   /* LDS x row stride (halves) */
+    /* PAIR: an LDS x buffer holds two quads, one barrier per pair of quads */
+    constexpr int XS = (PAIR ? 256 : 128) + 8;    /* LDS x row stride (halves) */
     constexpr int PIECES = 16;                    /* 16-byte pieces of a row per quad */
     constexpr int PPT = MB * PIECES / NT;         /* pieces per thread */
     static_assert(MB * PIECES % NT == 0 && MB % 16 == 0, "whole pieces and blocks");
@@ -648,9 +649,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
             xr[XB][i] = *(const rg_u4 *)(a.x + xoff[i] + qx_);                           \
     } while (0)
+/* the LDS place of quad Q: buffer and offset within a row */
+#define RGM_XBUF(Q) (PAIR ? ((((Q) - qb0) >> 1) & 1u) : ((Q) & 1u))
+#define RGM_XPOS(Q) (PAIR ? (((Q) - qb0) & 1u) * 128u : 0u)
 #define RGM_XSTORE(XB, Q)                                                                \
     do {                                                                                 \
-        unsigned short *xb_ = xl + ((Q) & 1u) * (unsigned int)(MB * XS) + xrow0 * XS + xpc * 8u; \
+        unsigned short *xb_ = xl + RGM_XBUF(Q) * (unsigned int)(MB * XS) + RGM_XPOS(Q)   \
+                            + xrow0 * XS + xpc * 8u;                                     \
         _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                  \
             *(rg_u4 *)(xb_ + (unsigned int)i * RSTEP * XS) =                             \
                 xrow0 + (unsigned int)i * RSTEP < mrows ? xr[XB][i] : (rg_u4){0u, 0u, 0u, 0u}; \
@@ -664,14 +669,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     RGM_WLOAD(0, qb0);
     RGM_WLOAD(1, qb0 + 1u);
     RGM_XSTORE(0, qb0);
+    if (PAIR) RGM_XSTORE(1, qb0 + 1u);
     rg_sync_lds();
     for (unsigned int q = qb0; q < qn; q += 2u) {
-#define RGM_STEP(BUF, QQ)                                                                \
+/* quad QQ's MFMAs from weight buffer BUF, then quad QQ + 2's weights into it */
+#define RGM_COMPUTE(BUF, QQ)                                                             \
     do {                                                                                 \
         const unsigned int qc_ = (QQ);                                                   \
-        RGM_XLOAD(BUF, qc_ + 2u);                                                        \
-        __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */ \
-        const unsigned short *xb = xl + (qc_ & 1u) * (unsigned int)(MB * XS);           \
+        const unsigned short *xb = xl + RGM_XBUF(qc_) * (unsigned int)(MB * XS) + RGM_XPOS(qc_); \
         const unsigned int sq_ = qc_ < qn ? 0xffffffffu : 0u;                            \
         rg_h8 A[2][4];                                                                   \
         _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                  \
@@ -698,13 +703,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         __builtin_amdgcn_sched_barrier(0);     /* the MFMAs before the new loads */      \
         RGM_WLOAD(BUF, qc_ + 2u);                                                        \
         __builtin_amdgcn_sched_barrier(0);                                               \
-        RGM_XSTORE(BUF ^ 1, qc_ + 1u);                                                   \
-        rg_sync_lds();                                                                   \
     } while (0)
-        RGM_STEP(0, q);
-        RGM_STEP(1, q + 1u);
-#undef RGM_STEP
+        if (PAIR) {
+            /* the next pair's x first, then both quads, then its store and one barrier */
+            RGM_XLOAD(0, q + 2u);
+            RGM_XLOAD(1, q + 3u);
+            __builtin_amdgcn_sched_barrier(0);
+            RGM_COMPUTE(0, q);
+            RGM_COMPUTE(1, q + 1u);
+            RGM_XSTORE(0, q + 2u);
+            RGM_XSTORE(1, q + 3u);
+            rg_sync_lds();
+        } else {
+            RGM_XLOAD(0, q + 2u);
+            __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */
+            RGM_COMPUTE(0, q);
+            RGM_XSTORE(1, q + 1u);
+            rg_sync_lds();
+            RGM_XLOAD(1, q + 3u);
+            __builtin_amdgcn_sched_barrier(0);
+            RGM_COMPUTE(1, q + 1u);
+            RGM_XSTORE(0, q + 2u);
+            rg_sync_lds();
+        }
+#undef RGM_COMPUTE
     }
+#undef RGM_XBUF
+#undef RGM_XPOS
 #undef RGM_WLOAD
 #undef RGM_XLOAD
 #undef RGM_XSTORE
@@ -1010,11 +1035,22 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             return e != nullptr ? atoi(e) & 3 : 3;
         }();
         const dim3 g2(a.groups, ny * a.splits), g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
+        static const bool pair = [] {
+            const char *e = getenv("AOTX_GEMM_PAIR");     /* 0: a barrier per quad (sweeps) */
+            return !(e != nullptr && e[0] == '0');
+        }();
         switch (mode) {
         case 0: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, true>), g2, dim3(512), lds, s, a, ny); break;
         case 1: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, false>), g2, dim3(512), lds, s, a, ny); break;
         case 2: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, true>), g1, dim3(512), lds, s, a, ny); break;
-        default: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false>), g1, dim3(512), lds, s, a, ny); break;
+        default:
+            if (pair) {
+                const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u;
+                hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false, true>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
+            } else {
+                hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false>), g1, dim3(512), lds, s, a, ny);
+            }
+            break;
         }
         AOTX_LAUNCH_CHECK();
         return;
