@@ -141,7 +141,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
             const rg_u4 *src = (const rg_u4 *)(qb + (unsigned long long)qq * 2048ull);   \
             wa[BUF][qi][0] = __builtin_nontemporal_load(src);                            \
             wa[BUF][qi][1] = __builtin_nontemporal_load(src + 64);                       \
-            ws[BUF][qi] = sb[(unsigned long long)qq * 64ull];                            \
+            ws[BUF][qi] = __builtin_nontemporal_load(&sb[(unsigned long long)qq * 64ull]); \
         }                                                                                \
     } while (0)
     /* branch-free: a quad past the range reads a valid x quad and has its scale zeroed */
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
                 const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
                 wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                      \
                 wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                 \
-                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                   \
+                ws[BUF][qi][j] = __builtin_nontemporal_load(&sb[j][(unsigned long long)qq * 64ull]); \
             }                                                                             \
             _Pragma("unroll") for (int t = 0; t < 2; ++t)                                 \
                 _Pragma("unroll") for (int st = 0; st < 4; ++st)                          \
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
                 wa[BUF][t][0] = src[0];                                                  \
                 wa[BUF][t][1] = src[64];                                                 \
             }                                                                            \
-            ws[BUF][t] = sb[t][(unsigned long long)qq_ * 64ull];                         \
+            ws[BUF][t] = __builtin_nontemporal_load(&sb[t][(unsigned long long)qq_ * 64ull]); \
         }                                                                                \
     } while (0)
     /* x pieces of quad Q (k is a whole number of quads: a quad past k repeats the last) */

@@ -714,7 +714,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                 const rg_u4 *src = (const rg_u4 *)(qb[j] + (unsigned long long)qq * 2048ull); \
                 wa[BUF][qi][j][0] = __builtin_nontemporal_load(src);                    \
                 wa[BUF][qi][j][1] = __builtin_nontemporal_load(src + 64);                \
-                ws[BUF][qi][j] = sb[j][(unsigned long long)qq * 64ull];                  \
+                ws[BUF][qi][j] = __builtin_nontemporal_load(&sb[j][(unsigned long long)qq * 64ull]); \
             }                                                                            \
         }                                                                                \
     } while (0)
