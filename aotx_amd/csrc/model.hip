@@ -59,6 +59,7 @@ struct aotx_rlayer {
 
 struct aotx_hold {
     int ready;
+    int record_failed;      /* a launch of the step being recorded was refused */
     int described;
     aotx_model_desc desc;
     unsigned int role;
@@ -261,7 +262,8 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
                                          : aotx_rgemv_plan(&a, w, rows, nseg, k, epi, mt);
         if (refused != 0) {
             fprintf(stderr, "aotx: a product of the model was refused (k=%u)\n", k);
-            exit(1);
+            h->record_failed = 1;
+            return;
         }
         aotx_roperands(&a, tmpl);
         a.m_dev = m_dev;
@@ -270,12 +272,14 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
             size_t need = aotx_rgemv_partial_bytes(a);
             if (need > h->gemv_partial_bytes) {
                 fprintf(stderr, "aotx: split partials exceed the planned buffer\n");
-                exit(1);
+                h->record_failed = 1;
+                return;
             }
             a.partial = h->gemv_partial;
             if (aotx_rgemv_count_words(a) > AOTX_GEMV_COUNTS) {
                 fprintf(stderr, "aotx: split counters exceed the planned buffer\n");
-                exit(1);
+                h->record_failed = 1;
+                return;
             }
             a.count = h->gemv_count;
         }
@@ -361,7 +365,8 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
         if (aotx_plan_launch(h->role, tk->slots, tk->tokens, tk->stride, tk->budget,
                              tk->pool_pages, tk->plan, s) != 0) {
             fprintf(stderr, "aotx: the tick plan was refused\n");
-            exit(1);
+            h->record_failed = 1;
+            return;
         }
         aotx_launch_tick_begin(h->step, tk->plan, h->tick_token, h->tick_draw, s);
     } else {
@@ -459,7 +464,8 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
                                d->kv_heads, hd, l, d->layers, max_context, h->attn_partial,
                                h->attn_count, s, frag ? 1u : 0u) != 0) {
             fprintf(stderr, "aotx: attention refused the shape\n");
-            exit(1);
+            h->record_failed = 1;
+            return;
         }
         {
             aotx_rgemv_args t;
@@ -622,7 +628,8 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
                               h->tick_token, h->tick_draw, tk->plan, tk->records, tk->capacity,
                               s) != 0) {
         fprintf(stderr, "aotx: the tick commit was refused\n");
-        exit(1);
+        h->record_failed = 1;
+        return;
     }
 }
 
@@ -896,8 +903,13 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
         if (exec == nullptr) {
             hipGraph_t graph = nullptr;
             AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+            h->record_failed = 0;
             aotx_record_step(h, all, bt, br, nullptr);
             AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
+            if (h->record_failed) {
+                AOTX_CHECK(hipGraphDestroy(graph));
+                return 1;
+            }
             size_t count = 0;
             AOTX_CHECK(hipGraphGetNodes(graph, nullptr, &count));
             if ((unsigned int)count > h->nodes) h->nodes = (unsigned int)count;
@@ -906,7 +918,12 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
         }
         AOTX_CHECK(hipGraphLaunch(exec, h->stream));
     } else {
+        h->record_failed = 0;
         aotx_record_step(h, all, bt, br, nullptr);
+        if (h->record_failed) {
+            aotx_wait(h->stream);
+            return 1;
+        }
     }
     if (set->logits != nullptr) {
         AOTX_CHECK(hipMemcpyAsync(set->logits, h->logits,
@@ -964,8 +981,13 @@ extern "C" int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *t
     if (exec == nullptr) {
         hipGraph_t graph = nullptr;
         AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        h->record_failed = 0;
         aotx_record_step(h, 0u, bt, br, &tk);
         AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
+        if (h->record_failed) {
+            AOTX_CHECK(hipGraphDestroy(graph));
+            return 1;
+        }
         AOTX_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
         AOTX_CHECK(hipGraphDestroy(graph));
         h->tick_setup[bt] = tk;
