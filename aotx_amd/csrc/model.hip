@@ -37,6 +37,7 @@
 unsigned long long aotx_mem_weights_bytes(void);
 
 #define AOTX_BUCKETS 10u   /* 1, 2, 4, ..., 512 */
+#define AOTX_WIDE_PASSES 4u        /* 32-row passes of a wide product in one launch */
 #define AOTX_GEMV_COUNTS 65536u   /* split arrival counters: experts x product groups */
 
 /* The operands of a decode tick; a tick graph is captured for one set of them. */
@@ -268,6 +269,14 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
         aotx_roperands(&a, tmpl);
         a.m_dev = m_dev;
         a.m0 = m0;
+        /* whole 32-row passes of a wide product over direct rows run as one launch (grid.y
+         * is the pass): one launch's ramp and tail instead of one per pass */
+        if (!gemm && a.wide && mt == 32u && cap - m0 >= 64u && tmpl.expert_stride == 0ull
+            && tmpl.list == nullptr && tmpl.xrow == nullptr) {
+            a.passes = (cap - m0) / 32u;
+            if (a.passes > AOTX_WIDE_PASSES) a.passes = AOTX_WIDE_PASSES;
+            mt = 32u * a.passes;
+        }
         if (a.splits > 1u) {
             size_t need = aotx_rgemv_partial_bytes(a);
             if (need > h->gemv_partial_bytes) {
@@ -778,7 +787,7 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
                 gp = gp > aotx_rgemv_partial_bytes(a) ? gp : aotx_rgemv_partial_bytes(a);
         }
     }
-    h->gemv_partial_bytes = gp + 4096u;
+    h->gemv_partial_bytes = gp * AOTX_WIDE_PASSES + 4096u;   /* passes in one launch */
     h->gemv_partial = (float *)aotx_take(h, h->gemv_partial_bytes);
     h->gemv_count = (unsigned int *)aotx_take(h, AOTX_GEMV_COUNTS * sizeof(unsigned int));
     size_t ap = 0u;

@@ -90,6 +90,9 @@ struct aotx_rgemv_args {
     unsigned int list_cap;
     unsigned int xrow_div;
     unsigned int experts;
+    /* wide products of direct rows: consecutive 32-row passes in one launch (grid.y is the
+     * pass, rows m0 + 32 * pass on); 0 or 1 is one pass */
+    unsigned int passes;
 };
 
 /* Plan a product over Q8R tensors; rows per segment; returns 1 when refused. mt is the

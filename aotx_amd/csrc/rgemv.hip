@@ -86,8 +86,11 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv(aotx_rgemv_args a)
  * workgroups, the last split to finish adds the splits first). More phases put more waves
  * on the same tiles (more loads in flight per CU) at the price of more x staging. */
 template <int T, int P, int KC, int PDQ>
-__global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args a)
+__global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args a0)
 {
+    /* direct rows: grid.y is the 32-row pass (routed experts: the expert) */
+    aotx_rgemv_args a = a0;
+    if (a0.expert_stride == 0ull) a.m0 = a0.m0 + 32u * blockIdx.y;
     constexpr int MT = 32;
     constexpr int W = T * P;
     constexpr int NT = 64 * W;
@@ -973,18 +976,25 @@ int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigne
     return 0;
 }
 
+/* grid.y of a product: its experts, or the passes of a wide product of direct rows */
+static unsigned int aotx_rgemv_rows_y(const aotx_rgemv_args &a)
+{
+    if (a.expert_stride != 0ull) return a.experts;
+    return a.wide && a.passes > 1u ? a.passes : 1u;
+}
+
 size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
 {
     if (a.splits <= 1u) return 0u;
     if (a.gemm) return (size_t)aotx_rgemv_count_words(a) * a.splits * RGM_RT * 16u * RGM_MB * sizeof(float);
-    size_t e = a.expert_stride != 0ull ? a.experts : 1u;
+    size_t e = aotx_rgemv_rows_y(a);
     return e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float);
 }
 
 unsigned int aotx_rgemv_count_words(const aotx_rgemv_args &a)
 {
     if (a.gemm) return a.groups * ((a.m + RGM_MB - 1u) / RGM_MB);
-    return (a.expert_stride != 0ull ? a.experts : 1u) * a.groups;
+    return aotx_rgemv_rows_y(a) * a.groups;
 }
 
 template <int MT, int RT, int PD>
@@ -1089,7 +1099,7 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         exit(1);
     }
     if (a.wide) {
-        unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
+        const unsigned int ey = aotx_rgemv_rows_y(a);
         const dim3 grid(a.groups * a.splits, ey);
         if (a.xmode != AOTX_X_F16) {
             fprintf(stderr, "aotx: the wide-batch product takes fp16 x only\n");
