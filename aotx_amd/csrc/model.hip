@@ -1103,6 +1103,7 @@ extern "C" unsigned long long aotx_model_buffer(unsigned int role, unsigned int 
     /* routed experts, the last layer of the last pass (null without experts) */
     case 4: return (unsigned long long)h->ecount;   /* rows per expert, u32 [experts] */
     case 5: return (unsigned long long)h->ids;      /* experts of each token, u32 [T][used] */
+    case 6: return (unsigned long long)h->prob;     /* router probabilities, f32 [T][experts] */
     default: return 0ull;
     }
 }

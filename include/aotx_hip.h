@@ -288,7 +288,8 @@ int aotx_model_seat(unsigned int agent, unsigned int position);
  * reference. which: 0 the rows after the last norm (half [max_tokens][hidden]; a 5..32-row
  * pass in the fragment layout), 1 the residual stream (float), 2 the head's rows (float
  * [rows][vocab]), 3 the head's input rows (half), 4 the routed rows per expert of the last
- * layer run (u32 [experts]), 5 the experts each token chose there (u32 [tokens][used]).
+ * layer run (u32 [experts]), 5 the experts each token chose there (u32 [tokens][used]), 6 the
+ * router's probabilities there (f32 [tokens][experts]).
  * 0 for an unknown buffer or one the role does not have. */
 unsigned long long aotx_model_buffer(unsigned int role, unsigned int which);
 

@@ -453,6 +453,10 @@ struct orc_model {
     uint16_t *keys;  /* [slots][layers][max_context][kv_heads*d], fp16 as the pages hold */
     uint16_t *values;
     float *last_xnorm;
+    /* routing of the last experts layer of the last step: [tokens][experts], [tokens][used] */
+    float *last_prob;
+    unsigned int *last_ids;
+    unsigned int last_route_tokens;
 };
 
 
@@ -484,7 +488,8 @@ orc_model *orc_model_new(const aotx_model_desc *desc, const uint8_t *weights,
 void orc_model_free(orc_model *m)
 {
     if (!m) return;
-    free(m->seen); free(m->keys); free(m->values); free(m->last_xnorm); free(m);
+    free(m->seen); free(m->keys); free(m->values); free(m->last_xnorm);
+    free(m->last_prob); free(m->last_ids); free(m);
 }
 
 void orc_model_forget(orc_model *m)
@@ -493,6 +498,16 @@ void orc_model_forget(orc_model *m)
 }
 
 const float *orc_model_last_xnorm(const orc_model *m) { return m->last_xnorm; }
+
+/* The router's probabilities and chosen experts of the last experts layer the last step
+ * ran; *tokens is the step's row count (0 when no experts layer ran). */
+const float *orc_model_last_route(const orc_model *m, const unsigned int **ids,
+                                  unsigned int *tokens)
+{
+    *ids = m->last_ids;
+    *tokens = m->last_route_tokens;
+    return m->last_prob;
+}
 
 /* The model's cache as fp16 words [slots][layers][max_context][kv_heads * head_dim]:
  * which = 0 keys, 1 values. For tests that write the same cache into the device pages. */
@@ -639,6 +654,7 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
     for (unsigned int s = 0; s < seqs; ++s) {
         if (agent[s] >= m->slots || m->seen[agent[s]] + (offset[s + 1] - offset[s]) > m->max_context) return 1;
     }
+    m->last_route_tokens = 0;
     float *resid = (float *)calloc((size_t)tokens * h, sizeof(float));
     float *x = (float *)calloc((size_t)tokens * big, sizeof(float));
     float *q = (float *)calloc((size_t)tokens * wide, sizeof(float));
@@ -758,7 +774,11 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
                 }
             }
             for (size_t i = 0; i < (size_t)tokens * h; ++i) resid[i] += esum[i];
-            free(prob); free(sel); free(x16);
+            free(m->last_prob); free(m->last_ids);
+            m->last_prob = prob;
+            m->last_ids = sel;
+            m->last_route_tokens = tokens;
+            free(x16);
         } else {
             orc_matmul(m, (const uint8_t *)orc_tensor(m, L->offset[AOTX_SLOT_FFN_GATE]), f, h, x, tokens, gate);
             orc_matmul(m, (const uint8_t *)orc_tensor(m, L->offset[AOTX_SLOT_FFN_UP]), f, h, x, tokens, up);

@@ -52,6 +52,8 @@ def lib():
         L.orc_model_seat.argtypes = [vp, u32, u32, u64]
         L.orc_model_last_xnorm.restype = ctypes.POINTER(f32)
         L.orc_model_last_xnorm.argtypes = [vp]
+        L.orc_model_last_route.restype = ctypes.POINTER(f32)
+        L.orc_model_last_route.argtypes = [vp, ctypes.POINTER(ctypes.POINTER(u32)), ctypes.POINTER(u32)]
         L.orc_model_cache.restype = ctypes.POINTER(ctypes.c_uint16)
         L.orc_model_cache.argtypes = [vp, u32]
         _lib = L
@@ -152,6 +154,21 @@ class Model:
     def last_xnorm(self, seqs):
         p = lib().orc_model_last_xnorm(self.h)
         return np.ctypeslib.as_array(p, shape=(seqs * self.hidden,)).reshape(seqs, self.hidden).copy()
+
+    def last_route(self):
+        """(probabilities [tokens][experts], ids [tokens][used]) of the last experts layer of
+        the last step, or None when that step ran no experts layer."""
+        ids = ctypes.POINTER(ctypes.c_uint32)()
+        tokens = ctypes.c_uint32(0)
+        p = lib().orc_model_last_route(self.h, ctypes.byref(ids), ctypes.byref(tokens))
+        t = tokens.value
+        if t == 0:
+            return None
+        d = self.desc
+        prob = np.ctypeslib.as_array(p, shape=(t * d.expert_count,)).reshape(t, d.expert_count).copy()
+        sel = np.ctypeslib.as_array(ids, shape=(t * d.expert_used_count,)).reshape(
+            t, d.expert_used_count).copy()
+        return prob, sel
 
     def cache(self):
         """Views of the cache, (keys, values) fp16 words [slots][layers][max_context][kv_heads *

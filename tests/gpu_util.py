@@ -28,3 +28,19 @@ def rel_rms(got, want):
     err = np.abs(got - want) / np.maximum(np.abs(want), rms)
     err[~np.isfinite(got)] = np.inf
     return float(err.max())
+
+
+def read_device(addr, dtype, count):
+    """Copy `count` elements of `dtype` from a device address the library handed out (for
+    example aotx_model_buffer) into a numpy array, through the HIP runtime the library
+    itself is linked against."""
+    import aotx_amd
+    import torch
+    torch.cuda.synchronize()
+    out = np.empty(count, dtype=dtype)
+    L = aotx_amd.lib()
+    L.hipMemcpy.restype = ctypes.c_int
+    L.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    rc = L.hipMemcpy(out.ctypes.data, ctypes.c_void_p(addr), out.nbytes, 2)  # device to host
+    assert rc == 0, f"hipMemcpy returned {rc}"
+    return out

@@ -30,7 +30,7 @@ import pytest
 import aotx_amd
 from aotx_amd.model import LLAMA_8B, MIXTRAL, TINY, Runtime, Shape, build_device, build_host, \
     layout_pages
-from tests.gpu_util import rel_rms
+from tests.gpu_util import read_device, rel_rms
 
 pytestmark = pytest.mark.gpu
 
@@ -159,11 +159,36 @@ def test_config5_mixtral_width_full_size(torch, orc):
         rng = np.random.default_rng(5)
         ids = rng.integers(0, shape.vocab, batch).tolist()
         offs = list(range(batch + 1))
+        E, used = shape.experts, shape.used
+        checked = 0
         for step in range(2):
             tok, _, lg = rt.step(ids, offs, slots)
             want = ref.step(ids, offs, slots)
             assert rel_rms(lg, want) < 1e-2, step
+            _deep_close(lg, want)
+            err = float(np.abs(lg - want).max())
+            for r in range(batch):
+                if _gap(want[r]) > 2 * err:
+                    assert int(tok[r]) == int(np.argmax(want[r])), (step, r)
+            # the routing of the last layer: ids bit-exact wherever the oracle's neighbouring
+            # ranks (0..used) are further apart than the measured probability error
+            got_ids = read_device(rt.L.aotx_model_buffer(rt.role, 5), np.uint32, batch * used)
+            got_p = read_device(rt.L.aotx_model_buffer(rt.role, 6), np.float32, batch * E)
+            got_ids = got_ids.reshape(batch, used)
+            got_p = got_p.reshape(batch, E)
+            want_p, want_ids = ref.last_route()
+            perr = float(np.abs(got_p - want_p).max())
+            srt = -np.sort(-want_p.astype(np.float64), axis=1)
+            gaps = (srt[:, :used] - srt[:, 1:used + 1]).min(axis=1)
+            clear = gaps > 2 * perr
+            print(f"step {step}: logits err {err:.2e}, router prob err {perr:.2e}, "
+                  f"{int(clear.sum())}/{batch} tokens with clear ranks", flush=True)
+            assert perr < 1e-2
+            assert clear.sum() >= batch * 3 // 4
+            assert np.array_equal(got_ids[clear], want_ids[clear])
+            checked += int(clear.sum())
             ids = [int(t) for t in tok]
+        assert checked > 0
         assert rt.faulted() == 0
     finally:
         rt.close()

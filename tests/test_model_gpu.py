@@ -235,17 +235,19 @@ def _device_model(torch, shape, seed):
     return region_dev, region_dev.cpu().numpy(), lay
 
 
-@pytest.mark.parametrize("rows", [32, 20, 12, 6])
+@pytest.mark.parametrize("rows", [32, 20, 12, 6, 40, 48])
 def test_8b_width_wide_batch_vs_oracle(torch, orc, rows):
     """8B-width layer (d_model 4096, FFN 14336, 32/8 heads x 128) at 5..32 batch rows (token
     buckets 8, 16 and 32): QKV (rotary + page write) and O (residual add + sums of squares)
     take the fragment-layout product, with x written in that layout by the norm, the down
     epilogue and the attention; gate/up and down take the wide kernel. A prompt pass of 4
-    tokens per slot, then a decode step of one token per slot, logits vs the oracle."""
+    tokens per slot, then a decode step of one token per slot, logits vs the oracle.
+    40 and 48 rows fall in the 64-token bucket: two 32-row passes in one launch, the second
+    one partly filled (8 and 16 rows)."""
     shape = Shape(layers=1, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
                   vocab=1024)
     region_dev, region, lay = _device_model(torch, shape, 5)
-    rt = Runtime(region_dev, lay.desc, max_tokens=128, pool_pages=256)
+    rt = Runtime(region_dev, lay.desc, max_tokens=256, pool_pages=256)
     try:
         ref = orc.Model(lay.desc, region, slots=rows, max_context=64, threads=8)
         rng = np.random.default_rng(7)
@@ -265,19 +267,26 @@ def test_8b_width_wide_batch_vs_oracle(torch, orc, rows):
         rt.close()
 
 
-def test_8b_width_experts_wide_batch_vs_oracle(torch, orc):
-    """Routed experts at d_model 4096 with 24 rows: the expert down product (k = 4096) takes
-    the wide kernel through the expert row lists."""
+@pytest.mark.parametrize("rows", [24, 40])
+def test_8b_width_experts_wide_batch_vs_oracle(torch, orc, rows):
+    """Routed experts at d_model 4096 with 24 and 40 rows: the expert down product (k = 4096)
+    takes the wide kernel through the expert row lists; at 40 rows the dense products run
+    two 32-row passes in one launch, the second with 8 rows."""
     shape = Shape(layers=1, hidden=4096, ffn=4096, heads=32, kv_heads=8, head_dim=128,
                   vocab=1024, experts=4, used=2)
     region_dev, region, lay = _device_model(torch, shape, 6)
-    rt = Runtime(region_dev, lay.desc, max_tokens=64, pool_pages=128)
+    rt = Runtime(region_dev, lay.desc, max_tokens=128, pool_pages=128)
     try:
-        ref = orc.Model(lay.desc, region, slots=24, max_context=64, threads=8)
+        ref = orc.Model(lay.desc, region, slots=rows, max_context=64, threads=8)
         rng = np.random.default_rng(8)
-        ids = rng.integers(0, shape.vocab, 48).tolist()
-        offs = [2 * i for i in range(25)]
-        agents = list(range(24))
+        ids = rng.integers(0, shape.vocab, 2 * rows).tolist()
+        offs = [2 * i for i in range(rows + 1)]
+        agents = list(range(rows))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        ids = rng.integers(0, shape.vocab, rows).tolist()
+        offs = list(range(rows + 1))
         _, _, lg = rt.step(ids, offs, agents)
         want = ref.step(ids, offs, agents)
         assert rel_rms(lg, want) < 1e-2
