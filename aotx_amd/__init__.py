@@ -23,6 +23,8 @@ AOTX_MODEL_MAX_TOKENS = 512
 AOTX_MODEL_MAX_LAYERS = 64
 AOTX_LAYER_TENSOR_SLOTS = 14
 AOTX_MODEL_STEERS = 2
+AOTX_MODEL_EMBEDDING = 0
+AOTX_MODEL_RERANKER = 1
 AOTX_MODEL_LANGUAGE = 2
 AOTX_WEIGHT_F32 = 0
 AOTX_WEIGHT_F16 = 1
@@ -204,6 +206,8 @@ PROTOTYPES = {
     "aotx_model_prefill": (i32, [u32, vp, vp, u32, vp, vp, vp]),
     "aotx_model_probe": (i32, [u32, vp, vp, u32, vp, vp, vp, u32, vp, vp, u32]),
     "aotx_model_buffer": (u64, [u32, u32]),
+    "aotx_model_rerank": (i32, [vp, vp, u32, vp, vp]),
+    "aotx_model_graphs": (None, [u32]),
     "aotx_model_seat": (i32, [u32, u32]),
     # the tick plan (include/aotx_plan.h)
     "aotx_decode_plan": (i32, [u32, vp, vp, u32, u32, u32, vp, vp]),

@@ -43,10 +43,7 @@ aotx_state *aotx_state_existing(void);
 /* Per-call scratch of the library (partial sums, arrival counters). One growable buffer
  * per use; counters are zeroed once at allocation and every kernel that uses one puts
  * it back to zero before it exits. */
-void *aotx_scratch(int which, size_t bytes);
-/* 4 KB of pinned host memory for step read-backs (one host thread per runtime). */
-void *aotx_pinned(void);
-enum {
+enum aotx_scratch_kind : int {
     AOTX_SCRATCH_GEMV_PARTIAL = 0,
     AOTX_SCRATCH_GEMV_COUNT,
     AOTX_SCRATCH_ATTN_PARTIAL,
@@ -55,6 +52,9 @@ enum {
     AOTX_SCRATCH_PICK,
     AOTX_SCRATCH_KINDS
 };
+void *aotx_scratch(aotx_scratch_kind which, size_t bytes);
+/* 4 KB of pinned host memory for step read-backs (one host thread per runtime). */
+void *aotx_pinned(void);
 
 static inline hipStream_t aotx_stream(void *s) { return (hipStream_t)s; }
 

@@ -33,15 +33,6 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
     aotx_attend_body<D, G, W, 1>(a, blockIdx.x);
 }
 
-/* Prompt pieces: 16 / G consecutive queries of a sequence per workgroup, all of them on
- * one read of their keys and values (the score tile's 16 columns are queries x heads). */
-template <int D, int G, int W>
-__global__ __launch_bounds__(64 * W) void aotx_attend_piece(aotx_attn_args a)
-{
-    aotx_args_touch(a);
-    aotx_attend_body<D, G, W, 16 / G>(a, blockIdx.x);
-}
-
 /* Prompt pieces one wave each (aotx_attend_runs). */
 template <int D, int G, int W>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void aotx_attend_run(aotx_attn_args a)
@@ -57,13 +48,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) voi
 unsigned int aotx_attn_splits(unsigned int tokens, unsigned int kv_heads,
                               unsigned int max_context)
 {
-    /* about ATTN_TARGET_GROUPS workgroups over the launch (AOTX_ATTN_GROUPS overrides it
-     * for measurement sweeps), chunks of at least 64 positions */
-    static const unsigned int target = [] {
-        const char *e = getenv("AOTX_ATTN_GROUPS");
-        unsigned int v = e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 0u;
-        return v != 0u ? v : ATTN_TARGET_GROUPS;
-    }();
+    /* about ATTN_TARGET_GROUPS workgroups over the launch, chunks of at least 64 positions */
+    const unsigned int target = ATTN_TARGET_GROUPS;
     unsigned int units = tokens * kv_heads;
     unsigned int s = (target + units - 1u) / units;
     unsigned int cap = (max_context + ATTN_CHUNK_ALIGN - 1u) / ATTN_CHUNK_ALIGN;
@@ -135,20 +121,13 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
     a.out_frag = out_frag;
     const unsigned int g = heads / kv_heads;
     if (tokens >= AOTX_ATTN_PIECE_TOKENS) {
-        /* more tokens than sequence slots: a batch with prompt pieces. One workgroup per
-         * token and KV head; the ones that lead a run of queries compute it. */
+        /* more tokens than sequence slots: a batch with prompt pieces, one wave per piece
+         * of consecutive queries of a sequence, 4 waves per 16-token range and KV head */
         a.splits = 1u;
-        /* AOTX_ATTN_RUNS=0: the piece per workgroup, for comparison */
-        static const bool runs = [] {
-            const char *v = getenv("AOTX_ATTN_RUNS");
-            return !(v != nullptr && v[0] == '0');
-        }();
-        dim3 grid(tokens * kv_heads);
         const dim3 rgrid((tokens + AOTX_RUN_RANGE - 1u) / AOTX_RUN_RANGE * kv_heads);
 #define AOTX_PIECE_GO(DD, GG)                                                              \
         do {                                                                               \
-            if (runs) hipLaunchKernelGGL((aotx_attend_run<DD, GG, 4>), rgrid, dim3(256), 0, stream, a); \
-            else hipLaunchKernelGGL((aotx_attend_piece<DD, GG, 8>), grid, dim3(512), 0, stream, a); \
+            hipLaunchKernelGGL((aotx_attend_run<DD, GG, 4>), rgrid, dim3(256), 0, stream, a); \
             AOTX_LAUNCH_CHECK();                                                           \
         } while (0)
         if (head_dim == 128u) {
@@ -253,6 +232,16 @@ extern "C" int aotx_attend_paged_static(const void *q, const unsigned int *pos,
         fprintf(stderr, "aotx_attend_paged_static: no page pool is open on this process\n");
         return 1;
     }
+    unsigned char *base = aotx_attn_static_ptr();
+    if (base == nullptr) return 1;
+    float *partial = (float *)base;
+    unsigned int *count = (unsigned int *)(base + AOTX_ATTN_STATIC_PARTIAL);
+    /* the shape is checked before anything is enqueued */
+    aotx_attn_args plan;
+    if (aotx_attend_plan(&plan, (const unsigned short *)q, (unsigned short *)out, pos, agent,
+                         nullptr, tokens, heads, kv_heads, head_dim, layer, layers,
+                         AOTX_SEQ_MAX_TOKENS, partial, count) != 0)
+        return 1;
     /* the scratch this launch needs must fit the fixed array */
     const unsigned int splits = aotx_attn_splits(tokens, kv_heads, AOTX_SEQ_MAX_TOKENS);
     const size_t units = (size_t)tokens * kv_heads;
@@ -263,10 +252,6 @@ extern "C" int aotx_attend_paged_static(const void *q, const unsigned int *pos,
                 kv_heads, need, units, AOTX_ATTN_STATIC_PARTIAL, AOTX_ATTN_STATIC_COUNTS);
         return 1;
     }
-    unsigned char *base = aotx_attn_static_ptr();
-    if (base == nullptr) return 1;
-    float *partial = (float *)base;
-    unsigned int *count = (unsigned int *)(base + AOTX_ATTN_STATIC_PARTIAL);
     hipStream_t s = aotx_stream(stream);
     /* counters start at zero (a fill kernel, which a graph capture may hold) */
     hipLaunchKernelGGL(aotx_attn_clear_kernel, dim3(((unsigned int)units + 255u) / 256u), dim3(256),

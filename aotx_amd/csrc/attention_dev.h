@@ -176,7 +176,8 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
 template <int D, int G, int W, int QT>
 static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a, unsigned int bx)
 {
-    constexpr int C = G * QT;           /* score columns: QT queries x G heads */
+    static_assert(QT == 1, "one query per workgroup: prompt pieces take aotx_attend_runs");
+    constexpr int C = G * QT;           /* score columns: G heads */
     static_assert(C <= 16, "one MFMA tile of query columns");
     constexpr int KK = D / 32;          /* score MFMA steps */
     constexpr int VP = D / 32;          /* 16-byte value pieces per lane per block */
@@ -197,70 +198,32 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     unsigned int tokens = a.m_dev != nullptr ? counted : a.tokens;
     unsigned int S, c, kh, t, n, st, p0, p1, nq = 1u, plim;
     unsigned int agent;
-    if constexpr (QT == 1) {
-        S = a.splits;
-        /* chunk-major: the workgroups of one chunk index are consecutive, so they spread
-         * over every XCD whichever chunks are empty (dispatch goes round the XCDs) */
-        const unsigned int units = a.tokens * a.kv_heads;
-        c = bx / units;
-        const unsigned int rest = bx - c * units;
-        kh = rest % a.kv_heads;
-        t = rest / a.kv_heads;
-        /* the token's position and slot are read before its row count is known (t is below
-         * the launch's token capacity, so both words exist): one memory round trip for all
-         * three, where a load after the count's test would wait for the count first */
-        const unsigned int pos_t = a.pos[t];
-        agent = a.agent[t];
-        __builtin_amdgcn_sched_barrier(0);
-        if (tokens > a.tokens) tokens = a.tokens;
-        /* the test reads both words, so neither load is sunk past it (a position of all
-         * ones, which no sequence reaches, would end the workgroup as a token past the
-         * count does) */
-        if (t >= tokens || (pos_t & agent) == 0xFFFFFFFFu) return;
-        n = pos_t + 1u;
-        const unsigned int chunk = aotx_attn_chunk(n, S);
-        st = (n + chunk - 1u) / chunk;
-        if (c >= st) return;
-        p0 = c * chunk;
-        p1 = (p0 + chunk < n) ? p0 + chunk : n;
-        plim = p1;
-    } else {
-        /* a prompt piece: the workgroup of token t leads when t starts its sequence's run
-         * in the batch or sits at a multiple of QT, and takes the next tokens of the same
-         * sequence up to the next multiple; every query reads the keys once */
-        if (tokens > a.tokens) tokens = a.tokens;
-        S = 1u;
-        c = 0u;
-        st = 1u;
-        kh = bx % a.kv_heads;
-        t = bx / a.kv_heads;
-        if (t >= tokens) return;
-        /* one round trip for every word the test needs: lane i holds the slot and position
-         * of token t - 1 + i (i <= QT; lane 0 a token before the batch, or one past it, holds
-         * no slot: all ones) */
-        const unsigned int ti = t + lane - 1u;
-        unsigned int ag = 0xFFFFFFFFu, ps = 0u;
-        if (lane <= (unsigned int)QT && (lane != 0u || t != 0u) && ti < tokens) {
-            ag = a.agent[ti];
-            ps = a.pos[ti];
-        }
-        const unsigned int agent0 = (unsigned int)__shfl((int)ag, 1, 64);
-        const unsigned int pos0 = (unsigned int)__shfl((int)ps, 1, 64);
-        const unsigned int agent_prev = (unsigned int)__shfl((int)ag, 0, 64);
-        if (t != 0u && agent_prev == agent0 && pos0 % QT != 0u) return;
-        /* the run: tokens t + 1 .. of the same slot off a multiple of QT (lanes 2 ..) */
-        const bool more = lane >= 2u && lane <= (unsigned int)QT && ag == agent0 && ps % QT != 0u;
-        const unsigned long long run = (unsigned long long)__ballot(more) >> 2;
-        nq = 1u + (unsigned int)__builtin_ctzll(~run);
-        if (nq > (unsigned int)QT) nq = QT;
-        n = (unsigned int)__shfl((int)ps, (int)nq, 64) + 1u;
-        agent = agent0;
-        p0 = 0u;
-        p1 = n;
-        /* this lane's column: query r / G; a column with no query sees position 0 only */
-        const unsigned int qpos = (unsigned int)__shfl((int)ps, (int)(r / (unsigned int)G) + 1, 64);
-        plim = r / (unsigned int)G < nq ? qpos + 1u : 1u;
-    }
+    S = a.splits;
+    /* chunk-major: the workgroups of one chunk index are consecutive, so they spread
+     * over every XCD whichever chunks are empty (dispatch goes round the XCDs) */
+    const unsigned int units = a.tokens * a.kv_heads;
+    c = bx / units;
+    const unsigned int rest = bx - c * units;
+    kh = rest % a.kv_heads;
+    t = rest / a.kv_heads;
+    /* the token's position and slot are read before its row count is known (t is below
+     * the launch's token capacity, so both words exist): one memory round trip for all
+     * three, where a load after the count's test would wait for the count first */
+    const unsigned int pos_t = a.pos[t];
+    agent = a.agent[t];
+    __builtin_amdgcn_sched_barrier(0);
+    if (tokens > a.tokens) tokens = a.tokens;
+    /* the test reads both words, so neither load is sunk past it (a position of all
+     * ones, which no sequence reaches, would end the workgroup as a token past the
+     * count does) */
+    if (t >= tokens || (pos_t & agent) == 0xFFFFFFFFu) return;
+    n = pos_t + 1u;
+    const unsigned int chunk = aotx_attn_chunk(n, S);
+    st = (n + chunk - 1u) / chunk;
+    if (c >= st) return;
+    p0 = c * chunk;
+    p1 = (p0 + chunk < n) ? p0 + chunk : n;
+    plim = p1;
     const unsigned int nblk = (p1 - p0 + 15u) / 16u;
     const unsigned int per = (nblk + W - 1u) / W;
     const unsigned int b0 = p0 / 16u + wave * per;

@@ -239,7 +239,7 @@ int aotx_launch_expert_ffn(const aotx_expert_plan &p, const unsigned short *x,
         aotx_gemv_args q = a;
         q.m0 = 32u * i;
         q.m = 32u;
-        aotx_gemv_launch(q, s);
+        if (aotx_gemv_launch(q, s) != 0) return 1;
     }
     /* down, per expert, into the routed slot rows */
     const void *dw[1] = {p.down};
@@ -262,7 +262,7 @@ int aotx_launch_expert_ffn(const aotx_expert_plan &p, const unsigned short *x,
         aotx_gemv_args q = b;
         q.m0 = 32u * i;
         q.m = 32u;
-        aotx_gemv_launch(q, s);
+        if (aotx_gemv_launch(q, s) != 0) return 1;
     }
     return 0;
 }

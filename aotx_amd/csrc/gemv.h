@@ -76,7 +76,7 @@ int aotx_gemv_plan(aotx_gemv_args *a, const void *const *w, const unsigned int *
 
 /* Launch the product on rows [m0, m0 + mt) of x, mt <= 32; m is the host row count or
  * the device count at m_dev. Scratch comes from the library. */
-void aotx_gemv_launch(aotx_gemv_args a, hipStream_t stream);
+int aotx_gemv_launch(aotx_gemv_args a, hipStream_t stream);    /* 1 when refused */
 
 /* Raise the LDS limit of the kernels (once; outside any stream capture). */
 void aotx_gemv_init(void);
@@ -85,6 +85,6 @@ void aotx_gemv_init(void);
 size_t aotx_gemv_scratch_partial(const aotx_gemv_args &a);
 
 /* The product for any row count: passes of 32 rows. */
-void aotx_gemv_run(aotx_gemv_args a, unsigned int m, hipStream_t stream);
+int aotx_gemv_run(aotx_gemv_args a, unsigned int m, hipStream_t stream);
 
 #endif

@@ -469,14 +469,14 @@ void aotx_gemv_init(void)
 }
 
 template <int MT, int CB>
-static void aotx_gemv_go(const aotx_gemv_args &a, hipStream_t stream)
+static int aotx_gemv_go(const aotx_gemv_args &a, hipStream_t stream)
 {
     size_t lds = aotx_gemv_lds(a, MT);
     aotx_gemv_init();
     if (lds + 64u > aotx_gemv_lds_limit) {
         fprintf(stderr, "aotx: the product needs %zu bytes of LDS, the device gives %zu\n",
                 lds, aotx_gemv_lds_limit);
-        exit(1);
+        return 1;
     }
     unsigned int ey = a.expert_stride != 0ull ? a.experts : 1u;
     hipLaunchKernelGGL((aotx_gemv_q8<MT, CB>), dim3(a.groups * a.splits, ey), dim3(GEMV_THREADS),
@@ -486,19 +486,20 @@ static void aotx_gemv_go(const aotx_gemv_args &a, hipStream_t stream)
         hipLaunchKernelGGL((aotx_gemv_reduce<MT>), dim3(a.groups), dim3(GEMV_THREADS), 0, stream, a);
         AOTX_LAUNCH_CHECK();
     }
+    return 0;
 }
 
 template <int MT>
-static void aotx_gemv_cb(const aotx_gemv_args &a, hipStream_t stream)
+static int aotx_gemv_cb(const aotx_gemv_args &a, hipStream_t stream)
 {
     bool aligned = (a.row_bytes % 16ull) == 0ull;
-    if (aligned && a.cb == 32u) aotx_gemv_go<MT, 32>(a, stream);
-    else if (aligned && a.cb == 16u) aotx_gemv_go<MT, 16>(a, stream);
-    else if (aligned && a.cb == 8u) aotx_gemv_go<MT, 8>(a, stream);
-    else aotx_gemv_go<MT, 0>(a, stream);
+    if (aligned && a.cb == 32u) return aotx_gemv_go<MT, 32>(a, stream);
+    if (aligned && a.cb == 16u) return aotx_gemv_go<MT, 16>(a, stream);
+    if (aligned && a.cb == 8u) return aotx_gemv_go<MT, 8>(a, stream);
+    return aotx_gemv_go<MT, 0>(a, stream);
 }
 
-void aotx_gemv_launch(aotx_gemv_args a, hipStream_t stream)
+int aotx_gemv_launch(aotx_gemv_args a, hipStream_t stream)
 {
     /* With a device row count, a.m is the capacity of the pass (16 or 32). */
     unsigned int mt_need = a.m;
@@ -506,19 +507,20 @@ void aotx_gemv_launch(aotx_gemv_args a, hipStream_t stream)
         a.partial = (float *)aotx_scratch(AOTX_SCRATCH_GEMV_PARTIAL,
                                           (size_t)a.groups * a.splits * 64u * 32u * sizeof(float));
     }
-    if (mt_need <= 16u) aotx_gemv_cb<16>(a, stream);
-    else aotx_gemv_cb<32>(a, stream);
+    if (mt_need <= 16u) return aotx_gemv_cb<16>(a, stream);
+    return aotx_gemv_cb<32>(a, stream);
 }
 
-void aotx_gemv_run(aotx_gemv_args a, unsigned int m, hipStream_t stream)
+int aotx_gemv_run(aotx_gemv_args a, unsigned int m, hipStream_t stream)
 {
     for (unsigned int m0 = 0; m0 < m; m0 += 32u) {
         aotx_gemv_args p = a;
         p.m0 = m0;
         p.m = (m - m0 < 32u) ? (m - m0) : 32u;
         p.m_dev = nullptr;
-        aotx_gemv_launch(p, stream);
+        if (aotx_gemv_launch(p, stream) != 0) return 1;
     }
+    return 0;
 }
 
 /* ---------------------------------------------------------------------------------------
@@ -538,8 +540,7 @@ static int aotx_q8_gemv_any(const void *w, unsigned int n, unsigned int k, const
     a.ldx = k;
     a.y = y;
     a.ldy = n;
-    aotx_gemv_run(a, m, aotx_stream(stream));
-    return 0;
+    return aotx_gemv_run(a, m, aotx_stream(stream));
 }
 
 extern "C" int aotx_q8_gemv(const void *w, unsigned int n, unsigned int k, const void *x,

@@ -18,8 +18,8 @@
  *
  * Every kernel reads the batch from the device copy of the call block, so one captured
  * graph serves every call whose token count fits its bucket (1, 2, 4, ..., max_tokens);
- * graphs are captured on first use of a bucket and replayed after (AOTX_GRAPHS=0 launches
- * the same kernels eagerly).
+ * graphs are captured on first use of a bucket and replayed after (aotx_model_graphs(0)
+ * records a fresh graph for every call instead).
  */
 #include "aotx_internal.h"
 #include "../../include/aotx_plan.h"
@@ -39,6 +39,7 @@ unsigned long long aotx_mem_weights_bytes(void);
 #define AOTX_BUCKETS 10u   /* 1, 2, 4, ..., 512 */
 #define AOTX_WIDE_PASSES 4u        /* 32-row passes of a wide product in one launch */
 #define AOTX_GEMV_COUNTS 65536u   /* split arrival counters: experts x product groups */
+#define AOTX_PIECES 48u            /* device buffers of one role */
 
 /* The operands of a decode tick; a tick graph is captured for one set of them. */
 struct aotx_tick_setup {
@@ -61,6 +62,7 @@ struct aotx_rlayer {
 struct aotx_hold {
     int ready;
     int record_failed;      /* a launch of the step being recorded was refused */
+    int take_failed;        /* open ran out of buffer places */
     int described;
     aotx_model_desc desc;
     unsigned int role;
@@ -95,7 +97,7 @@ struct aotx_hold {
     float *ey;
     unsigned short *eact;
     unsigned int *elist, *ecount;
-    void *piece[48];
+    void *piece[AOTX_PIECES];
     unsigned int pieces;
     /* the decode tick (aotx_decode_tick): the step's outputs, the sampler's adjustment
      * scratch, and one graph per token bucket with the operands it was captured for */
@@ -105,8 +107,9 @@ struct aotx_hold {
     float *pen_raw;
     aotx_tick_setup tick_setup[AOTX_BUCKETS];
     hipGraphExec_t tick_exec[AOTX_BUCKETS];
-    /* graphs per row selection, token bucket and head-row bucket */
-    hipGraphExec_t exec[2][AOTX_BUCKETS][AOTX_BUCKETS];
+    /* graphs per residual capture (probe calls that ask for it), row selection, token
+     * bucket and head-row bucket */
+    hipGraphExec_t exec[2][2][AOTX_BUCKETS][AOTX_BUCKETS];
     unsigned int nodes;
 };
 
@@ -116,6 +119,12 @@ static int aotx_is_language(unsigned int role)
 {
     return role == AOTX_MODEL_LANGUAGE || role == AOTX_MODEL_LANGUAGE_Q4
         || role == AOTX_MODEL_LANGUAGE_AUDIO;
+}
+
+/* The roles whose passes end in a head of their own instead of the vocabulary head. */
+static int aotx_is_head_role(unsigned int role)
+{
+    return role == AOTX_MODEL_EMBEDDING || role == AOTX_MODEL_RERANKER;
 }
 
 static const unsigned char *aotx_tensor(unsigned long long off)
@@ -135,12 +144,14 @@ static void *aotx_take(aotx_hold *h, size_t bytes)
 {
     void *p = nullptr;
     if (bytes == 0u) bytes = 256u;
+    if (h->pieces >= AOTX_PIECES) {
+        /* open checks the flag and refuses */
+        fprintf(stderr, "aotx: a role holds at most %u buffers\n", AOTX_PIECES);
+        h->take_failed = 1;
+        return nullptr;
+    }
     AOTX_CHECK(hipMalloc(&p, bytes));
     AOTX_CHECK(hipMemset(p, 0, bytes));
-    if (h->pieces >= 48u) {
-        fprintf(stderr, "aotx: too many buffers\n");
-        exit(1);
-    }
     h->piece[h->pieces++] = p;
     return p;
 }
@@ -218,7 +229,9 @@ extern "C" unsigned int aotx_model_kv_pages(unsigned int role, unsigned int cont
 
 extern "C" int aotx_model_set_desc(unsigned int role, const aotx_model_desc *desc)
 {
-    if (role >= AOTX_MODEL_ROLES || desc == nullptr || !aotx_is_language(role)) return 1;
+    if (role >= AOTX_MODEL_ROLES || desc == nullptr
+        || (!aotx_is_language(role) && !aotx_is_head_role(role)))
+        return 1;
     if (!aotx_desc_ok(desc)) return 1;
     aotx_hold *h = &aotx_holds[role];
     if (h->ready) return 1;
@@ -242,16 +255,7 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
      * 10.15 -> 8.49 ms against passes of 32 rows, while at 64 rows its few workgroups are
      * slower than re-reading the weights per 32 rows: the Mixtral-shape step 17.2 -> 19.3
      * ms); routed experts keep passes of 32 rows through their row lists */
-    static const bool gemm_on = [] {
-        const char *v = getenv("AOTX_GEMM");       /* 0: 32-row passes, for comparison */
-        return !(v != nullptr && v[0] == '0');
-    }();
-    static const unsigned int gemm_min = [] {
-        const char *v = getenv("AOTX_GEMM_MIN");   /* the smallest pass for the GEMM (sweeps) */
-        const unsigned int m = v != nullptr ? (unsigned int)atoi(v) : 0u;
-        return m >= 33u && m <= AOTX_RGEMM_ROWS ? m : 128u;
-    }();
-    const bool gemm = gemm_on && cap >= gemm_min && tmpl.expert_stride == 0ull && tmpl.list == nullptr
+    const bool gemm = cap >= 128u && tmpl.expert_stride == 0ull && tmpl.list == nullptr
                    && tmpl.xrow == nullptr && tmpl.xmode == AOTX_X_F16;
     for (unsigned int m0 = 0, mt = 0; m0 < cap; m0 += mt) {
         mt = gemm ? (cap - m0 < AOTX_RGEMM_ROWS ? cap - m0 : AOTX_RGEMM_ROWS)
@@ -292,7 +296,10 @@ static void aotx_rproduct(aotx_hold *h, const void *const *w, const unsigned int
             }
             a.count = h->gemv_count;
         }
-        aotx_rgemv_launch(a, h->stream);
+        if (aotx_rgemv_launch(a, h->stream) != 0) {
+            h->record_failed = 1;
+            return;
+        }
     }
 }
 
@@ -329,8 +336,11 @@ static void aotx_roperands(aotx_rgemv_args *p, const aotx_rgemv_args &tmpl)
 
 /* ---- the step ---------------------------------------------------------------------- */
 
+/* Records one step on h->stream. A refused launch sets h->record_failed and ends the
+ * recording at once; the callers record under stream capture and then drop the graph, so
+ * nothing of a refused step runs. capture: the probe's residual rows after every layer. */
 static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt, unsigned int br,
-                             const aotx_tick_setup *tk)
+                             const aotx_tick_setup *tk, bool capture)
 {
     (void)sel_all;    /* the head's rows are selected on the device from the call block */
     const aotx_model_desc *d = &h->desc;
@@ -353,21 +363,11 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
      * norm's and the down products' output) and of O (the attention's) are written in the
      * fragment layout and read by the fragment product, whose waves load their MFMA
      * operands straight from it; gate/up and down keep the wide kernel, measured faster
-     * there (AOTX_FRAG=0 keeps the row layout everywhere, for comparison) */
-    static const bool frag_on = [] {
-        const char *v = getenv("AOTX_FRAG");
-        return !(v != nullptr && v[0] == '0');
-    }();
+     * there */
     const bool frag_dims = d->hidden % 128u == 0u && wide % 128u == 0u && d->ffn % 128u == 0u;
-    const bool frag = frag_on && scaled_x && T <= AOTX_XFRAG_ROWS && frag_dims;
-    const bool head_frag = frag_on && d->hidden % 128u == 0u && R > AOTX_NARROW_ROWS
-                        && R <= AOTX_XFRAG_ROWS;
+    const bool frag = scaled_x && T <= AOTX_XFRAG_ROWS && frag_dims;
+    const bool head_frag = d->hidden % 128u == 0u && R > AOTX_NARROW_ROWS && R <= AOTX_XFRAG_ROWS;
     const int xmode_in = frag ? AOTX_X_FRAG : AOTX_X_F16;
-    static const bool frag_down_on = [] {
-        const char *v = getenv("AOTX_FRAG_DOWN");
-        return v != nullptr && v[0] == '1';
-    }();
-    const bool frag_down = frag && frag_down_on;
 
     if (tk != nullptr) {
         /* the tick: the plan packs the batch on the device and the call block points at it */
@@ -438,11 +438,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             t.qkv.theta = d->rope_theta;
             t.qkv.factor = (const float *)aotx_tensor(d->rope_freqs);
             aotx_rproduct(h, qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_QKV, T, m_tokens, t);
+            if (h->record_failed) return;
         } else {
             aotx_rgemv_args t = x_in;
             t.y = h->qkv;
             t.ldy = wide + 2u * narrow;
             aotx_rproduct(h, qkv_w, qkv_rows, 3u, d->hidden, AOTX_EPI_F32, T, m_tokens, t);
+            if (h->record_failed) return;
             aotx_rope_args r;
             memset(&r, 0, sizeof r);
             r.m_dev = m_tokens;
@@ -492,6 +494,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             const void *o_w[1] = {RL->o};
             unsigned int o_rows[1] = {d->hidden};
             aotx_rproduct(h, o_w, o_rows, 1u, wide, AOTX_EPI_RESID, T, m_tokens, t);
+            if (h->record_failed) return;
         }
 
         /* ---- feed-forward half ---- */
@@ -520,6 +523,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             unsigned int gu_rows[2] = {d->ffn, d->ffn};
             /* an expert takes at most every token once */
             aotx_rproduct(h, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, nullptr, t);
+            if (h->record_failed) return;
             aotx_rgemv_args u = t;
             u.x = h->eact;
             u.ldx = d->ffn;
@@ -530,6 +534,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             const void *dn_w[1] = {RL->down};
             unsigned int dn_rows[1] = {d->hidden};
             aotx_rproduct(h, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_F32, T, nullptr, u);
+            if (h->record_failed) return;
             aotx_expert_resid_args er;
             er.m_dev = m_tokens;
             er.resid = h->resid;
@@ -559,13 +564,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             }
             t.y = h->act;
             t.ldy = d->ffn;
-            t.out_frag = frag_down ? 1u : 0u;
             const void *gu_w[2] = {RL->gate, RL->up};
             unsigned int gu_rows[2] = {d->ffn, d->ffn};
             aotx_rproduct(h, gu_w, gu_rows, 2u, d->hidden, AOTX_EPI_SWIGLU, T, m_tokens, t);
+            if (h->record_failed) return;
             aotx_rgemv_args u;
             memset(&u, 0, sizeof u);
-            u.xmode = frag_down ? AOTX_X_FRAG : AOTX_X_F16;
+            u.xmode = AOTX_X_F16;
             u.x = h->act;
             u.ldx = d->ffn;
             u.y = h->resid;
@@ -579,7 +584,21 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             const void *dn_w[1] = {RL->down};
             unsigned int dn_rows[1] = {d->hidden};
             aotx_rproduct(h, dn_w, dn_rows, 1u, d->ffn, AOTX_EPI_RESID, T, m_tokens, u);
+            if (h->record_failed) return;
         }
+        if (capture) aotx_launch_capture(h->step, h->resid, d->hidden, l, s);
+    }
+    /* the embedding and rank roles end in their own heads over each sequence's last row
+     * (cuda/model/graph_host.cu:115-126) */
+    if (aotx_is_head_role(h->role)) {
+        const float *out_w = (const float *)aotx_tensor(d->output_norm);
+        if (h->role == AOTX_MODEL_EMBEDDING)
+            aotx_launch_pool(h->step, h->resid, out_w, d->hidden, d->rms_eps, s);
+        else
+            aotx_launch_score(h->step, h->resid, out_w, aotx_tensor(d->cls_output), d->weight_type,
+                              d->hidden, d->rms_eps, s);
+        aotx_launch_shut_rows(h->step, s);
+        return;
     }
     /* output head on the selected rows (each sequence's last token, or every token) */
     {
@@ -607,6 +626,7 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
         const void *hw[1] = {h->rhead};
         unsigned int hrows[1] = {d->vocab};
         aotx_rproduct(h, hw, hrows, 1u, d->hidden, AOTX_EPI_F32, R, m_rows, t);
+        if (h->record_failed) return;
     }
     aotx_pen_args pen;
     if (tk != nullptr) {
@@ -644,10 +664,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
 
 /* ---- lifecycle ----------------------------------------------------------------------- */
 
-static int aotx_use_graphs(void)
+/* Keep each bucket's recorded graph for the calls after (1, the default), or record a
+ * fresh graph for every call (0, aotx_model_graphs). */
+static int aotx_graph_cache = 1;
+
+extern "C" void aotx_model_graphs(unsigned int keep)
 {
-    const char *v = getenv("AOTX_GRAPHS");
-    return !(v != nullptr && v[0] == '0');
+    aotx_graph_cache = keep != 0u ? 1 : 0;
 }
 
 extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
@@ -660,6 +683,13 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
         return 1;
     }
     const aotx_model_desc *d = &h->desc;
+    if (role == AOTX_MODEL_RERANKER
+        && (d->cls_output == AOTX_MODEL_ABSENT
+            || (d->weight_type != AOTX_WEIGHT_Q8_0 && d->weight_type != AOTX_WEIGHT_F16
+                && d->weight_type != AOTX_WEIGHT_F32))) {
+        fprintf(stderr, "aotx: the rank role needs a class head of Q8_0, F16 or F32\n");
+        return 1;
+    }
     aotx_gemv_init();
     aotx_state_device();
     /* the token capacity is a power of two, so every bucket of a call fits */
@@ -807,9 +837,17 @@ extern "C" int aotx_model_open(unsigned int role, unsigned int max_tokens)
         h->elist = (unsigned int *)aotx_take(h, (size_t)d->expert_count * slots * 4u);
         h->ecount = (unsigned int *)aotx_take(h, (size_t)d->expert_count * 4u);
     }
+    h->step = (aotx_step *)aotx_take(h, sizeof(aotx_step));
+    if (h->take_failed) {
+        for (unsigned int i = 0; i < h->pieces; ++i) AOTX_CHECK(hipFree(h->piece[i]));
+        aotx_model_desc keep = h->desc;
+        memset(h, 0, sizeof *h);
+        h->desc = keep;
+        h->described = 1;
+        return 1;
+    }
     AOTX_CHECK(hipHostMalloc((void **)&h->pinned, sizeof(aotx_step), hipHostMallocDefault));
     memset(h->pinned, 0, sizeof(aotx_step));
-    h->step = (aotx_step *)aotx_take(h, sizeof(aotx_step));
     AOTX_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     AOTX_CHECK(hipDeviceSynchronize());
     h->ready = 1;
@@ -822,10 +860,12 @@ extern "C" void aotx_model_shut(unsigned int role)
     aotx_hold *h = &aotx_holds[role];
     if (!h->ready) return;
     AOTX_CHECK(hipStreamSynchronize(h->stream));
-    for (unsigned int a = 0; a < 2u; ++a)
-        for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
-            for (unsigned int j = 0; j < AOTX_BUCKETS; ++j)
-                if (h->exec[a][i][j] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->exec[a][i][j]));
+    for (unsigned int c = 0; c < 2u; ++c)
+        for (unsigned int a = 0; a < 2u; ++a)
+            for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
+                for (unsigned int j = 0; j < AOTX_BUCKETS; ++j)
+                    if (h->exec[c][a][i][j] != nullptr)
+                        AOTX_CHECK(hipGraphExecDestroy(h->exec[c][a][i][j]));
     for (unsigned int i = 0; i < AOTX_BUCKETS; ++i)
         if (h->tick_exec[i] != nullptr) AOTX_CHECK(hipGraphExecDestroy(h->tick_exec[i]));
     AOTX_CHECK(hipStreamDestroy(h->stream));
@@ -899,47 +939,53 @@ extern "C" int aotx_model_launch(unsigned int role, const aotx_model_run *set)
     if (!h->ready || set->tokens > h->max_tokens || set->rows > h->max_rows || set->seqs > AOTX_SLOTS)
         return 1;
     if (set->tokens == 0u || set->seqs == 0u || set->rows == 0u) return 1;
-    if (set->pooled != nullptr || set->score != nullptr || set->capture != nullptr) return 1;
+    /* residual capture: up to one slot per layer, the layer list in device memory; pooled
+     * and score are written by the embedding and rank roles' heads (other roles leave them
+     * untouched, as the reference's graphs do) */
+    if (set->capture != nullptr && set->capture_count != 0u
+        && (set->capture_count > AOTX_MODEL_MAX_LAYERS || set->capture_layer == nullptr))
+        return 1;
     if (set->token != nullptr && set->select != AOTX_MODEL_ROWS_LAST) return 1;
+    if (set->token != nullptr && aotx_is_head_role(role)) return 1;   /* no sampler there */
     if (set->select == AOTX_MODEL_ROWS_LAST && set->rows != set->seqs) return 1;
     if (set->select == AOTX_MODEL_ROWS_ALL && set->rows != set->tokens) return 1;
     h->pinned->run = *set;
+    const unsigned int cap = set->capture != nullptr && set->capture_count != 0u ? 1u : 0u;
     unsigned int bt = aotx_bucket_of(set->tokens);
     unsigned int br = aotx_bucket_of(set->rows);
     unsigned int all = set->select == AOTX_MODEL_ROWS_ALL ? 1u : 0u;
-    if (aotx_use_graphs()) {
-        hipGraphExec_t &exec = h->exec[all][bt][br];
-        if (exec == nullptr) {
-            hipGraph_t graph = nullptr;
-            AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
-            h->record_failed = 0;
-            aotx_record_step(h, all, bt, br, nullptr);
-            AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
-            if (h->record_failed) {
-                AOTX_CHECK(hipGraphDestroy(graph));
-                return 1;
-            }
-            size_t count = 0;
-            AOTX_CHECK(hipGraphGetNodes(graph, nullptr, &count));
-            if ((unsigned int)count > h->nodes) h->nodes = (unsigned int)count;
-            AOTX_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-            AOTX_CHECK(hipGraphDestroy(graph));
-        }
-        AOTX_CHECK(hipGraphLaunch(exec, h->stream));
-    } else {
+    hipGraphExec_t &exec = h->exec[cap][all][bt][br];
+    if (exec == nullptr) {
+        /* recorded under stream capture: a refused launch leaves a graph that is dropped,
+         * so nothing of the step runs */
+        hipGraph_t graph = nullptr;
+        AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
         h->record_failed = 0;
-        aotx_record_step(h, all, bt, br, nullptr);
+        aotx_record_step(h, all, bt, br, nullptr, cap != 0u);
+        AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
         if (h->record_failed) {
-            aotx_wait(h->stream);
+            AOTX_CHECK(hipGraphDestroy(graph));
             return 1;
         }
+        size_t count = 0;
+        AOTX_CHECK(hipGraphGetNodes(graph, nullptr, &count));
+        if ((unsigned int)count > h->nodes) h->nodes = (unsigned int)count;
+        AOTX_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        AOTX_CHECK(hipGraphDestroy(graph));
     }
-    if (set->logits != nullptr) {
+    AOTX_CHECK(hipGraphLaunch(exec, h->stream));
+    hipGraphExec_t drop = nullptr;        /* dropped once the call has waited for it */
+    if (!aotx_graph_cache) {
+        drop = exec;
+        exec = nullptr;
+    }
+    if (set->logits != nullptr && !aotx_is_head_role(role)) {
         AOTX_CHECK(hipMemcpyAsync(set->logits, h->logits,
                                   (size_t)set->rows * h->desc.vocab * sizeof(float),
                                   hipMemcpyDeviceToDevice, h->stream));
     }
     aotx_wait(h->stream);
+    if (drop != nullptr) AOTX_CHECK(hipGraphExecDestroy(drop));
     return 0;
 }
 
@@ -953,7 +999,8 @@ extern "C" int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *t
                                 unsigned int capacity, float *logits)
 {
     if (role >= AOTX_MODEL_ROLES || slots == nullptr || tokens == nullptr || plan == nullptr
-        || stride == 0u || (records == nullptr && capacity != 0u))
+        || stride == 0u || (records == nullptr && capacity != 0u)
+        || aotx_is_head_role(role))
         return 1;
     aotx_hold *h = &aotx_holds[role];
     if (!h->ready) return 1;
@@ -991,7 +1038,7 @@ extern "C" int aotx_decode_tick(unsigned int role, aotx_plan_slot *slots, int *t
         hipGraph_t graph = nullptr;
         AOTX_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
         h->record_failed = 0;
-        aotx_record_step(h, 0u, bt, br, &tk);
+        aotx_record_step(h, 0u, bt, br, &tk, false);
         AOTX_CHECK(hipStreamEndCapture(h->stream, &graph));
         if (h->record_failed) {
             AOTX_CHECK(hipGraphDestroy(graph));
@@ -1054,6 +1101,19 @@ extern "C" int aotx_model_sample(unsigned int role, const int *ids, const unsign
     int state = aotx_model_launch(role, &set);
     if (state == 0 && seed != nullptr) *seed = how->seed;
     return state;
+}
+
+/* The rank role's pass (call_host.cu:58-69): the score of each sequence from its last
+ * row. */
+extern "C" int aotx_model_rerank(const int *ids, const unsigned int *offset, unsigned int seqs,
+                                 const unsigned int *agent, float *score)
+{
+    aotx_model_run set;
+    if (aotx_call_set(&set, ids, offset, seqs, agent) != 0) return 1;
+    set.score = score;
+    set.select = AOTX_MODEL_ROWS_LAST;
+    set.rows = seqs;
+    return aotx_model_launch(AOTX_MODEL_RERANKER, &set);
 }
 
 extern "C" int aotx_model_prefill(unsigned int role, const int *ids, const unsigned int *offset,

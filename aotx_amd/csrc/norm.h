@@ -63,5 +63,13 @@ void aotx_launch_norm(const aotx_norm_args &a, unsigned int max_tokens, hipStrea
 void aotx_launch_expert_resid(const aotx_expert_resid_args &a, unsigned int max_tokens,
                               hipStream_t s);
 void aotx_launch_rope(const aotx_rope_args &a, unsigned int max_tokens, hipStream_t s);
+/* the probe's residual capture after one layer; the embedding and rank heads */
+void aotx_launch_capture(const aotx_step *step, const float *resid, unsigned int hidden,
+                         unsigned int layer, hipStream_t s);
+void aotx_launch_pool(const aotx_step *step, const float *resid, const float *norm_w,
+                      unsigned int hidden, float eps, hipStream_t s);
+void aotx_launch_score(const aotx_step *step, const float *resid, const float *norm_w,
+                       const unsigned char *cls, unsigned int type, unsigned int hidden,
+                       float eps, hipStream_t s);
 
 #endif

@@ -277,6 +277,106 @@ __global__ void aotx_rope_kernel(aotx_rope_args a)
 /* ---------------------------------------------------------------------------------------
  * Host launchers
  * ------------------------------------------------------------------------------------- */
+/* Residual capture of the probe (cuda/model/conduct.cu:99-178, the capture at :165-173):
+ * after layer `layer`, the residual row of each sequence's last token goes to capture
+ * slot c for every c whose named layer is this one, laid out [c][seq][hidden]. One block
+ * per sequence. (The reference adds registered steer vectors in the same kernel; this
+ * build has no steer registry, so there is nothing to add, as in the reference with no
+ * vector registered.) */
+__global__ __launch_bounds__(256) void aotx_capture_kernel(const aotx_step *step,
+                                                           const float *resid,
+                                                           unsigned int hidden,
+                                                           unsigned int layer)
+{
+    const aotx_model_run *run = &step->run;
+    const unsigned int s = blockIdx.x;
+    if (run->capture == nullptr || s >= run->seqs) return;
+    const unsigned int row = run->offset[s + 1u] - 1u;
+    if (row >= run->tokens) return;
+    const float *src = resid + (unsigned long long)row * hidden;
+    for (unsigned int c = 0; c < run->capture_count; ++c) {
+        if (run->capture_layer[c] != layer) continue;
+        float *dst = run->capture + ((unsigned long long)c * run->seqs + s) * hidden;
+        for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) dst[d] = src[d];
+    }
+}
+
+/* The embedding head (cuda/embed/embed.cu:8-65): for each sequence, its last residual row
+ * under the last RMSNorm in fp32, scaled to unit length, into pooled[seq][hidden]. One
+ * block per sequence. */
+__global__ __launch_bounds__(256) void aotx_pool_kernel(const aotx_step *step, const float *resid,
+                                                        const float *norm_w, unsigned int hidden,
+                                                        float eps)
+{
+    __shared__ float share[4];
+    const aotx_model_run *run = &step->run;
+    const unsigned int s = blockIdx.x;
+    if (run->pooled == nullptr || s >= run->seqs) return;
+    const unsigned int row = run->offset[s + 1u] - 1u;
+    if (row >= run->tokens) return;
+    const float *r = resid + (unsigned long long)row * hidden;
+    float sq = 0.0f;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) sq += r[d] * r[d];
+    const float scale = rsqrtf(aotx_block_sum(sq, share) / (float)hidden + eps);
+    float len = 0.0f;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
+        const float v = scale * r[d] * norm_w[d];
+        len += v * v;
+    }
+    len = aotx_block_sum(len, share);
+    const float unit = len > 0.0f ? rsqrtf(len) : 0.0f;
+    float *out = run->pooled + (unsigned long long)s * hidden;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x)
+        out[d] = scale * r[d] * norm_w[d] * unit;
+}
+
+/* One weight of a row of the class head: Q8_0 blocks (fp32 scale times the quant, as the
+ * reference's reader cuda/model/blocks.cuh:96-105), fp16 or fp32. */
+static __device__ __forceinline__ float aotx_cls_at(const unsigned char *w, unsigned int type,
+                                                    unsigned long long i)
+{
+    if (type == AOTX_WEIGHT_Q8_0) {
+        const unsigned char *b = w + (i / 32ull) * 34ull;
+        const float scale = aotx_h2f((unsigned short)(b[0] | (b[1] << 8)));
+        return scale * (float)(int)(signed char)b[2u + (unsigned int)(i % 32ull)];
+    }
+    if (type == AOTX_WEIGHT_F16) return aotx_h2f(((const unsigned short *)w)[i]);
+    return ((const float *)w)[i];
+}
+
+/* The rank head (cuda/rerank/rerank.cu:8-81): the last residual row of each sequence
+ * under the last RMSNorm in fp32, against the two class rows (yes, no), and the score
+ * softmax(yes, no)[0] into score[seq]. One block per sequence. */
+__global__ __launch_bounds__(256) void aotx_score_kernel(const aotx_step *step, const float *resid,
+                                                         const float *norm_w,
+                                                         const unsigned char *cls,
+                                                         unsigned int type, unsigned int hidden,
+                                                         float eps)
+{
+    __shared__ float share[4];
+    const aotx_model_run *run = &step->run;
+    const unsigned int s = blockIdx.x;
+    if (run->score == nullptr || s >= run->seqs) return;
+    const unsigned int row = run->offset[s + 1u] - 1u;
+    if (row >= run->tokens) return;
+    const float *r = resid + (unsigned long long)row * hidden;
+    float sq = 0.0f;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) sq += r[d] * r[d];
+    const float scale = rsqrtf(aotx_block_sum(sq, share) / (float)hidden + eps);
+    float yes = 0.0f, no = 0.0f;
+    for (unsigned int d = threadIdx.x; d < hidden; d += blockDim.x) {
+        const float v = scale * r[d] * norm_w[d];
+        yes += v * aotx_cls_at(cls, type, d);
+        no += v * aotx_cls_at(cls, type, (unsigned long long)hidden + d);
+    }
+    yes = aotx_block_sum(yes, share);
+    no = aotx_block_sum(no, share);
+    if (threadIdx.x != 0u) return;
+    const float top = fmaxf(yes, no);
+    const float ey = expf(yes - top), en = expf(no - top);
+    run->score[s] = ey / (ey + en);
+}
+
 void aotx_launch_rows(const aotx_step *step, unsigned int max_tokens, unsigned int *pos,
                       unsigned int *tagent, unsigned int *last, hipStream_t s)
 {
@@ -332,5 +432,30 @@ void aotx_launch_rope(const aotx_rope_args &a, unsigned int max_tokens, hipStrea
     if (threads < 64u) threads = 64u;
     hipLaunchKernelGGL(aotx_rope_kernel, dim3(max_tokens, a.heads + a.kv_heads), dim3(threads), 0,
                        s, a);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_capture(const aotx_step *step, const float *resid, unsigned int hidden,
+                         unsigned int layer, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_capture_kernel, dim3(AOTX_SLOTS), dim3(256), 0, s, step, resid, hidden,
+                       layer);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_pool(const aotx_step *step, const float *resid, const float *norm_w,
+                      unsigned int hidden, float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_pool_kernel, dim3(AOTX_SLOTS), dim3(256), 0, s, step, resid, norm_w,
+                       hidden, eps);
+    AOTX_LAUNCH_CHECK();
+}
+
+void aotx_launch_score(const aotx_step *step, const float *resid, const float *norm_w,
+                       const unsigned char *cls, unsigned int type, unsigned int hidden,
+                       float eps, hipStream_t s)
+{
+    hipLaunchKernelGGL(aotx_score_kernel, dim3(AOTX_SLOTS), dim3(256), 0, s, step, resid, norm_w,
+                       cls, type, hidden, eps);
     AOTX_LAUNCH_CHECK();
 }

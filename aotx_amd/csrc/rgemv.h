@@ -114,7 +114,7 @@ int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigne
                          unsigned int nseg, unsigned int k, int epi, unsigned int mt);
 /* Launch one pass (<= 32 rows) and, with splits > 1, the kernel that adds the partials
  * and applies the epilogue. */
-void aotx_rgemv_launch(const aotx_rgemv_args &a, hipStream_t stream);
+int aotx_rgemv_launch(const aotx_rgemv_args &a, hipStream_t stream);   /* 1 when refused */
 size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a);
 /* The split arrival counters a plan needs (one per tile group and expert or row block). */
 unsigned int aotx_rgemv_count_words(const aotx_rgemv_args &a);

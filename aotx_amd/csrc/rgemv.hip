@@ -555,19 +555,18 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
  * results pass through LDS to the same epilogues. */
 #define RGM_MB 64
 #define RGM_RT 16
-/* XCD: the grid is one-dimensional, ordered so that the row blocks of a weight group run
+/* The grid is one-dimensional, ordered so that the row blocks of a weight group run
  * together on one XCD (dispatch goes round the 8 XCDs by workgroup index): they read each
- * weight quad at about the same time, and the XCD's L2 serves all but the first read.
- * NTL: the weights are read with nontemporal loads. */
-template <int MB, bool XCD, bool NTL, bool PAIR = false>
+ * weight quad at about the same time, and the XCD's L2 serves all but the first read, so
+ * the weights take plain loads. An LDS x buffer holds two quads: one barrier per pair. */
+template <int MB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void aotx_rgemm(aotx_rgemv_args a0, unsigned int ny)
 {
     aotx_args_touch(a0);
     constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
     constexpr int CB = MB / 16;                   /* column blocks per wave */
     constexpr int NT = 512;
-    /* PAIR: an LDS x buffer holds two quads, one barrier per pair of quads */
-    constexpr int XS = (PAIR ? 256 : 128) + 8;    /* LDS x row stride (halves) */
+    constexpr int XS = 256 + 8;                   /* LDS x row stride (halves): two quads */
     constexpr int PIECES = 16;                    /* 16-byte pieces of a row per quad */
     constexpr int PPT = MB * PIECES / NT;         /* pieces per thread */
     static_assert(MB * PIECES % NT == 0 && MB % 16 == 0, "whole pieces and blocks");
@@ -576,16 +575,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     const unsigned int lane = tid & 63u;
     const unsigned int wave = tid >> 6;
     const unsigned int r = lane & 15u, g = lane >> 4;
-    /* the row block runs fastest, then the k split, then the weight group */
-    unsigned int group = blockIdx.x, yb = blockIdx.y % ny, split = blockIdx.y / ny;
-    if (XCD) {
-        const unsigned int seq = blockIdx.x >> 3;           /* index on its XCD */
-        yb = seq % ny;
-        const unsigned int rest = seq / ny;
-        split = rest % a0.splits;
-        group = (rest / a0.splits) * 8u + (blockIdx.x & 7u);
-        if (group >= a0.groups) return;
-    }
+    /* on an XCD the row block runs fastest, then the k split, then the weight group */
+    const unsigned int seq = blockIdx.x >> 3;               /* index on its XCD */
+    const unsigned int yb = seq % ny;
+    const unsigned int rest = seq / ny;
+    const unsigned int split = rest % a0.splits;
+    const unsigned int group = (rest / a0.splits) * 8u + (blockIdx.x & 7u);
+    if (group >= a0.groups) return;
 
     aotx_rgemv_args a = a0;
     a.m0 = a0.m0 + yb * (unsigned int)MB;
@@ -634,13 +630,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         const unsigned int qq_ = (Q) < qn ? (Q) : qn - 1u;                               \
         _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                  \
             const rg_u4 *src = (const rg_u4 *)(qb[t] + (unsigned long long)qq_ * 2048ull); \
-            if (NTL) {                                                                   \
-                wa[BUF][t][0] = __builtin_nontemporal_load(src);                        \
-                wa[BUF][t][1] = __builtin_nontemporal_load(src + 64);                    \
-            } else {                                                                     \
-                wa[BUF][t][0] = src[0];                                                  \
-                wa[BUF][t][1] = src[64];                                                 \
-            }                                                                            \
+            wa[BUF][t][0] = src[0];                                                      \
+            wa[BUF][t][1] = src[64];                                                     \
             ws[BUF][t] = __builtin_nontemporal_load(&sb[t][(unsigned long long)qq_ * 64ull]); \
         }                                                                                \
     } while (0)
@@ -653,8 +644,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
             xr[XB][i] = *(const rg_u4 *)(a.x + xoff[i] + qx_);                           \
     } while (0)
 /* the LDS place of quad Q: buffer and offset within a row */
-#define RGM_XBUF(Q) (PAIR ? ((((Q) - qb0) >> 1) & 1u) : ((Q) & 1u))
-#define RGM_XPOS(Q) (PAIR ? (((Q) - qb0) & 1u) * 128u : 0u)
+#define RGM_XBUF(Q) ((((Q) - qb0) >> 1) & 1u)
+#define RGM_XPOS(Q) ((((Q) - qb0) & 1u) * 128u)
 #define RGM_XSTORE(XB, Q)                                                                \
     do {                                                                                 \
         unsigned short *xb_ = xl + RGM_XBUF(Q) * (unsigned int)(MB * XS) + RGM_XPOS(Q)   \
@@ -672,7 +663,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     RGM_WLOAD(0, qb0);
     RGM_WLOAD(1, qb0 + 1u);
     RGM_XSTORE(0, qb0);
-    if (PAIR) RGM_XSTORE(1, qb0 + 1u);
+    RGM_XSTORE(1, qb0 + 1u);
     rg_sync_lds();
     for (unsigned int q = qb0; q < qn; q += 2u) {
 /* quad QQ's MFMAs from weight buffer BUF, then quad QQ + 2's weights into it */
@@ -707,28 +698,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         RGM_WLOAD(BUF, qc_ + 2u);                                                        \
         __builtin_amdgcn_sched_barrier(0);                                               \
     } while (0)
-        if (PAIR) {
-            /* the next pair's x first, then both quads, then its store and one barrier */
-            RGM_XLOAD(0, q + 2u);
-            RGM_XLOAD(1, q + 3u);
-            __builtin_amdgcn_sched_barrier(0);
-            RGM_COMPUTE(0, q);
-            RGM_COMPUTE(1, q + 1u);
-            RGM_XSTORE(0, q + 2u);
-            RGM_XSTORE(1, q + 3u);
-            rg_sync_lds();
-        } else {
-            RGM_XLOAD(0, q + 2u);
-            __builtin_amdgcn_sched_barrier(0);     /* the x loads stay ahead of the MFMAs */
-            RGM_COMPUTE(0, q);
-            RGM_XSTORE(1, q + 1u);
-            rg_sync_lds();
-            RGM_XLOAD(1, q + 3u);
-            __builtin_amdgcn_sched_barrier(0);
-            RGM_COMPUTE(1, q + 1u);
-            RGM_XSTORE(0, q + 2u);
-            rg_sync_lds();
-        }
+        /* the next pair's x first, then both quads, then its store and one barrier */
+        RGM_XLOAD(0, q + 2u);
+        RGM_XLOAD(1, q + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        RGM_COMPUTE(0, q);
+        RGM_COMPUTE(1, q + 1u);
+        RGM_XSTORE(0, q + 2u);
+        RGM_XSTORE(1, q + 3u);
+        rg_sync_lds();
 #undef RGM_COMPUTE
     }
 #undef RGM_XBUF
@@ -770,35 +748,6 @@ static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
     return x > red ? x : red;
 }
 
-/* Planning overrides for measurement sweeps, read once from AOTX_RGEMV_TUNE
- * ("rt,pd,target,minq"; 0 keeps the default). */
-struct aotx_rgemv_tune {
-    unsigned int rt, pd, target, minq;
-};
-
-static const aotx_rgemv_tune &aotx_rgemv_tuning()
-{
-    static aotx_rgemv_tune t = [] {
-        aotx_rgemv_tune v = {0u, 0u, 0u, 0u};
-        const char *e = getenv("AOTX_RGEMV_TUNE");
-        if (e != nullptr) sscanf(e, "%u,%u,%u,%u", &v.rt, &v.pd, &v.target, &v.minq);
-        if (v.rt != 0u && v.rt != 1u && v.rt != 2u && v.rt != 4u && v.rt != 8u) v.rt = 0u;
-        return v;
-    }();
-    return t;
-}
-
-/* Workgroup count up to which the narrow product runs 8 waves per workgroup
- * (AOTX_RGEMV_NW8 overrides it for measurement sweeps). */
-static unsigned int tune_nw_limit()
-{
-    static const unsigned int v = [] {
-        const char *e = getenv("AOTX_RGEMV_NW8");
-        return e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 256u;
-    }();
-    return v;
-}
-
 /* narrow_max: the most batch rows that take the streaming (narrow) kernel. */
 static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                              unsigned int nseg, unsigned int k, int epi, unsigned int mt,
@@ -838,15 +787,10 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
                                            : (tiles + 15u) / 16u;
         /* k split while the launch stays within one workgroup per CU and a split keeps 8
          * quads: a workgroup's time is its k length, and a second workgroup on a CU shares
-         * its VALU and matrix cores (AOTX_GEMM_SPLIT caps the split for measurement sweeps) */
-        static const unsigned int split_cap = [] {
-            const char *e = getenv("AOTX_GEMM_SPLIT");
-            const unsigned int v = e != nullptr ? (unsigned int)atoi(e) : 0u;
-            return v != 0u ? v : 64u;
-        }();
+         * its VALU and matrix cores */
         const unsigned int ny = (mt + 63u) / 64u;
         unsigned int sp = 1u;
-        while (sp * 2u <= split_cap && a->groups * ny * sp * 2u <= 256u && a->qn / (sp * 2u) >= 8u)
+        while (a->groups * ny * sp * 2u <= 256u && a->qn / (sp * 2u) >= 8u)
             sp *= 2u;
         a->qps = (a->qn + sp - 1u) / sp;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
@@ -857,10 +801,9 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
      * rows it streams the config-2 shapes 1.0-1.5x faster than the streaming kernel, whose
      * per-workgroup x staging grows with the rows; at 2 rows the streaming kernel wins. */
     if (mt > narrow_max) {
-        const aotx_rgemv_tune &tw = aotx_rgemv_tuning();
         /* T tiles x P phases of 8 waves per workgroup (aotx_rgemv_wide): 8 x 1 for many
          * tiles (gate/up pair, head), 4 x 2 for a 14336-row matrix, 2 x 4 for few (QKV, O,
-         * down), measured best at the 8B shapes; AOTX_RGEMV_TUNE rt = 8, 4 or 2 picks T. Products run unsplit (no partials,
+         * down), measured best at the 8B shapes. Products run unsplit (no partials,
          * no second launch) unless they have fewer than 192 workgroups and k of 32 quads or more (down, a 4096-row O):
          * those split k towards 256 workgroups while a split keeps a whole chunk, and the
          * last split of a group to finish adds the partials. */
@@ -871,32 +814,25 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
          * half as often (Mixtral shape, 64 tokens: 73.7 -> 58.3 us per pass with 4 tiles,
          * 65.0 with 8); the gated unit and dense products keep the rule above */
         if (routed && epi != AOTX_EPI_SWIGLU && a->rt == 2u) a->rt = 4u;
-        if (tw.rt == 8u || tw.rt == 4u || tw.rt == 2u) a->rt = tw.rt;
         a->pd = 8u / a->rt;                            /* phases */
         const unsigned int kc = a->pd == 4u ? 8u : 4u;
         if (epi == AOTX_EPI_SWIGLU)
             a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + a->rt / 2u - 1u) / (a->rt / 2u);
         else a->groups = (tiles + a->rt - 1u) / a->rt;
-        const unsigned int wtarget = tw.target != 0u ? tw.target : 256u;
         unsigned int s = 1u;
         if (a->groups < 192u && a->qn >= 32u)
-            while (a->groups * s < wtarget && a->qn / (s + 1u) >= kc) s += 1u;
+            while (a->groups * s < 256u && a->qn / (s + 1u) >= kc) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
         return 0;
     }
     /* rows per workgroup: one tile (measured best at every 8B shape), the gated unit two
      * gate/up pairs. */
-    const aotx_rgemv_tune &tune = aotx_rgemv_tuning();
-    unsigned int rt = 1u;
-    if (tune.rt != 0u) rt = tune.rt;
     /* the gated unit takes two gate/up pairs per workgroup: its 448 workgroups are resident
      * at once (896 single pairs ran in two rounds) */
-    if (epi == AOTX_EPI_SWIGLU && tune.rt == 0u) rt = 4u;
-    if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
+    const unsigned int rt = epi == AOTX_EPI_SWIGLU ? 4u : 1u;
     a->rt = rt;
-    a->pd = rt == 1u ? 4u : (rt == 2u ? 2u : 1u);
-    if (tune.pd != 0u) a->pd = tune.pd;
+    a->pd = rt == 1u ? 4u : 1u;
     if (epi == AOTX_EPI_SWIGLU) {
         unsigned int half_tiles = (unsigned int)aotx_q8r_tiles(rows[0]);
         a->groups = (half_tiles + rt / 2u - 1u) / (rt / 2u);
@@ -905,8 +841,7 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
     }
     /* k split: the staged x rows of a workgroup's k range fit 96 KB of LDS; split further
      * while there are fewer than `target` workgroups and a split keeps >= `minq` quads */
-    const unsigned int target = tune.target != 0u ? tune.target : 256u;
-    const unsigned int minq = tune.minq != 0u ? tune.minq : 8u;
+    const unsigned int target = 256u, minq = 8u;
     unsigned int kmax = 98304u / (mt * 256u);
     if (kmax < 1u) kmax = 1u;
     unsigned int s = (a->qn + kmax - 1u) / kmax;
@@ -915,7 +850,7 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
     a->splits = (a->qn + a->qps - 1u) / a->qps;
     /* 8 waves per workgroup while the launch has few workgroups (each wave then has half
      * the quads to dequantise after its data arrives), 4 otherwise */
-    a->nw = a->groups * a->splits <= tune_nw_limit() ? 8u : 4u;
+    a->nw = a->groups * a->splits <= 256u ? 8u : 4u;
     return 0;
 }
 
@@ -935,28 +870,15 @@ int aotx_rgemv_plan_routed(aotx_rgemv_args *a, const void *const *w, const unsig
 /* Fragment-layout products: RT tiles x NW waves x PD quads per buffer, measured at the 8B
  * shapes with 32 rows: one tile per workgroup up to 256 tiles (O, down), two up to 512
  * (QKV), four beyond (gate/up pairs, the head); 8 waves up to 256 workgroups (O: 10.1
- * against 10.7 us with 4); two quads per buffer for long k (down). AOTX_FRAG_TUNE="rt,nw,pd[,k[,n]]" overrides them for
- * measurement sweeps (with k, and n the rows of all segments, given: only for those). */
+ * against 10.7 us with 4); two quads per buffer for long k. */
 int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigned int *rows,
                          unsigned int nseg, unsigned int k, int epi, unsigned int mt)
 {
     if (k % 128u != 0u || mt == 0u || mt > AOTX_XFRAG_ROWS) return 1;
     if (aotx_rgemv_plan(a, w, rows, nseg, k, epi, mt) != 0) return 1;
-    static const unsigned int *tv0 = [] {
-        static unsigned int v[5] = {0u, 0u, 0u, 0u, 0u};
-        const char *e = getenv("AOTX_FRAG_TUNE");
-        if (e != nullptr) sscanf(e, "%u,%u,%u,%u,%u", &v[0], &v[1], &v[2], &v[3], &v[4]);
-        return v;
-    }();
-    static const unsigned int none[5] = {0u, 0u, 0u, 0u, 0u};
-    unsigned int rows_all = 0u;
-    for (unsigned int sg = 0; sg < nseg; ++sg) rows_all += rows[sg];
-    const unsigned int *tv = (tv0[3] == 0u || tv0[3] == k) && (tv0[4] == 0u || tv0[4] == rows_all)
-                           ? tv0 : none;
     const unsigned int tiles = epi == AOTX_EPI_SWIGLU ? 2u * (unsigned int)aotx_q8r_tiles(a->n)
                                                       : (a->n + 15u) / 16u;
     unsigned int rt = epi == AOTX_EPI_SWIGLU ? 4u : (tiles <= 256u ? 1u : (tiles <= 512u ? 2u : 4u));
-    if (tv[0] == 1u || tv[0] == 2u || tv[0] == 4u) rt = tv[0];
     if (epi == AOTX_EPI_SWIGLU && rt == 1u) rt = 2u;
     a->wide = 0u;
     a->gemm = 0u;
@@ -969,9 +891,7 @@ int aotx_rgemv_plan_frag(aotx_rgemv_args *a, const void *const *w, const unsigne
     a->qps = (a->qn + s - 1u) / s;
     a->splits = (a->qn + a->qps - 1u) / a->qps;
     a->nw = a->groups * a->splits <= 256u ? 8u : 4u;
-    if (tv[1] == 4u || tv[1] == 8u) a->nw = tv[1];
     a->pd = a->qps >= 64u ? 2u : 1u;
-    if (tv[2] == 1u || tv[2] == 2u) a->pd = tv[2];
     if (rt > 1u) a->pd = 1u;
     return 0;
 }
@@ -1019,7 +939,7 @@ static void aotx_rgemv_go(const aotx_rgemv_args &a, hipStream_t s)
     AOTX_LAUNCH_CHECK();
 }
 
-void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
+int aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
 {
     aotx_rgemv_args a = a0;
     if (a.splits > 1u && a.partial == nullptr) {
@@ -1033,43 +953,20 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         if (a.xmode != AOTX_X_F16 || a.expert_stride != 0ull || a.list != nullptr
             || a.xrow != nullptr || (a.splits > 1u && (a.partial == nullptr || a.count == nullptr))) {
             fprintf(stderr, "aotx: the GEMM takes fp16 x of direct rows only\n");
-            exit(1);
+            return 1;
         }
         const unsigned int ny = (a.m + RGM_MB - 1u) / RGM_MB;
-        const size_t x = 2u * RGM_MB * (128u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
-        const size_t lds = x > res ? x : res;
-        static const int mode = [] {
-            /* measurement sweeps (AOTX_GEMM_MODE): bit 1 the XCD order, bit 0 plain weight
-             * loads; the default 3 measured fastest (512 rows: 19.87 ms per step at 0) */
-            const char *e = getenv("AOTX_GEMM_MODE");
-            return e != nullptr ? atoi(e) & 3 : 3;
-        }();
-        const dim3 g2(a.groups, ny * a.splits), g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
-        static const bool pair = [] {
-            const char *e = getenv("AOTX_GEMM_PAIR");     /* 0: a barrier per quad (sweeps) */
-            return !(e != nullptr && e[0] == '0');
-        }();
-        switch (mode) {
-        case 0: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, true>), g2, dim3(512), lds, s, a, ny); break;
-        case 1: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false, false>), g2, dim3(512), lds, s, a, ny); break;
-        case 2: hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, true>), g1, dim3(512), lds, s, a, ny); break;
-        default:
-            if (pair) {
-                const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u;
-                hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false, true>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
-            } else {
-                hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true, false>), g1, dim3(512), lds, s, a, ny);
-            }
-            break;
-        }
+        const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
+        const dim3 g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
+        hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
         AOTX_LAUNCH_CHECK();
-        return;
+        return 0;
     }
     if (a.frag) {
         if (a.xmode != AOTX_X_FRAG || a.expert_stride != 0ull || a.list != nullptr
             || a.xrow != nullptr || a.m0 != 0u || a.m > AOTX_XFRAG_ROWS) {
             fprintf(stderr, "aotx: the fragment product takes fragment-layout x of one pass\n");
-            exit(1);
+            return 1;
         }
         const dim3 grid(a.groups * a.splits);
         const bool ss = a.row_ss != nullptr && a.k <= 4096u;
@@ -1088,22 +985,22 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         }
 #undef RGF_GO
         AOTX_LAUNCH_CHECK();
-        return;
+        return 0;
     }
     if (a.xmode == AOTX_X_FRAG) {
         fprintf(stderr, "aotx: fragment-layout x needs the fragment product's plan\n");
-        exit(1);
+        return 1;
     }
     if (a.row_ss != nullptr && (!a.wide || a.list != nullptr || a.xrow != nullptr)) {
         fprintf(stderr, "aotx: the row-scaled product takes wide batches of direct rows only\n");
-        exit(1);
+        return 1;
     }
     if (a.wide) {
         const unsigned int ey = aotx_rgemv_rows_y(a);
         const dim3 grid(a.groups * a.splits, ey);
         if (a.xmode != AOTX_X_F16) {
             fprintf(stderr, "aotx: the wide-batch product takes fp16 x only\n");
-            exit(1);
+            return 1;
         }
         if (a.rt == 2u) {
             const size_t xb = 2u * 32u * (8u * 128u + 8u) * 2u;
@@ -1116,7 +1013,7 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             hipLaunchKernelGGL((aotx_rgemv_wide<8, 1, 4, 2>), grid, dim3(512), xb, s, a);
         }
         AOTX_LAUNCH_CHECK();
-        return;
+        return 0;
     }
     if (a.rt == 1u) {
         if (a.pd >= 8u) aotx_rgemv_go<16, 1, 8>(a, s);
@@ -1128,6 +1025,7 @@ void aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         if (a.pd >= 2u) aotx_rgemv_go<16, 4, 2>(a, s);
         else aotx_rgemv_go<16, 4, 1>(a, s);
     }
+    return 0;
 }
 
 /* ---- kernel-level C ABI ---------------------------------------------------------------- */
@@ -1160,15 +1058,8 @@ static int aotx_q8r_gemv_any(const void *wr, unsigned int n, unsigned int k, con
         /* up to 8 rows of a product of at most 256 tiles and k <= 4096 (4096 square) stream
          * faster through the narrow kernel: 9.0 against 9.8 us at 8 rows, where the wide
          * kernel splits k to fill the chip; larger products keep the wide kernel from 5 rows
-         * (measured on the four 8B shapes; AOTX_NARROW_MAX, 1..16, overrides the choice for
-         * measurement sweeps) */
-        static const unsigned int forced = [] {
-            const char *e = getenv("AOTX_NARROW_MAX");
-            const unsigned int v = e != nullptr ? (unsigned int)strtoul(e, nullptr, 10) : 0u;
-            return v <= 16u ? v : 0u;
-        }();
-        const unsigned int narrow_max = forced != 0u ? forced
-                                      : ((n + 15u) / 16u <= 256u && k <= 4096u ? 8u : AOTX_NARROW_ROWS);
+         * (measured on the four 8B shapes) */
+        const unsigned int narrow_max = (n + 15u) / 16u <= 256u && k <= 4096u ? 8u : AOTX_NARROW_ROWS;
         if (aotx_rgemv_plan_n(&a, ws, rows, 1u, k, epi, mt, narrow_max) != 0) return 1;
         a.xmode = AOTX_X_F16;
         a.x = (const unsigned short *)x;
@@ -1176,7 +1067,7 @@ static int aotx_q8r_gemv_any(const void *wr, unsigned int n, unsigned int k, con
         a.m0 = m0;
         a.y = y;
         a.ldy = n;
-        aotx_rgemv_launch(a, aotx_stream(stream));
+        if (aotx_rgemv_launch(a, aotx_stream(stream)) != 0) return 1;
     }
     return 0;
 }

@@ -40,12 +40,8 @@ void *aotx_pinned(void)
  * allocates a zeroed new one. Counters stay zero because every kernel that counts
  * arrivals resets its counter before it exits. Growth inside a stream capture is an
  * error: the model sizes every buffer before it captures. */
-void *aotx_scratch(int which, size_t bytes)
+void *aotx_scratch(aotx_scratch_kind which, size_t bytes)
 {
-    if (which < 0 || which >= AOTX_SCRATCH_KINDS) {
-        fprintf(stderr, "aotx: bad scratch kind %d\n", which);
-        exit(1);
-    }
     if (bytes == 0u) bytes = 256u;
     if (bytes > aotx_scratch_size[which]) {
         hipStreamCaptureStatus status = hipStreamCaptureStatusNone;

@@ -101,6 +101,7 @@ class Shape:
     qk_norm: bool = False
     pairs: int = AOTX_ROPE_PAIRS_ADJACENT
     sigma: float = 0.02
+    cls: bool = False           # a two-row class head (cls_output) for the rank role
 
     def q8_bytes(self, rows, k):
         return rows * (k // 32) * 34
@@ -209,6 +210,8 @@ def layout(shape: Shape, seed=0x5EED):
             L.offset[SLOT["router"]] = place("router", shape.experts, h)
         for s in ("attn_q", "attn_k", "attn_v", "attn_o", "ffn_gate", "ffn_up", "ffn_down"):
             d.layer_type[l][SLOT[s]] = AOTX_WEIGHT_Q8_0
+    if shape.cls:
+        d.cls_output = place("q8", 2, h)
     return Layout(desc=d, total=_align(cursor), tensors=tensors)
 
 
@@ -357,6 +360,50 @@ class Runtime:
                                         ag_d.data_ptr(), logits.data_ptr(), None),
               "aotx_model_prefill")
         return logits.cpu().numpy()
+
+    def probe(self, ids, offset, agent, layers, how=None):
+        """aotx_model_probe with the logits of each sequence's last row and the residual
+        capture of `layers`. Returns (logits [seqs][vocab], capture [len(layers)][seqs][hidden])."""
+        t = self.torch
+        ids_d, off_d, ag_d = self._batch(ids, offset, agent)
+        seqs = len(agent)
+        self.pages(off_d, ag_d, seqs)
+        logits = t.zeros((seqs, self.desc.vocab), dtype=t.float32, device=self.dev)
+        cap = t.full((max(1, len(layers)), seqs, self.desc.hidden), float("nan"),
+                     dtype=t.float32, device=self.dev)
+        lay_d = t.tensor(np.asarray(layers if layers else [0], dtype=np.uint32).view(np.int32),
+                         device=self.dev)
+        hows = how or [neutral_how() for _ in range(seqs)]
+        how_d = t.tensor(np.frombuffer(b"".join(bytes(h) for h in hows), dtype=np.uint8),
+                         device=self.dev)
+        check(self.L.aotx_model_probe(self.role, ids_d.data_ptr(), off_d.data_ptr(), seqs,
+                                      ag_d.data_ptr(), how_d.data_ptr(), logits.data_ptr(),
+                                      AOTX_MODEL_ROWS_LAST, cap.data_ptr(), lay_d.data_ptr(),
+                                      len(layers)), "aotx_model_probe")
+        return logits.cpu().numpy(), cap.cpu().numpy()[:len(layers)]
+
+    def pooled(self, ids, offset, agent):
+        """aotx_model_prefill with a pooled buffer and no logits: [seqs][hidden]."""
+        t = self.torch
+        ids_d, off_d, ag_d = self._batch(ids, offset, agent)
+        seqs = len(agent)
+        self.pages(off_d, ag_d, seqs)
+        out = t.full((seqs, self.desc.hidden), float("nan"), dtype=t.float32, device=self.dev)
+        check(self.L.aotx_model_prefill(self.role, ids_d.data_ptr(), off_d.data_ptr(), seqs,
+                                        ag_d.data_ptr(), None, out.data_ptr()),
+              "aotx_model_prefill")
+        return out.cpu().numpy()
+
+    def rerank(self, ids, offset, agent):
+        """aotx_model_rerank (the rank role): one score per sequence."""
+        t = self.torch
+        ids_d, off_d, ag_d = self._batch(ids, offset, agent)
+        seqs = len(agent)
+        self.pages(off_d, ag_d, seqs)
+        out = t.full((seqs,), float("nan"), dtype=t.float32, device=self.dev)
+        check(self.L.aotx_model_rerank(ids_d.data_ptr(), off_d.data_ptr(), seqs, ag_d.data_ptr(),
+                                       out.data_ptr()), "aotx_model_rerank")
+        return out.cpu().numpy()
 
     def faulted(self):
         return self.L.aotx_model_faulted()

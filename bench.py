@@ -385,8 +385,7 @@ def moe_run(args):
 def prefill_run(args):
     """`--prefill`: one prompt chunk of 128, 256 and 512 tokens of the 8B shape (a fresh
     slot each time) through aotx_model_launch, whole step; best of 5 after a warm-up.
-    Prints one JSON line. AOTX_GEMM=0 in the environment times the 32-row passes instead
-    of the GEMM."""
+    Prints one JSON line."""
     import torch
     from aotx_amd.model import LLAMA_8B, Runtime, build_device, layout_pages
     torch.cuda.init()
@@ -409,8 +408,7 @@ def prefill_run(args):
         best = min(times[1:])
         out[str(t)] = {"ms": round(best * 1e3, 3), "tokens_per_s": round(t / best, 1)}
     rt.close()
-    print(json.dumps({"metric": "prefill tokens/s (8B shape, one prompt chunk)",
-                      "gemm": os.environ.get("AOTX_GEMM", "1") != "0", "chunks": out}))
+    print(json.dumps({"metric": "prefill tokens/s (8B shape, one prompt chunk)", "chunks": out}))
 
 
 def _text_corpus(seed, lines, words=60):

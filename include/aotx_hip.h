@@ -54,7 +54,8 @@ extern "C" {
 #define AOTX_MODEL_STEERS      2u              /* cuda/model/forward.cuh:80 (affect off) */
 #define AOTX_MODEL_CONDUCT_NONE 0xFFFFFFFFu
 
-/* Roles (cuda/model/model.cuh:16-21). This build runs the language roles. */
+/* Roles (cuda/model/model.cuh:16-21). The language roles end in the vocabulary head and
+ * the sampler; the embedding role in the pooled unit row, the rank role in the score. */
 #define AOTX_MODEL_EMBEDDING      0u
 #define AOTX_MODEL_RERANKER       1u
 #define AOTX_MODEL_LANGUAGE       2u
@@ -269,16 +270,36 @@ int aotx_model_sample(unsigned int role, const int *ids, const unsigned int *off
                       unsigned int seqs, const unsigned int *agent,
                       const aotx_model_how *how, int *token, unsigned int *draw,
                       unsigned long long *seed);
-/* Prefill that writes the logits of every token (call_host.cu:40-56). */
+/* Prefill (call_host.cu:40-56; model.cuh:120-128). logits, when given, receives the row of
+ * every token. pooled, when given, receives [seqs][hidden]: each sequence's last residual
+ * row under the last RMSNorm, scaled to unit length (cuda/embed/embed.cu:8-65). As in the
+ * reference, only the embedding role's pass writes pooled; the other roles leave it as it
+ * was. */
 int aotx_model_prefill(unsigned int role, const int *ids, const unsigned int *offset,
                        unsigned int seqs, const unsigned int *agent, float *logits,
                        float *pooled);
-/* Language prefill with per-sequence samples and logits (call_host.cu:95-117). Residual
- * capture is not built: a non-null capture is refused. */
+/* The rank role's score of each sequence (call_host.cu:58-69; model.cuh:130-133):
+ * softmax(yes, no)[0] of the two cls_output rows against the last row under the last
+ * RMSNorm (cuda/rerank/rerank.cu:8-81). The rank role opens only with a class head of
+ * Q8_0, F16 or F32 (the descriptor's weight type). */
+int aotx_model_rerank(const int *ids, const unsigned int *offset, unsigned int seqs,
+                      const unsigned int *agent, float *score);
+/* Language prefill with per-sequence samples, logits and residual capture
+ * (call_host.cu:95-117; forward.cuh:361-368). capture, when given with layer_count > 0,
+ * receives [layer_count][seqs][hidden]: slot c holds, for each sequence, the residual row
+ * of its last token after layer layers[c] (layers: device memory). The reference adds
+ * registered steer vectors (how->steer) in the same place; this build has no steer
+ * registry, so none is ever registered and none is added, which is what the reference
+ * does while its registry is empty. The per-token logprob and entropy that the reference
+ * writes to its telemetry records are not produced (no record stream here). */
 int aotx_model_probe(unsigned int role, const int *ids, const unsigned int *offset,
                      unsigned int seqs, const unsigned int *agent,
                      const aotx_model_how *how, float *logits, unsigned int select,
                      float *capture, const unsigned int *layers, unsigned int layer_count);
+/* Keep each token bucket's recorded graph for the calls after (keep = 1, the default), or
+ * record and drop a fresh graph on every call (keep = 0), for tests that compare replays
+ * with first runs. No counterpart in the reference, which captures once at open. */
+void aotx_model_graphs(unsigned int keep);
 /* Set one slot's cache position. No counterpart in the reference, which restores a slot
  * by prefilling its tokens again (cuda/model/decode.cu:230-305); this is for callers that
  * write a slot's KV pages out of band (restore from a copy, benchmarks that seat a

@@ -453,6 +453,9 @@ struct orc_model {
     uint16_t *keys;  /* [slots][layers][max_context][kv_heads*d], fp16 as the pages hold */
     uint16_t *values;
     float *last_xnorm;
+    /* the residual row of each sequence's last token after every layer of the last step,
+     * [layers][seqs][hidden] (the probe's capture, cuda/model/conduct.cu:165-173) */
+    float *last_resid;
     /* routing of the last experts layer of the last step: [tokens][experts], [tokens][used] */
     float *last_prob;
     unsigned int *last_ids;
@@ -482,13 +485,14 @@ orc_model *orc_model_new(const aotx_model_desc *desc, const uint8_t *weights,
     m->keys = (uint16_t *)calloc(cells, sizeof(uint16_t));
     m->values = (uint16_t *)calloc(cells, sizeof(uint16_t));
     m->last_xnorm = (float *)calloc((size_t)slots * desc->hidden, sizeof(float));
+    m->last_resid = (float *)calloc((size_t)desc->layers * slots * desc->hidden, sizeof(float));
     return m;
 }
 
 void orc_model_free(orc_model *m)
 {
     if (!m) return;
-    free(m->seen); free(m->keys); free(m->values); free(m->last_xnorm);
+    free(m->seen); free(m->keys); free(m->values); free(m->last_xnorm); free(m->last_resid);
     free(m->last_prob); free(m->last_ids); free(m);
 }
 
@@ -498,6 +502,7 @@ void orc_model_forget(orc_model *m)
 }
 
 const float *orc_model_last_xnorm(const orc_model *m) { return m->last_xnorm; }
+const float *orc_model_last_resid(const orc_model *m) { return m->last_resid; }
 
 /* The router's probabilities and chosen experts of the last experts layer the last step
  * ran; *tokens is the step's row count (0 when no experts layer ran). */
@@ -789,6 +794,9 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
             orc_matmul(m, (const uint8_t *)orc_tensor(m, L->offset[AOTX_SLOT_FFN_DOWN]), h, f, act, tokens, proj);
             for (size_t i = 0; i < (size_t)tokens * h; ++i) resid[i] += proj[i];
         }
+        for (unsigned int s = 0; s < seqs; ++s)
+            memcpy(m->last_resid + ((size_t)l * seqs + s) * h,
+                   resid + (size_t)(offset[s + 1] - 1u) * h, (size_t)h * sizeof(float));
     }
     /* head: last norm, last row of each sequence, output matrix (graph_host.cu:115-153) */
     const float *on = (const float *)orc_tensor(m, d->output_norm);

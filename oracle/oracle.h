@@ -91,6 +91,9 @@ int orc_model_step(orc_model *m, const int *ids, const unsigned int *offset,
 int orc_model_seat(orc_model *m, unsigned int slot, unsigned int position, uint64_t seed);
 /* The xnorm (half values as float) of the last row of each sequence of the last step. */
 const float *orc_model_last_xnorm(const orc_model *m);
+/* The residual row of each sequence's last token after every layer of the last step,
+ * [layers][seqs][hidden]. */
+const float *orc_model_last_resid(const orc_model *m);
 const float *orc_model_last_route(const orc_model *m, const unsigned int **ids,
                                   unsigned int *tokens);
 const uint16_t *orc_model_cache(const orc_model *m, unsigned int which);

@@ -52,6 +52,8 @@ def lib():
         L.orc_model_seat.argtypes = [vp, u32, u32, u64]
         L.orc_model_last_xnorm.restype = ctypes.POINTER(f32)
         L.orc_model_last_xnorm.argtypes = [vp]
+        L.orc_model_last_resid.restype = ctypes.POINTER(f32)
+        L.orc_model_last_resid.argtypes = [vp]
         L.orc_model_last_route.restype = ctypes.POINTER(f32)
         L.orc_model_last_route.argtypes = [vp, ctypes.POINTER(ctypes.POINTER(u32)), ctypes.POINTER(u32)]
         L.orc_model_cache.restype = ctypes.POINTER(ctypes.c_uint16)
@@ -154,6 +156,14 @@ class Model:
     def last_xnorm(self, seqs):
         p = lib().orc_model_last_xnorm(self.h)
         return np.ctypeslib.as_array(p, shape=(seqs * self.hidden,)).reshape(seqs, self.hidden).copy()
+
+    def last_resid(self, seqs):
+        """The residual row of each sequence's last token after every layer of the last
+        step, [layers][seqs][hidden]."""
+        p = lib().orc_model_last_resid(self.h)
+        n = self.desc.layers * seqs * self.hidden
+        return np.ctypeslib.as_array(p, shape=(n,)).reshape(self.desc.layers, seqs,
+                                                            self.hidden).copy()
 
     def last_route(self):
         """(probabilities [tokens][experts], ids [tokens][used]) of the last experts layer of

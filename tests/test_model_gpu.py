@@ -139,37 +139,32 @@ def test_tiny_sampling_seeded(torch, tiny):
         rt.close()
 
 
-def test_graph_replay_equals_eager(torch, tiny, monkeypatch):
-    """The captured graph of a bucket gives the same logits on every replay as the eager
-    launch of the same kernels, with other work and synchronisation between replays."""
-    import subprocess, sys, os, json
+def test_graph_replay_equals_eager(torch, tiny):
+    """The recorded graph of a bucket gives on every replay, with other work and
+    synchronisation between replays, the logits of a graph recorded afresh for the call
+    (aotx_model_graphs(0))."""
     region, lay = tiny
-    code = r'''
-import sys, json, numpy as np, torch
-sys.path.insert(0, %r)
-from aotx_amd.model import TINY, Runtime, build_host
-region, lay = build_host(TINY, seed=1)
-rt = Runtime(torch.from_numpy(region).cuda(), lay.desc, max_tokens=32, pool_pages=16)
-rows = []
-for rep in range(4):
-    rt.L.aotx_model_forget()
-    t, d, lg = rt.step(list(range(50, 60)), [0, 10], [3])
-    x = torch.randn(1000, 1000, device="cuda") @ torch.randn(1000, 1000, device="cuda")
-    torch.cuda.synchronize()
-    rows.append(lg[0].tolist())
-print(json.dumps(rows))
-''' % os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    outs = []
-    for graphs in ("1", "0"):
-        env = dict(os.environ, AOTX_GRAPHS=graphs)
-        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
-                           timeout=300)
-        assert r.returncode == 0, r.stderr[-2000:]
-        outs.append(np.array(json.loads(r.stdout.strip().splitlines()[-1])))
-    graph, eager = outs
-    for i in range(4):
-        assert np.array_equal(graph[i], eager[0])
-        assert np.array_equal(eager[i], eager[0])
+    rt = _runtime(torch, region, lay)
+    L = rt.L
+    try:
+        outs = []
+        for keep in (1, 0):
+            L.aotx_model_graphs(keep)
+            rows = []
+            for rep in range(4):
+                L.aotx_model_forget()
+                _, _, lg = rt.step(list(range(50, 60)), [0, 10], [3])
+                x = torch.randn(1000, 1000, device="cuda") @ torch.randn(1000, 1000, device="cuda")
+                torch.cuda.synchronize()
+                rows.append(lg[0].copy())
+            outs.append(rows)
+        graph, fresh = outs
+        for i in range(4):
+            assert np.array_equal(graph[i], fresh[0])
+            assert np.array_equal(fresh[i], fresh[0])
+    finally:
+        L.aotx_model_graphs(1)
+        rt.close()
 
 
 def test_qknorm_split_layer_kind(torch, orc):

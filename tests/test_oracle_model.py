@@ -14,9 +14,10 @@ def h(x):
     return np.asarray(x, dtype=np.float64).astype(np.float16).astype(np.float64)
 
 
-def numpy_forward(region, lay, shape, ids_per_step, renorm=False):
+def numpy_forward(region, lay, shape, ids_per_step, renorm=False, layer_resid=None):
     """ids_per_step: list of token lists for one sequence (each list = one pass). renorm
-    (a negative control): routed weights renormalised over the chosen experts."""
+    (a negative control): routed weights renormalised over the chosen experts. layer_resid,
+    when a list, receives per pass the residual after every layer of its last token."""
     d = lay.desc
     def t(off, rows, k):
         return dequant_q8(region[off:off + rows * (k // 32) * 34].reshape(rows, -1), k).astype(np.float64)
@@ -43,7 +44,7 @@ def numpy_forward(region, lay, shape, ids_per_step, renorm=False):
             v[hi] = a * math.sin(ang) + b * math.cos(ang)
         return h(v)
     for ids in ids_per_step:
-        for tok in ids:
+        for ti, tok in enumerate(ids):
             sc = emb_blk[tok, :, :2].copy().view(np.float16).astype(np.float64)
             q8 = emb_blk[tok, :, 2:].copy().view(np.int8).astype(np.float64)
             resid = (q8 * sc).reshape(H)
@@ -106,6 +107,10 @@ def numpy_forward(region, lay, shape, ids_per_step, renorm=False):
                     up = t(L.offset[SLOT["ffn_up"]], F, H) @ x
                     act = h(gate / (1 + np.exp(-gate)) * up)
                     resid = resid + t(L.offset[SLOT["ffn_down"]], H, F) @ act
+                if layer_resid is not None and ti == len(ids) - 1:
+                    if l == 0:
+                        layer_resid.append([])
+                    layer_resid[-1].append(resid.copy())
             pos += 1
         xn = rms(resid, f(d.output_norm, H))
         head_off = d.token_embd if shape.tied else d.output
@@ -151,3 +156,23 @@ def test_oracle_model_batch_equals_serial(orc):
     s0 = b.step([1, 2, 3], [0, 3], [0])
     s1 = b.step([7, 8], [0, 2], [2])
     assert np.array_equal(both[0], s0[0]) and np.array_equal(both[1], s1[0])
+
+
+def test_oracle_layer_residuals_vs_numpy(orc):
+    """The residual rows after every layer (the probe's capture) against the numpy forward;
+    a wrong layer index (the rows of the layer before) is caught by the same figure."""
+    shape = Shape(layers=3, hidden=128, ffn=192, heads=4, kv_heads=2, head_dim=64, vocab=512)
+    region, lay = build_host(shape, seed=23)
+    steps = [[5, 77, 300, 12], [9]]
+    want = []
+    numpy_forward(region, lay, shape, steps, layer_resid=want)
+    m = orc.Model(lay.desc, region, slots=2, max_context=64)
+    for i, ids in enumerate(steps):
+        m.step(ids, [0, len(ids)], [1])
+        got = m.last_resid(1)[:, 0, :]
+        for l in range(shape.layers):
+            ref = want[i][l]
+            err = np.abs(got[l] - ref).max() / np.abs(ref).max()
+            assert err < 5e-3, (i, l, err)
+            if l > 0:
+                assert np.abs(got[l - 1] - ref).max() / np.abs(ref).max() > 5e-2

@@ -58,6 +58,15 @@ def test_static_attention_equals_allocating(torch, lib):
         big = 4097
         assert lib.aotx_attend_paged_static(p(qd), p(pd), p(ad), big, 8, 1, d, layer, layers,
                                             p(got), None) == 1
+        # so are shapes the kernels do not take (head width 96; 3 query heads per KV head):
+        # the output keeps what it held, so nothing ran
+        before = got.clone()
+        assert lib.aotx_attend_paged_static(p(qd), p(pd), p(ad), 2, heads, kvh, 96, layer,
+                                            layers, p(got), None) == 1
+        assert lib.aotx_attend_paged_static(p(qd), p(pd), p(ad), 2, 24, kvh, d, layer,
+                                            layers, p(got), None) == 1
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), before.view(torch.int16))
         assert lib.aotx_model_faulted() == 0
     finally:
         lib.aotx_kv_close(ctypes.byref(m))
