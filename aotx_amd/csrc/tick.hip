@@ -130,13 +130,19 @@ void aotx_launch_pen(const aotx_pen_args &a, unsigned int rows_cap, int restore,
     AOTX_LAUNCH_CHECK();
 }
 
-/* Apply token records in order (cuda/model/decode.cu:230-305), one thread: a record at
- * position 0 opens the slot (a slot that held a sequence gives its pages back first), with
- * the slot's own limit, stop and sample and the record's seed; a prompt record puts its
- * token in the list and extends the prompt; a sampled record appends its token with its
- * seed and draw, and the slot's draw counter continues after that draw; the last record
- * ends the slot. The pages of an opened slot are empty, so the next plans prefill the
- * whole list again. A record that does not continue its slot is refused and counted. */
+/* Apply token records in order (cuda/model/decode.cu:230-305), one thread:
+ *   - a record at position 0 on a slot that already kept records of a sequence shuts it
+ *     (its pages go back, the slot is free);
+ *   - a free slot opens on a record at position 0 (any other is refused), with the slot's
+ *     own limit, stop and sample and the record's seed;
+ *   - a prompt record below the slot's prompt (a slot whose open already put the prompt in
+ *     its list) must name the token standing there: it confirms it and adds nothing;
+ *   - otherwise a record must continue the slot's list: a prompt record puts its token in
+ *     the list and extends the prompt; a sampled record appends its token with its seed and
+ *     draw, and the slot's draw counter continues after that draw; the last record ends
+ *     the slot.
+ * The pages of an opened slot are empty, so the next plans prefill the whole list again
+ * (the plan's page check asks for the pages). A refused record is counted. */
 __global__ void aotx_seq_apply_kernel(unsigned int role, aotx_plan_slot *slots, int *tokens,
                                       unsigned int stride, aotx_plan_state *p,
                                       const aotx_token_record *rec, unsigned int n,
@@ -151,9 +157,15 @@ __global__ void aotx_seq_apply_kernel(unsigned int role, aotx_plan_slot *slots, 
             continue;
         }
         aotx_plan_slot &seq = slots[slot];
-        if (b.position == 0u) {
-            if (seq.state != AOTX_SEQ_STATE_FREE && st->kv.count[slot] != 0u) {
-                if (aotx_kv_put(&st->kv, slot, 0u)) st->kv.count[slot] = 0u;
+        if (b.position == 0u && seq.state != AOTX_SEQ_STATE_FREE && p->kept[slot] != 0u) {
+            if (st->kv.count[slot] != 0u && aotx_kv_put(&st->kv, slot, 0u)) st->kv.count[slot] = 0u;
+            seq.state = AOTX_SEQ_STATE_FREE;
+            p->asked[slot] = 0u;
+        }
+        if (seq.state == AOTX_SEQ_STATE_FREE) {
+            if (b.position != 0u) {
+                p->refused += 1u;
+                continue;
             }
             seq.state = AOTX_SEQ_STATE_PREFILL;
             seq.role = role;
@@ -167,15 +179,21 @@ __global__ void aotx_seq_apply_kernel(unsigned int role, aotx_plan_slot *slots, 
             st->draw[slot] = 0u;
             p->asked[slot] = 0u;
             p->kept[slot] = 0u;
-        } else if (seq.state == AOTX_SEQ_STATE_FREE) {
-            p->refused += 1u;
+        }
+        int *list = tokens + (unsigned long long)slot * stride;
+        if ((b.flags & AOTX_TOKEN_PROMPT) != 0u && b.position < seq.prompt) {
+            if (list[b.position] != (int)b.token) {
+                p->refused += 1u;
+                continue;
+            }
+            p->kept[slot] = b.position + 1u;
             continue;
         }
         if (b.position != seq.prompt + seq.sampled) {
             p->refused += 1u;
             continue;
         }
-        tokens[(unsigned long long)slot * stride + b.position] = (int)b.token;
+        list[b.position] = (int)b.token;
         seq.last = b.token;
         if ((b.flags & AOTX_TOKEN_SAMPLED) != 0u) {
             seq.sampled = b.position + 1u - seq.prompt;

@@ -32,6 +32,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 matrix-core peak
 CONFIG4_STEPS = 128           # 128 decode steps from a 2048-token cache
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "attention_b32_ctx2048_traffic.md")
 
@@ -349,55 +350,67 @@ def traffic_run(args):
                       "copy_bytes": src.numel()}))
 
 
-def moe_run(args):
-    """BASELINE config 5 (`--moe`): Mixtral-shape routed-expert decoder (32 layers, d_model
-    4096, 8 experts of FFN 14336, top-2, vocab 32000), 64 slots at 4096-token paged KV, one
-    token per slot per step, greedy. Prints one JSON line with tokens/s and the step's
-    fraction of the HBM roofline (every expert is touched at 128 routed rows per layer)."""
-    import torch
+def moe_measure(torch, steps, warmup):
+    """Mixtral-shape routed-expert decoder (32 layers, d_model 4096, 8
+    experts of FFN 14336, top-2, vocab 32000), 64 slots at 4096-token paged KV, one token
+    per slot per step, greedy. Returns tokens/s and the step's fraction of the HBM roofline
+    (every expert is touched at 128 routed rows per layer)."""
     import aotx_amd as A
     from aotx_amd.model import MIXTRAL, Runtime, build_device, layout_pages
-    torch.cuda.init()
     shape, batch, context = MIXTRAL, 64, 4096
     t0 = time.perf_counter()
     region, lay = build_device(shape, seed=0x5EED)
     log(f"moe: weights {region.numel() / 1e9:.2f} GB built in {time.perf_counter() - t0:.1f}s")
-    reserve = args.warmup * 3 + args.steps * 3 + 8
+    reserve = warmup * 3 + steps * 3 + 8
     per_slot = layout_pages(context + reserve, shape.layers, shape.kv_heads, shape.head_dim)
     slots = list(range(batch))
     rt = Runtime(region, lay.desc, max_tokens=batch, pool_pages=per_slot * batch + 8)
     seat_context(torch, rt, slots, context, reserve, shape.layers, shape.kv_heads, shape.head_dim)
     log(f"moe: seated {batch} x {context} in {time.perf_counter() - t0:.1f}s")
-    tps, ms = decode(torch, rt, slots, args.steps, args.warmup, A.neutral_how())
+    tps, ms = decode(torch, rt, slots, steps, warmup, A.neutral_how())
     rt.close()
+    del region
+    torch.cuda.empty_cache()
     # attended positions per token, averaged over the timed steps (pos + 1)
-    ctx_mean = context + args.warmup + (args.steps + 1) / 2.0
+    ctx_mean = context + warmup + (steps + 1) / 2.0
     sb = step_bytes(lay, shape, batch, ctx_mean)
-    out = {"metric": "Mixtral-shape MoE decode tokens/s (BASELINE config 5)",
-           "value": round(tps, 2), "unit": "tokens/s", "ms_per_step": round(ms, 4),
-           "steps": args.steps, "warmup": args.warmup, "batch": batch, "context": context,
-           "step_gb": round(sb / 1e9, 3),
-           "step_roofline_frac": round(sb / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-           "data": "synthetic (seeded N(0,0.02) Q8_0 weights; random fp16 KV; greedy ids)"}
-    print(json.dumps(out))
+    return {"metric": "Mixtral-shape MoE decode tokens/s (BASELINE config 5)",
+            "value": round(tps, 2), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "steps": steps, "warmup": warmup, "batch": batch, "context": context,
+            "step_gb": round(sb / 1e9, 3),
+            "step_roofline_frac": round(sb / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+            "data": "synthetic (seeded N(0,0.02) Q8_0 weights; random fp16 KV; greedy ids)"}
 
 
-def prefill_run(args):
-    """`--prefill`: one prompt chunk of 128, 256 and 512 tokens of the 8B shape (a fresh
-    slot each time) through aotx_model_launch, whole step; best of 5 after a warm-up.
-    Prints one JSON line."""
+def moe_run(args):
+    """`--moe`: BASELINE config 5 alone; prints one JSON line."""
     import torch
-    from aotx_amd.model import LLAMA_8B, Runtime, build_device, layout_pages
     torch.cuda.init()
-    shape = LLAMA_8B
-    region, lay = build_device(shape, seed=7)
-    per = layout_pages(512 + 16, shape.layers, shape.kv_heads, shape.head_dim)
-    rt = Runtime(region, lay.desc, max_tokens=512, pool_pages=per * 20 + 8)
+    print(json.dumps(moe_measure(torch, args.steps, args.warmup)))
+
+
+def prefill_flops(shape, t):
+    """Matrix-core work of one t-token prompt chunk: every dense product over t rows (the
+    head over the chunk's last row) plus the causal attention's two products."""
+    h, f = shape.hidden, shape.ffn
+    wide, narrow = shape.heads * shape.head_dim, shape.kv_heads * shape.head_dim
+    per_layer = h * (wide + 2 * narrow) + wide * h + 3 * f * h
+    dense = 2.0 * t * per_layer * shape.layers + 2.0 * shape.vocab * h
+    attn = 2.0 * 2.0 * shape.head_dim * shape.heads * shape.layers * t * (t + 1) / 2.0
+    return dense + attn
+
+
+def prefill_measure(torch, region, lay, shape, sizes, reps=6):
+    """One prompt chunk of each size in `sizes` (a fresh slot each time) through
+    aotx_model_launch, the whole step; best of reps - 1 after a warm-up."""
+    from aotx_amd.model import Runtime, layout_pages
+    per = layout_pages(max(sizes) + 16, shape.layers, shape.kv_heads, shape.head_dim)
+    rt = Runtime(region, lay.desc, max_tokens=max(sizes), pool_pages=per * (reps * len(sizes) + 2) + 8)
     rng = np.random.default_rng(0)
     out, slot = {}, 0
-    for t in (128, 256, 512):
+    for t in sizes:
         times = []
-        for _ in range(6):
+        for _ in range(reps):
             ids = rng.integers(0, shape.vocab, t).tolist()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -406,8 +419,22 @@ def prefill_run(args):
             times.append(time.perf_counter() - t0)
             slot += 1
         best = min(times[1:])
-        out[str(t)] = {"ms": round(best * 1e3, 3), "tokens_per_s": round(t / best, 1)}
+        fl = prefill_flops(shape, t)
+        out[str(t)] = {"ms": round(best * 1e3, 3), "tokens_per_s": round(t / best, 1),
+                       "tflops": round(fl / best / 1e12, 1),
+                       "mfma_frac_fp16": round(fl / best / (MFMA_PEAK_FP16_TFLOPS * 1e12), 4)}
     rt.close()
+    return out
+
+
+def prefill_run(args):
+    """`--prefill`: one prompt chunk of 128, 256 and 512 tokens of the 8B shape. Prints one
+    JSON line."""
+    import torch
+    from aotx_amd.model import LLAMA_8B, build_device
+    torch.cuda.init()
+    region, lay = build_device(LLAMA_8B, seed=7)
+    out = prefill_measure(torch, region, lay, LLAMA_8B, (128, 256, 512))
     print(json.dumps({"metric": "prefill tokens/s (8B shape, one prompt chunk)", "chunks": out}))
 
 
@@ -568,6 +595,8 @@ def main():
     ap.add_argument("--context", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the prefill chunk and the Mixtral-shape (config 5) lines")
     ap.add_argument("--moe", action="store_true",
                     help="BASELINE config 5 only: the Mixtral-shape routed-expert decoder")
     ap.add_argument("--prefill", action="store_true",
@@ -731,6 +760,21 @@ def main():
             "host_cores": os.cpu_count(), "host_cores_available": len(os.sched_getaffinity(0)),
             "sample": f"one oracle decode step, batch {cbatch}, context {args.context} "
                       f"({cdt:.1f} s on {threads} threads)"}
+
+    if not args.no_extra:
+        # the prefill path (one 512-token prompt chunk of the same 8B weights) and
+        # BASELINE config 5 (Mixtral shape), both timed in this run
+        pf = prefill_measure(torch, region, lay, shape, (512,))["512"]
+        log(f"bench: prefill 512 tokens: {pf['ms']} ms, {pf['tflops']} TFLOP/s")
+        result["prefill_512"] = dict(pf, workload="8B shape, one 512-token prompt chunk, whole step",
+                                     peak_tflops=MFMA_PEAK_FP16_TFLOPS)
+        del region
+        torch.cuda.empty_cache()
+        moe = moe_measure(torch, 16, 2)
+        log(f"bench: moe config 5: {moe['value']} tokens/s, {moe['ms_per_step']} ms/step")
+        result["moe_config5"] = {k: moe[k] for k in ("value", "unit", "ms_per_step", "steps",
+                                                     "warmup", "batch", "context", "step_gb",
+                                                     "step_roofline_frac")}
     print(json.dumps(result))
 
 

@@ -235,3 +235,54 @@ def test_tick_restore_continues_the_same_tokens(torch, orc):
         assert rt.faulted() == 0
     finally:
         rt.close()
+
+
+def test_apply_confirms_the_prompt_of_an_open_slot(torch, orc):
+    """Records replayed onto a slot that was opened with its prompt (kept 0): prompt records
+    below the slot's prompt confirm the token standing there and change nothing else, a
+    wrong token is refused, a sampled record continues the list; a position-0 record on a
+    slot that has kept records shuts it and opens it again (cuda/model/decode.cu:240-272)."""
+    rng = np.random.default_rng(5)
+    region, lay = build_host(TINY, seed=1)
+    rt = Runtime(torch.from_numpy(region).cuda(), lay.desc, max_tokens=64, pool_pages=256)
+    try:
+        stride, s = 32, 9
+        slots, toks = _slots(rng, [s], stride, [6], [10])
+        samples = [SAMPLES[0]] * AOTX_SLOTS
+        tk = Tick(torch, rt, slots, toks, samples, stride)
+
+        def apply(recs):
+            arr = (TokenRecord * len(recs))(*recs)
+            rec_d = torch.from_numpy(np.frombuffer(bytes(arr), dtype=np.uint8).copy()).cuda()
+            assert rt.L.aotx_seq_apply(ROLE, tk.slots_d.data_ptr(), tk.lists_d.data_ptr(),
+                                       stride, tk.plan_d.data_ptr(), rec_d.data_ptr(),
+                                       len(recs), None) == 0
+            torch.cuda.synchronize()
+            table = (PlanSlot * AOTX_SLOTS).from_buffer_copy(tk.slots_d.cpu().numpy().tobytes())
+            state = PlanState.from_buffer_copy(tk.plan_d.cpu().numpy().tobytes())
+            return table[s], state, tk.lists_d.cpu().numpy()[s]
+
+        def rec(token, position, flags, seed=77, draw=0):
+            return TokenRecord(slot=s, token=token, position=position, flags=flags, seed=seed,
+                               draw=draw, role=ROLE)
+
+        prompt = toks[s]
+        seq, state, lst = apply([rec(prompt[i], i, 1) for i in range(6)])
+        assert state.refused == 0 and state.kept[s] == 6
+        assert (seq.state, seq.prompt, seq.sampled, seq.seed) == (AOTX_SEQ_STATE_PREFILL, 6, 0,
+                                                                 slots[s]["seed"])
+        assert list(lst[:6]) == prompt
+        seq, state, lst = apply([rec((prompt[2] + 1) % TINY.vocab, 2, 1)])
+        assert state.refused == 1 and list(lst[:6]) == prompt
+        seq, state, lst = apply([rec(123, 6, 2, seed=99, draw=4)])
+        assert state.refused == 1 and (seq.prompt, seq.sampled, seq.seed, seq.draw) == (6, 1, 99, 4)
+        assert lst[6] == 123 and state.kept[s] == 7
+        # a new sequence in the slot: shut and opened again by its position-0 record
+        seq, state, lst = apply([rec(555, 0, 1, seed=1234)])
+        assert state.refused == 1
+        assert (seq.state, seq.prompt, seq.sampled, seq.seed, seq.last) == (
+            AOTX_SEQ_STATE_PREFILL, 1, 0, 1234, 555)
+        assert lst[0] == 555 and state.kept[s] == 1
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
