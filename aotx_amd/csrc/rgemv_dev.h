@@ -611,9 +611,12 @@ static __device__ __forceinline__ float rg_get(const float *p)
 
 /* k split over workgroups: publish this split's sums out[0, n); the last split of the
  * product group to arrive adds all splits in split order (its own from LDS) into out and
- * returns true; the others return false. All of this workgroup's stores have completed
- * before its arrival is counted; the last arrival puts the counter back to zero. `last` is
- * one word of LDS. */
+ * returns true; the others return false. The partials move as 16-byte device-coherent
+ * (sc1) accesses, the form a relaxed agent-scope atomic word takes, four words at a time
+ * (n is a multiple of 16 and the partial blocks are 16-byte aligned). All of this
+ * workgroup's stores have completed before its arrival is counted; the last arrival puts
+ * the counter back to zero. `last` is one word of LDS. */
+#define RG_SC1 16    /* cache-policy bit of device-coherent accesses */
 template <int NT>
 static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, float *out,
                                                       unsigned int n, unsigned int expert,
@@ -623,7 +626,13 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
     const unsigned int tid = threadIdx.x;
     const unsigned long long tile = (unsigned long long)expert * a.groups + group;
     float *base = a.partial + tile * a.splits * n;
-    for (unsigned int idx = tid; idx < n; idx += NT) rg_put(base + (unsigned long long)split * n + idx, out[idx]);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)base, (short)0, (int)(a.splits * n * 4u), 0x00020000);
+    const unsigned int n4 = n / 4u;
+    const rg_f4 *o4 = (const rg_f4 *)out;
+    for (unsigned int i = tid; i < n4; i += NT)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(rg_u4, o4[i]), rs,
+                                               (int)((split * n + 4u * i) * 4u), 0, RG_SC1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0u) {
@@ -633,12 +642,18 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
     }
     __syncthreads();
     if (*last == 0u) return false;
-    for (unsigned int idx = tid; idx < n; idx += NT) {
-        float sum = 0.0f;
+    rg_f4 *w4 = (rg_f4 *)out;
+    for (unsigned int i = tid; i < n4; i += NT) {
+        rg_f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+        const rg_f4 mine = w4[i];
 #pragma unroll 8
-        for (unsigned int sp = 0; sp < a.splits; ++sp)
-            sum += sp == split ? out[idx] : rg_get(base + (unsigned long long)sp * n + idx);
-        out[idx] = sum;
+        for (unsigned int sp = 0; sp < a.splits; ++sp) {
+            const rg_f4 v = sp == split ? mine
+                : __builtin_bit_cast(rg_f4, __builtin_amdgcn_raw_buffer_load_b128(
+                      rs, (int)((sp * n + 4u * i) * 4u), 0, RG_SC1));
+            sum += v;
+        }
+        w4[i] = sum;
     }
     __syncthreads();
     return true;
