@@ -140,6 +140,38 @@ def test_config4_8b_decode_full_size(torch, orc):
         rt.close()
 
 
+def test_8b_width_narrow_batches_vs_oracle(torch, orc):
+    """Batches of 1 to 4 rows at 8B width (the streaming product with the norm fused into
+    its x staging; attention split into chunks merged by the last to finish). Slots seated
+    at contexts that put the new position's block first, second and third in a wave's run
+    (959 at batch 4: runs of 3 blocks, the block third) and in a chunk of its own; two
+    layers; logits vs the oracle at every step."""
+    shape = Shape(layers=2, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
+                  vocab=1024)
+    region_dev, lay = build_device(shape, seed=9)
+    host = region_dev.cpu().numpy()
+    slots, contexts = [1, 2, 3, 4], [959, 815, 47, 2000]
+    print(f"narrow batches at 8B width: slots {slots} at {contexts}", flush=True)
+    per = layout_pages(max(contexts) + 8, shape.layers, shape.kv_heads, shape.head_dim)
+    rt = Runtime(region_dev, lay.desc, max_tokens=32, pool_pages=per * len(slots) + 8)
+    try:
+        ref = orc.Model(lay.desc, host, slots=8, max_context=max(contexts) + 8,
+                        threads=_threads())
+        for s, c in zip(slots, contexts):
+            _request(rt, [s], c + 8, shape)
+            _seat_both(torch, rt, ref, shape, [s], c)
+        rng = np.random.default_rng(12)
+        for batch in ([1, 2, 3, 4], [1, 2, 4], [3], [2, 1], [4, 3, 2, 1]):
+            ids = rng.integers(0, shape.vocab, len(batch)).tolist()
+            offs = list(range(len(batch) + 1))
+            _, _, lg = rt.step(ids, offs, batch)
+            want = ref.step(ids, offs, batch)
+            _deep_close(lg, want)
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
 def test_config5_mixtral_width_full_size(torch, orc):
     shape = Shape(layers=2, hidden=4096, ffn=14336, heads=32, kv_heads=8, head_dim=128,
                   vocab=32000, experts=8, used=2, theta=1e6)
