@@ -290,8 +290,11 @@ int aotx_model_rerank(const int *ids, const unsigned int *offset, unsigned int s
  * of its last token after layer layers[c] (layers: device memory). The reference adds
  * registered steer vectors (how->steer) in the same place; this build has no steer
  * registry, so none is ever registered and none is added, which is what the reference
- * does while its registry is empty. The per-token logprob and entropy that the reference
- * writes to its telemetry records are not produced (no record stream here). */
+ * does while its registry is empty. The probe sets `telemetry` as the reference's does; the
+ * reference's pick returns before any figure when the call has no token buffer
+ * (cuda/model/sample.cu:481-483), and the probe passes none, so neither build computes the
+ * per-token logprob and entropy for a probe (the decode tick's figures go to the reference's
+ * record stream, which is not part of this path). */
 int aotx_model_probe(unsigned int role, const int *ids, const unsigned int *offset,
                      unsigned int seqs, const unsigned int *agent,
                      const aotx_model_how *how, float *logits, unsigned int select,
