@@ -273,7 +273,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
             if (idx < T * 16u * MT) {
                 const unsigned int j = rest % T, mm = rest / T;
                 const bool ok = mm < cap && rg_vrow(a, group, j, 0u, T) + rr < a.n;
-                rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+                rres[rg_o<MT>(j * 16u + rr, mm)] = ok ? rold[it] : 0.0f;
             }
         }
         if (tid < T * 16u) rgw[tid] = gwv;
@@ -305,7 +305,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            part[(wave * 16u + 4u * g + (unsigned int)i) * MT + (unsigned int)t * 16u + r] = acc[t][i];
+            part[P == 1 ? rg_o<MT>(wave * 16u + 4u * g + (unsigned int)i, (unsigned int)t * 16u + r)
+                        : (wave * 16u + 4u * g + (unsigned int)i) * MT + (unsigned int)t * 16u + r] = acc[t][i];
     __syncthreads();
     float *out = part + W * 16 * MT;
     if (P == 1) {
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
             float sum = part[(j * P) * 16u * MT + rest];
 #pragma unroll
             for (int p = 1; p < P; ++p) sum += part[((j * P) + (unsigned int)p) * 16u * MT + rest];
-            out[idx] = sum;
+            out[rg_of<MT>(idx)] = sum;
         }
         __syncthreads();
     }
@@ -326,7 +327,8 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     }
     if (ss_pre) {
         /* rs was written before the loop; the barriers since have published it */
-        for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT)
+            out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
         __syncthreads();
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
             if (idx < RT * 16u * MT) {
                 const unsigned int j = rest % RT, mm = rest / RT;
                 const bool ok = mm < cap && rg_vrow(a, group, j, 0u, RT) + rr < a.n;
-                rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+                rres[rg_o<MT>(j * 16u + rr, mm)] = ok ? rold[it] : 0.0f;
             }
         }
         if (tid < GR) rgw[tid] = gwv;
@@ -528,7 +530,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
     float *out = part;
 #pragma unroll
     for (unsigned int i = 0; i < (GR * MT + NT - 1u) / NT; ++i)
-        if (tid + i * NT < GR * MT) out[tid + i * NT] = sums[i];
+        if (tid + i * NT < GR * MT) out[rg_of<MT>(tid + i * NT)] = sums[i];
     __syncthreads();
     if (a.splits > 1u) {
         __shared__ unsigned int last;
@@ -536,7 +538,8 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
     }
     if (ss_pre) {
         /* rs was written before the loop; the barriers since have published it */
-        for (unsigned int idx = tid; idx < GR * MT; idx += NT) out[idx] *= rs[idx % MT];
+        for (unsigned int idx = tid; idx < GR * MT; idx += NT)
+            out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
         __syncthreads();
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, GR, mrows, rs);
@@ -715,8 +718,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
 #undef RGM_XLOAD
 #undef RGM_XSTORE
 
-    /* the tile results into LDS, out[(tile * 16 + row) * MB + batch row] (the x buffers
-     * are free after the last barrier), then the epilogue */
+    /* the residual epilogue's loads or the row scale's partial sums go out first (their
+     * round trip overlaps the split merge), then the tile results into LDS as
+     * out[rg_o(tile * 16 + row, batch row)] (the x buffers are free after the last
+     * barrier), the split merge and the epilogue */
+    const bool gresid = a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr;
+    /* one register block holds either (the residual products have no row scale) */
+    rg_ss_pre<MB, NT> sspre;
+    static_assert(sizeof(sspre.v) == rg_gres<MB, NT, RT>::ITER * sizeof(float), "one block");
+    float *gres = &sspre.v[0][0];
+    float gw = 0.0f;
+    bool ss_early = false;
+    if (gresid) rg_gres_load<MB, NT, RT>(a, group, mrows, gres, gw);
+    else ss_early = rg_row_ss_load<MB, NT>(a, mrows, sspre);
     float *out = (float *)lds;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -724,19 +738,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         for (int c = 0; c < CB; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                out[((wave * 2u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i) * MB
-                    + (unsigned int)c * 16u + r] = acc[t][c][i];
+                out[rg_o<MB>((wave * 2u + (unsigned int)t) * 16u + 4u * g + (unsigned int)i,
+                             (unsigned int)c * 16u + r)] = acc[t][c][i];
     __syncthreads();
     if (a.splits > 1u) {
         /* the last split of (row block, group) to finish adds the splits in order */
         __shared__ unsigned int last;
-        if (!rg_split_merge<NT>(a, out, RT * 16u * MB, yb, group, split, &last)) return;
+        if (!rg_split_merge<NT, RT * 4 * MB>(a, out, RT * 16u * MB, yb, group, split, &last)) return;
     }
-    if (a.row_ss != nullptr) {
-        __shared__ float rs[MB];
+    __shared__ float rs[MB];
+    if (ss_early) {
+        rg_row_ss_sum<MB, NT>(a, mrows, rs, sspre);
+        __syncthreads();
+        for (unsigned int idx = tid; idx < RT * 16u * MB; idx += NT)
+            out[idx] *= rs[rg_o<MB>(idx / MB, idx % MB) % MB];
+        __syncthreads();
+    } else if (a.row_ss != nullptr) {
         rg_row_scale<MB, NT>(a, out, RT * 16u, mrows, rs);
     }
-    rg_epilogue<MB, NT, RT>(a, out, group, RT, mrows, nullptr);
+    if (gresid) rg_gres_store<MB, NT, RT>(a, out, group, mrows, gres, gw);
+    else rg_epilogue<MB, NT, RT>(a, out, group, RT, mrows, nullptr);
 }
 
 /* ---- host ---------------------------------------------------------------------------- */
@@ -788,7 +809,7 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
         /* k split while the launch stays within one workgroup per CU and a split keeps 8
          * quads: a workgroup's time is its k length, and a second workgroup on a CU shares
          * its VALU and matrix cores */
-        const unsigned int ny = (mt + 63u) / 64u;
+        const unsigned int ny = (mt + RGM_MB - 1u) / RGM_MB;
         unsigned int sp = 1u;
         while (a->groups * ny * sp * 2u <= 256u && a->qn / (sp * 2u) >= 8u)
             sp *= 2u;
@@ -956,8 +977,8 @@ int aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
             return 1;
         }
         const unsigned int ny = (a.m + RGM_MB - 1u) / RGM_MB;
-        const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
         const dim3 g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
+        const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
         hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
         AOTX_LAUNCH_CHECK();
         return 0;

@@ -28,6 +28,28 @@ static __device__ __forceinline__ void rg_sync_lds()
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+/* The sum over the 16 lanes of a DPP row (every lane gets it): a butterfly over lane
+ * distances 1, 2, 4 and 8 with DPP moves inside the row (quad permutations, then the
+ * half-row and row mirrors, which pair the same quads and halves), no LDS round trip. Each
+ * step adds the same two values a cross-lane shuffle by XOR would, so the sum is the same
+ * as long as the summed value is itself rounded (see rg_sq). */
+static __device__ __forceinline__ float rg_sum16(float v)
+{
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
+/* v * v rounded to fp32 before any sum uses it: never fused into the first add of
+ * rg_sum16, whose partner lane adds the rounded square */
+static __device__ __forceinline__ float rg_sq(float v)
+{
+#pragma clang fp contract(off)
+    return v * v;
+}
+
 /* ---- product ------------------------------------------------------------------------ */
 
 /* Four Q8R quants (stored as q + 128, one byte each) to half(q * scale): the byte under
@@ -251,6 +273,25 @@ static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep_flat(const aotx_rgemv_a
     return p;
 }
 
+/* The place of output row `row`, batch row mm in a workgroup's result block out[] (rows of
+ * MT floats). The epilogues read one batch row of consecutive output rows with consecutive
+ * lanes; with a plain stride of 64 floats (the GEMM's block) those all fall in one LDS
+ * bank, so there mm is XORed with the row's low bits. Blocks of 16 or 32 batch rows keep
+ * the plain layout (their conflicts are 4- to 16-way, and the XOR's address arithmetic
+ * costs the streaming products registers). */
+template <int MT>
+static __device__ __forceinline__ unsigned int rg_o(unsigned int row, unsigned int mm)
+{
+    if constexpr (MT >= 64) return row * (unsigned int)MT + (mm ^ (row & (unsigned int)(MT - 1)));
+    else return row * (unsigned int)MT + mm;
+}
+/* the same for the element idx of the block in row-major order */
+template <int MT>
+static __device__ __forceinline__ unsigned int rg_of(unsigned int idx)
+{
+    return rg_o<MT>(idx / (unsigned int)MT, idx % (unsigned int)MT);
+}
+
 template <int MT>
 static __device__ __forceinline__ void rg_qkv_store(const aotx_rgemv_args &a, const float *out,
                                                     const rg_qkv_pre &p, unsigned int row,
@@ -261,8 +302,8 @@ static __device__ __forceinline__ void rg_qkv_store(const aotx_rgemv_args &a, co
         if (p.count_fault != 0u) atomicAdd(&a.qkv.state->faults, 1u);
         return;
     }
-    const float a0 = out[row * MT + mm];
-    const float a1 = out[(row + 1u) * MT + mm];
+    const float a0 = out[rg_o<MT>(row, mm)];
+    const float a1 = out[rg_o<MT>(row + 1u, mm)];
     unsigned short *dst = (unsigned short *)(p.base + p.off);
     if (p.mode == 3u) co_store2h(dst, aotx_f2h(a0), aotx_f2h(a1));
     else co_store2h(dst, aotx_f2h(a0 * p.cs - a1 * p.sn), aotx_f2h(a0 * p.sn + a1 * p.cs));
@@ -281,7 +322,75 @@ static __device__ __forceinline__ float rg_gw_load(const aotx_rgemv_args &a, uns
     return src[ok ? v : 0u];
 }
 
-/* Epilogue over the workgroup's result out[row * MT + m], row = tile j * 16 + rr. rpre and
+/* The GEMM's residual epilogue (rt == RTC, a tile of MT batch rows, the sums of squares
+ * wanted): every residual value the thread adds to, and the next norm's weight of its output
+ * row, requested together before the accumulators go to LDS, so that their round trip
+ * overlaps the split merge and the row scale. With NT a multiple of 16 * RTC a thread keeps
+ * one output row (tile j = (tid / 16) % RTC, row rr = tid % 16) for batch rows
+ * tid / (16 * RTC) + i * NT / (16 * RTC); rv holds ITER values. */
+template <int MT, int NT, int RTC>
+struct rg_gres {
+    static_assert(NT % (16 * RTC) == 0 && (RTC * 16 * MT) % NT == 0, "whole passes");
+    static constexpr unsigned int ITER = (unsigned int)RTC * 16u * MT / NT;
+    static constexpr unsigned int MSTEP = NT / (16u * RTC);
+};
+
+template <int MT, int NT, int RTC>
+static __device__ __forceinline__ void rg_gres_load(const aotx_rgemv_args &a, unsigned int group,
+                                                    unsigned int mrows, float *rv, float &gw)
+{
+    typedef rg_gres<MT, NT, RTC> G;
+    const unsigned int tid = threadIdx.x;
+    const unsigned int rr = tid & 15u, j = (tid >> 4) % RTC, mm0 = (tid >> 4) / RTC;
+    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
+    const bool v_ok = v0 + rr < a.n;
+    gw = a.xg_out != nullptr ? a.xg_w[v_ok ? v0 + rr : 0u] : 0.0f;
+#pragma unroll
+    for (unsigned int i = 0; i < G::ITER; ++i) {
+        const unsigned int mm = mm0 + i * G::MSTEP;
+        /* unconditional, from an address clamped into the operand */
+        const unsigned long long at = v_ok && mm < mrows ? (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr
+                                                         : (unsigned long long)a.m0 * a.ldy;
+        rv[i] = co_loadf((const float *)a.y + at);
+    }
+}
+
+template <int MT, int NT, int RTC>
+static __device__ __forceinline__ void rg_gres_store(const aotx_rgemv_args &a, const float *out,
+                                                     unsigned int group, unsigned int mrows,
+                                                     const float *rv, float gw)
+{
+    typedef rg_gres<MT, NT, RTC> G;
+    const unsigned int tid = threadIdx.x;
+    const unsigned int rr = tid & 15u, j = (tid >> 4) % RTC, mm0 = (tid >> 4) / RTC;
+    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
+    float sq[G::ITER];
+#pragma unroll
+    for (unsigned int i = 0; i < G::ITER; ++i) {
+        const unsigned int mm = mm0 + i * G::MSTEP;
+        const bool col_ok = mm < mrows && v0 + rr < a.n;
+        float v = 0.0f;
+        if (col_ok) {
+            v = rv[i] + out[rg_o<MT>(j * 16u + rr, mm)];
+            co_storef((float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr, v);
+            if (a.xg_out != nullptr)
+                a.xg_out[a.out_frag ? aotx_xfrag_at(a.m0 + mm, v0 + rr)
+                                    : (unsigned long long)(a.m0 + mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
+        }
+        sq[i] = rg_sq(v);
+    }
+    /* the tiles' sums of squares */
+#pragma unroll
+    for (unsigned int i = 0; i < G::ITER; ++i) sq[i] = rg_sum16(sq[i]);
+#pragma unroll
+    for (unsigned int i = 0; i < G::ITER; ++i) {
+        const unsigned int mm = mm0 + i * G::MSTEP;
+        if (mm < mrows && v0 < a.n && rr == 0u)
+            co_storef(a.sumsq_out + (unsigned long long)(a.m0 + mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq[i]);
+    }
+}
+
+/* Epilogue over the workgroup's result out[rg_o(row, m)], row = tile j * 16 + rr. rpre and
  * gpre, when given, hold the residual values out[] adds to and the next norm's weights of
  * the rows (gpre[row]), read while the weights streamed. */
 template <int MT, int NT, int RTC = 0>
@@ -296,55 +405,8 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
     const unsigned int gr = rt * 16u;
 #define RG_YROW(mm) (list != nullptr ? list[(mm)] : a.m0 + (mm))
     if constexpr (RTC > 0) {
-        /* rt == RTC, known when compiled (the GEMM's tile): a thread's outputs in chunks of
-         * CH, every load of a chunk issued before its first store (a store to y may alias
-         * the next output's residual, so a plain loop waits a round trip per output) */
-        if (a.epi == AOTX_EPI_RESID && a.sumsq_out != nullptr && list == nullptr) {
-            constexpr unsigned int ITER = ((unsigned int)RTC * 16u * MT + NT - 1u) / NT;
-            constexpr unsigned int CH = ITER < 16u ? ITER : 16u;
-            static_assert(ITER % CH == 0u && (RTC * 16 * MT) % NT == 0, "whole chunks");
-            for (unsigned int c0 = 0; c0 < ITER; c0 += CH) {
-                float rv[CH], gv[CH];
-#pragma unroll
-                for (unsigned int i = 0; i < CH; ++i) {
-                    const unsigned int idx = (c0 + i) * NT + tid;
-                    const unsigned int rr = idx & 15u, rest = idx >> 4;
-                    const unsigned int j = rest % RTC, mm = rest / RTC;
-                    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
-                    const bool col_ok = mm < mrows && v0 + rr < a.n;
-                    /* unconditional, from an address clamped into the operand */
-                    const unsigned long long at = col_ok ? (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr
-                                                         : (unsigned long long)a.m0 * a.ldy;
-                    rv[i] = co_loadf((const float *)a.y + at);
-                    gv[i] = a.xg_out != nullptr ? a.xg_w[col_ok ? v0 + rr : 0u] : 0.0f;
-                }
-#pragma unroll
-                for (unsigned int i = 0; i < CH; ++i) {
-                    const unsigned int idx = (c0 + i) * NT + tid;
-                    const unsigned int rr = idx & 15u, rest = idx >> 4;
-                    const unsigned int j = rest % RTC, mm = rest / RTC;
-                    const unsigned int v0 = rg_vrow(a, group, j, 0u, RTC);
-                    const bool row_ok = mm < mrows && v0 < a.n;
-                    const bool col_ok = row_ok && v0 + rr < a.n;
-                    float v = 0.0f;
-                    if (col_ok) {
-                        v = rv[i] + out[(j * 16u + rr) * MT + mm];
-                        co_storef((float *)a.y + (unsigned long long)(a.m0 + mm) * a.ldy + v0 + rr, v);
-                        if (a.xg_out != nullptr)
-                            a.xg_out[a.out_frag ? aotx_xfrag_at(a.m0 + mm, v0 + rr)
-                                                : (unsigned long long)(a.m0 + mm) * a.n + v0 + rr] = aotx_f2h(v * gv[i]);
-                    }
-                    float sq = v * v;
-                    sq += __shfl_xor(sq, 1, 64);
-                    sq += __shfl_xor(sq, 2, 64);
-                    sq += __shfl_xor(sq, 4, 64);
-                    sq += __shfl_xor(sq, 8, 64);
-                    if (row_ok && rr == 0u)
-                        co_storef(a.sumsq_out + (unsigned long long)(a.m0 + mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
-                }
-            }
-            return;
-        }
+        /* rt == RTC, known when compiled (the GEMM's tile; its residual epilogue is
+         * rg_gres_store) */
         if (a.epi == AOTX_EPI_QKV && qp == nullptr && list == nullptr) {
             constexpr unsigned int PAIRS = (unsigned int)RTC * 8u;     /* output pairs per batch row */
             constexpr unsigned int ITER = PAIRS * MT / NT;
@@ -397,18 +459,15 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             float v = 0.0f;
             if (col_ok) {
                 float *p = (float *)a.y + (unsigned long long)RG_YROW(mm) * a.ldy + v0 + rr;
-                v = (rpre != nullptr ? rpre[(j * 16u + rr) * MT + mm] : co_loadf(p))
-                  + out[(j * 16u + rr) * MT + mm];
+                v = (rpre != nullptr ? rpre[rg_o<MT>(j * 16u + rr, mm)] : co_loadf(p))
+                  + out[rg_o<MT>(j * 16u + rr, mm)];
                 co_storef(p, v);
             }
             if (a.xg_out != nullptr && col_ok)
                 a.xg_out[a.out_frag ? aotx_xfrag_at(RG_YROW(mm), v0 + rr)
                                     : (unsigned long long)RG_YROW(mm) * a.n + v0 + rr] = aotx_f2h(v * gw);
-            float sq = v * v;
-            sq += __shfl_xor(sq, 1, 64);
-            sq += __shfl_xor(sq, 2, 64);
-            sq += __shfl_xor(sq, 4, 64);
-            sq += __shfl_xor(sq, 8, 64);
+            float sq = rg_sq(v);
+            sq = rg_sum16(sq);
             if (row_ok && rr == 0u)
                 co_storef(a.sumsq_out + (unsigned long long)RG_YROW(mm) * ((a.n + 15u) / 16u) + v0 / 16u, sq);
         }
@@ -417,7 +476,7 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             unsigned int row = idx % gr, mm = idx / gr;
             unsigned int v = rg_vrow(a, group, row / 16u, row % 16u, rt);
             if (mm >= mrows || v >= a.n) continue;
-            float val = out[row * MT + mm];
+            float val = out[rg_o<MT>(row, mm)];
             unsigned long long at = (unsigned long long)RG_YROW(mm) * a.ldy + v;
             if (a.epi == AOTX_EPI_F32) co_storef((float *)a.y + at, val);
             else if (a.epi == AOTX_EPI_F16) ((unsigned short *)a.y)[at] = aotx_f2h(val);
@@ -433,8 +492,8 @@ static __device__ __forceinline__ void rg_epilogue(const aotx_rgemv_args &a, con
             unsigned int h[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                float gate = out[(row + e) * MT + mm];
-                float up = out[(row + e + half * 16u) * MT + mm];
+                float gate = out[rg_o<MT>(row + e, mm)];
+                float up = out[rg_o<MT>(row + e + half * 16u, mm)];
                 float unit = gate / (1.0f + expf(-gate));
                 h[e] = aotx_f2h(unit * up);
             }
@@ -490,14 +549,12 @@ static __device__ __forceinline__ void rg_row_scale(const aotx_rgemv_args &a, fl
                 for (int u = 0; u < 16; ++u) sum += v[u];
             }
         }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        sum += __shfl_xor(sum, 8, 64);
+        sum = rg_sum16(sum);
         if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
     }
     __syncthreads();
-    for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[idx] *= rs[idx % MT];
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT)
+        out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
     __syncthreads();
 }
 
@@ -549,10 +606,7 @@ static __device__ __forceinline__ void rg_row_ss_sum(const aotx_rgemv_args &a, u
 #pragma unroll
             for (int u = 0; u < 16; ++u) sum += l + 16u * (unsigned int)u < nss ? p.v[sl][u] : 0.0f;
         }
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        sum += __shfl_xor(sum, 8, 64);
+        sum = rg_sum16(sum);
         if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
     }
 }
@@ -617,7 +671,7 @@ static __device__ __forceinline__ float rg_get(const float *p)
  * workgroup's stores have completed before its arrival is counted; the last arrival puts
  * the counter back to zero. `last` is one word of LDS. */
 #define RG_SC1 16    /* cache-policy bit of device-coherent accesses */
-template <int NT>
+template <int NT, int N4 = 0>
 static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, float *out,
                                                       unsigned int n, unsigned int expert,
                                                       unsigned int group, unsigned int split,
@@ -643,6 +697,40 @@ static __device__ __forceinline__ bool rg_split_merge(const aotx_rgemv_args &a, 
     __syncthreads();
     if (*last == 0u) return false;
     rg_f4 *w4 = (rg_f4 *)out;
+    if constexpr (N4 > 0) {
+        /* n4 == N4, known when compiled: every element's loads of SC splits in flight
+         * together (one round trip per SC splits instead of one per element and split),
+         * added in split order as below */
+        constexpr unsigned int IT = ((unsigned int)N4 + NT - 1u) / NT;
+        constexpr unsigned int SC = IT >= 8u ? 1u : 4u;
+        rg_f4 sum[IT];
+#pragma unroll
+        for (unsigned int j = 0; j < IT; ++j) sum[j] = (rg_f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (unsigned int sp0 = 0; sp0 < a.splits; sp0 += SC) {
+            rg_f4 v[SC][IT];
+#pragma unroll
+            for (unsigned int c = 0; c < SC; ++c)
+#pragma unroll
+                for (unsigned int j = 0; j < IT; ++j) {
+                    const unsigned int sp = sp0 + c < a.splits ? sp0 + c : split;
+                    const unsigned int i = tid + j * NT < (unsigned int)N4 ? tid + j * NT : tid;
+                    v[c][j] = sp == split ? w4[i]
+                        : __builtin_bit_cast(rg_f4, __builtin_amdgcn_raw_buffer_load_b128(
+                              rs, (int)((sp * n + 4u * i) * 4u), 0, RG_SC1));
+                }
+#pragma unroll
+            for (unsigned int c = 0; c < SC; ++c)
+#pragma unroll
+                for (unsigned int j = 0; j < IT; ++j)
+                    if (sp0 + c < a.splits) sum[j] += v[c][j];
+        }
+        __syncthreads();      /* every read of this split's own values before the sums */
+#pragma unroll
+        for (unsigned int j = 0; j < IT; ++j)
+            if (tid + j * NT < (unsigned int)N4) w4[tid + j * NT] = sum[j];
+        __syncthreads();
+        return true;
+    }
     for (unsigned int i = tid; i < n4; i += NT) {
         rg_f4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
         const rg_f4 mine = w4[i];
@@ -892,10 +980,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
 #pragma unroll 4
                     for (unsigned int i = l; i < nss; i += 16u) sum += co_loadf(ss + i);
                 }
-                sum += __shfl_xor(sum, 1, 64);
-                sum += __shfl_xor(sum, 2, 64);
-                sum += __shfl_xor(sum, 4, 64);
-                sum += __shfl_xor(sum, 8, 64);
+                sum = rg_sum16(sum);
                 if (l == 0u && mm < mrows) xscale[mm] = rsqrtf(sum / (float)a.k + a.eps);
             }
         }
@@ -907,7 +992,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
                 if (idx < RT * 16u * MT) {
                     const unsigned int j = rest % RT, mm = rest / RT;
                     const bool ok = mm < cap && rg_vrow(a, group, j, 0u, RT) + rr < a.n;
-                    rres[(j * 16u + rr) * MT + mm] = ok ? rold[it] : 0.0f;
+                    rres[rg_o<MT>(j * 16u + rr, mm)] = ok ? rold[it] : 0.0f;
                 }
             }
             if (tid < RT * 16u) rgw[tid] = gwv;
@@ -978,7 +1063,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
         float sum = part[idx];
 #pragma unroll
         for (int w = 1; w < NW; ++w) sum += part[(unsigned int)w * gr * MT + idx];
-        out[idx] = sum;
+        out[rg_of<MT>(idx)] = sum;
     }
     __syncthreads();
     if (a.splits > 1u) {
