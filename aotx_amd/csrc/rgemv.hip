@@ -234,7 +234,7 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
      * addresses; masked where used), instead of in dependent rounds after the split merge */
     constexpr bool RP = T <= 2;
     constexpr unsigned int RPT = (T * 16u * MT + NT - 1u) / NT;
-    __shared__ float rres[RP ? T * 16 * MT : 1];
+    __shared__ float rres[RP ? T * 16 * rg_os<MT>() : 1];
     __shared__ float rgw[RP ? T * 16 : 1];
     const bool resid_pre = RP && list == nullptr && a.xrow == nullptr && a.epi == AOTX_EPI_RESID
                         && a.sumsq_out != nullptr;
@@ -323,12 +323,11 @@ __global__ __launch_bounds__(64 * T * P, 4) void aotx_rgemv_wide(aotx_rgemv_args
     }
     if (a.splits > 1u) {
         __shared__ unsigned int last;
-        if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
+        if (!rg_split_merge<NT>(a, out, gr * rg_os<MT>(), expert, group, split, &last)) return;
     }
     if (ss_pre) {
         /* rs was written before the loop; the barriers since have published it */
-        for (unsigned int idx = tid; idx < gr * MT; idx += NT)
-            out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
+        for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[rg_of<MT>(idx)] *= rs[idx % MT];
         __syncthreads();
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, gr, mrows, rs);
@@ -351,7 +350,7 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
     constexpr int MT = 32;
     constexpr unsigned int NT = 64u * NW;
     __shared__ float part[NW * RT * 16 * MT];           /* the waves' sums, then out */
-    __shared__ float rres[RT * 16 * MT];                /* the epilogue's residual values */
+    __shared__ float rres[RT * 16 * rg_os<MT>()];       /* the epilogue's residual values */
     aotx_args_touch(a);
     const unsigned int tid = threadIdx.x;
     const unsigned int lane = tid & 63u;
@@ -534,12 +533,11 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
     __syncthreads();
     if (a.splits > 1u) {
         __shared__ unsigned int last;
-        if (!rg_split_merge<NT>(a, out, GR * MT, 0u, group, split, &last)) return;
+        if (!rg_split_merge<NT>(a, out, GR * rg_os<MT>(), 0u, group, split, &last)) return;
     }
     if (ss_pre) {
         /* rs was written before the loop; the barriers since have published it */
-        for (unsigned int idx = tid; idx < GR * MT; idx += NT)
-            out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
+        for (unsigned int idx = tid; idx < GR * MT; idx += NT) out[rg_of<MT>(idx)] *= rs[idx % MT];
         __syncthreads();
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MT, NT>(a, out, GR, mrows, rs);
@@ -751,7 +749,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
         rg_row_ss_sum<MB, NT>(a, mrows, rs, sspre);
         __syncthreads();
         for (unsigned int idx = tid; idx < RT * 16u * MB; idx += NT)
-            out[idx] *= rs[rg_o<MB>(idx / MB, idx % MB) % MB];
+            out[rg_of<MB>(idx)] *= rs[idx % MB];
         __syncthreads();
     } else if (a.row_ss != nullptr) {
         rg_row_scale<MB, NT>(a, out, RT * 16u, mrows, rs);
@@ -929,7 +927,7 @@ size_t aotx_rgemv_partial_bytes(const aotx_rgemv_args &a)
     if (a.splits <= 1u) return 0u;
     if (a.gemm) return (size_t)aotx_rgemv_count_words(a) * a.splits * RGM_RT * 16u * RGM_MB * sizeof(float);
     size_t e = aotx_rgemv_rows_y(a);
-    return e * a.groups * a.splits * a.rt * 16u * 32u * sizeof(float);
+    return e * a.groups * a.splits * a.rt * 16u * 33u * sizeof(float);   /* rows of 33 (rg_os) */
 }
 
 unsigned int aotx_rgemv_count_words(const aotx_rgemv_args &a)

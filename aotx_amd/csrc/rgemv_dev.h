@@ -273,17 +273,22 @@ static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep_flat(const aotx_rgemv_a
     return p;
 }
 
-/* The place of output row `row`, batch row mm in a workgroup's result block out[] (rows of
- * MT floats). The epilogues read one batch row of consecutive output rows with consecutive
- * lanes; with a plain stride of 64 floats (the GEMM's block) those all fall in one LDS
- * bank, so there mm is XORed with the row's low bits. Blocks of 16 or 32 batch rows keep
- * the plain layout (their conflicts are 4- to 16-way, and the XOR's address arithmetic
- * costs the streaming products registers). */
+/* The place of output row `row`, batch row mm in a workgroup's result block out[]. The
+ * epilogues read one batch row of consecutive output rows with consecutive lanes; with a
+ * plain row stride of 32 or 64 floats those fall in one or two LDS banks. Blocks of 64
+ * batch rows (the GEMM's) XOR mm with the row's low bits; blocks of 32 pad each row to 33
+ * floats (a constant offset per row, so the accumulators' stores keep immediate offsets);
+ * blocks of 16 keep the plain layout. rg_os is the row stride, the block is rows * rg_os. */
+template <int MT>
+static __device__ __forceinline__ constexpr unsigned int rg_os()
+{
+    return MT == 32 ? 33u : (unsigned int)MT;
+}
 template <int MT>
 static __device__ __forceinline__ unsigned int rg_o(unsigned int row, unsigned int mm)
 {
     if constexpr (MT >= 64) return row * (unsigned int)MT + (mm ^ (row & (unsigned int)(MT - 1)));
-    else return row * (unsigned int)MT + mm;
+    else return row * rg_os<MT>() + mm;
 }
 /* the same for the element idx of the block in row-major order */
 template <int MT>
@@ -553,8 +558,7 @@ static __device__ __forceinline__ void rg_row_scale(const aotx_rgemv_args &a, fl
         if (l == 0u && mm < (unsigned int)MT) rs[mm] = rsqrtf(sum / (float)a.k + a.row_eps);
     }
     __syncthreads();
-    for (unsigned int idx = tid; idx < gr * MT; idx += NT)
-        out[idx] *= rs[rg_o<MT>(idx / MT, idx % MT) % MT];
+    for (unsigned int idx = tid; idx < gr * MT; idx += NT) out[rg_of<MT>(idx)] *= rs[idx % MT];
     __syncthreads();
 }
 
@@ -873,7 +877,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     const unsigned int kbeg = q0 * 128u;
     const unsigned int pieces = (q1 - q0) * 16u;       /* 16-byte pieces (8 values) per row */
     const unsigned int nss = (a.k + 15u) / 16u;
-    __shared__ float rres[RT * 16 * MT];               /* the epilogue's residual values */
+    __shared__ float rres[RT * 16 * rg_os<MT>()];      /* the epilogue's residual values */
     __shared__ float rgw[RT * 16];                     /* and the next norm's weights */
     rg_u4 pre[RG_PRE][4];
     float ssp[16];
@@ -1068,7 +1072,7 @@ static __device__ __forceinline__ void rg_narrow(const aotx_rgemv_args &a, unsig
     __syncthreads();
     if (a.splits > 1u) {
         __shared__ unsigned int last;
-        if (!rg_split_merge<NT>(a, out, gr * MT, expert, group, split, &last)) return;
+        if (!rg_split_merge<NT>(a, out, gr * rg_os<MT>(), expert, group, split, &last)) return;
     }
     rg_epilogue<MT, NT>(a, out, group, RT, mrows, list, resid_pre ? rres : nullptr,
                         qkv_pre ? &qpre : nullptr, resid_pre ? rgw : nullptr);
