@@ -763,7 +763,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
 static size_t aotx_rgemv_lds(const aotx_rgemv_args &a, unsigned int mt)
 {
     size_t x = (size_t)a.m * (a.qps * 128u + 8u) * 2u;
-    size_t red = (size_t)(a.nw + 1u) * a.rt * 16u * mt * 4u;
+    size_t red = (size_t)(a.nw + 1u) * a.rt * 16u * (mt + 1u) * 4u;   /* out rows padded (rg_os) */
     return x > red ? x : red;
 }
 

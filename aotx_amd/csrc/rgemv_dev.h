@@ -282,7 +282,7 @@ static __device__ __forceinline__ rg_qkv_pre rg_qkv_prep_flat(const aotx_rgemv_a
 template <int MT>
 static __device__ __forceinline__ constexpr unsigned int rg_os()
 {
-    return MT == 32 ? 33u : (unsigned int)MT;
+    return MT == 32 || MT == 16 ? (unsigned int)MT + 1u : (unsigned int)MT;
 }
 template <int MT>
 static __device__ __forceinline__ unsigned int rg_o(unsigned int row, unsigned int mm)
