@@ -838,8 +838,12 @@ static int aotx_rgemv_plan_n(aotx_rgemv_args *a, const void *const *w, const uns
         if (epi == AOTX_EPI_SWIGLU)
             a->groups = ((unsigned int)aotx_q8r_tiles(rows[0]) + a->rt / 2u - 1u) / (a->rt / 2u);
         else a->groups = (tiles + a->rt - 1u) / a->rt;
+        /* routed products are not split: their launch has a workgroup row per expert, which
+         * fills the chip with whole-k workgroups (Mixtral shape at 64 tokens: the down
+         * products of 8 experts as 512 workgroups in one round instead of 2048 in four, the
+         * step 16.75 -> 16.15 ms) */
         unsigned int s = 1u;
-        if (a->groups < 192u && a->qn >= 32u)
+        if (!routed && a->groups < 192u && a->qn >= 32u)
             while (a->groups * s < 256u && a->qn / (s + 1u) >= kc) s += 1u;
         a->qps = (a->qn + s - 1u) / s;
         a->splits = (a->qn + a->qps - 1u) / a->qps;
