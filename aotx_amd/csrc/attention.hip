@@ -121,13 +121,14 @@ int aotx_attend_launch(const unsigned short *q, unsigned short *out, const unsig
     a.out_frag = out_frag;
     const unsigned int g = heads / kv_heads;
     if (tokens >= AOTX_ATTN_PIECE_TOKENS) {
-        /* more tokens than sequence slots: a batch with prompt pieces, one wave per piece
-         * of consecutive queries of a sequence, 4 waves per 16-token range and KV head */
+        /* more tokens than sequence slots: a batch with prompt pieces, two waves per piece
+         * of consecutive queries of a sequence (each half of its blocks), 8 waves per
+         * 16-token range and KV head */
         a.splits = 1u;
         const dim3 rgrid((tokens + AOTX_RUN_RANGE - 1u) / AOTX_RUN_RANGE * kv_heads);
 #define AOTX_PIECE_GO(DD, GG)                                                              \
         do {                                                                               \
-            hipLaunchKernelGGL((aotx_attend_run<DD, GG, 4>), rgrid, dim3(256), 0, stream, a); \
+            hipLaunchKernelGGL((aotx_attend_run<DD, GG, 8>), rgrid, dim3(512), 0, stream, a); \
             AOTX_LAUNCH_CHECK();                                                           \
         } while (0)
         if (head_dim == 128u) {

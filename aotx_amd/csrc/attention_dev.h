@@ -391,14 +391,16 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     }
 }
 
-/* Prompt pieces one wave each: a workgroup of W waves takes the pieces led inside its
+/* Prompt pieces two waves each: a workgroup of W = 8 waves takes the pieces led inside its
  * range of AOTX_RUN_RANGE tokens (a piece: up to QT = 16 / G consecutive queries of one
  * sequence, led by a token that starts its sequence's run in the batch or sits at a
- * multiple of QT, as in the decode body's prompt pieces), in rank order, wave k taking
- * pieces k, k + W, ... A wave runs one ordered pass of online softmax over every block its
- * queries see (the reference's single pass per query, cuda/model/attention.cu:22-154) and
- * writes their outputs: no merge. The waves of one sequence read the same blocks at about
- * the same time, which the caches serve. */
+ * multiple of QT, as in the decode body's prompt pieces), in rounds of 4 in rank order.
+ * Wave k < 4 runs one ordered pass of online softmax (the reference's pass per query,
+ * cuda/model/attention.cu:22-154) over the first half of the blocks its round's piece sees,
+ * wave k + 4 over the second half; the second half's maxima, masses and accumulators pass
+ * through LDS and the first wave adds them in block order and writes the outputs. The
+ * waves of one sequence read the same blocks at about the same time, which the caches
+ * serve. */
 #define AOTX_RUN_RANGE 16u
 template <int D, int G, int W>
 static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a, unsigned int bx)
@@ -409,11 +411,18 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
     constexpr int NS = D / 16;
     constexpr int VS = D + 8;
     constexpr unsigned int RANGE = AOTX_RUN_RANGE;
+    constexpr unsigned int WP = 4u;                 /* waves of a round, a piece each */
+    static_assert(W == 2 * (int)WP, "two waves per piece: the halves of its blocks");
     static_assert(RANGE + QT <= 64u, "one lane per token word");
     __shared__ __attribute__((aligned(16))) unsigned short vl[W][16 * VS];
+    /* the second half's column maxima, masses, page-fault flag and accumulators (by lane) */
+    __shared__ float hm[WP][16], hl[WP][16];
+    __shared__ int hmiss[WP];
+    __shared__ float ho[WP][NS][4][64];
 
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
+    const unsigned int wp = wave % WP, half = wave / WP;
     const unsigned int r = lane & 15u, g = lane >> 4;
     const unsigned int counted = aotx_attn_scalar(a.m_dev != nullptr ? a.m_dev : a.pos);
     unsigned int tokens = a.m_dev != nullptr ? counted : a.tokens;
@@ -432,7 +441,10 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
     const unsigned int ag_prev = (unsigned int)__shfl((int)ag, (int)((lane - 1u) & 63u), 64);
     const bool lead = lane >= 1u && lane <= RANGE && ti < tokens
                    && (ag != ag_prev || ps % (unsigned int)QT == 0u);
-    unsigned long long leaders = (unsigned long long)__ballot(lead) >> 1;   /* bit j: token r0 + j */
+    const unsigned long long leaders = (unsigned long long)__ballot(lead) >> 1;   /* bit j: token r0 + j */
+    /* the same in every wave (one ballot over the same words), so every wave runs the same
+     * rounds and meets the same barriers */
+    const unsigned int npieces = (unsigned int)__builtin_popcountll(leaders);
 
     const aotx_kv_table *kv = &a.state->kv;
     const float scale = 1.4426950408889634f / sqrtf((float)D);
@@ -441,10 +453,13 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
     unsigned short *vw = vl[wave];
     constexpr int CPOL = 0;
 
-    for (unsigned int rank = 0; leaders != 0ull; ++rank) {
-        const unsigned int j = (unsigned int)__builtin_ctzll(leaders);
-        leaders &= leaders - 1ull;
-        if (rank % (unsigned int)W != wave) continue;
+    for (unsigned int round = 0; round * WP < npieces; ++round) {
+        /* piece rank (in token order) round * WP + wp, its blocks split in two halves */
+        const unsigned int rank = round * WP + wp;
+        const bool have = rank < npieces;
+        unsigned long long lb = leaders;
+        for (unsigned int k = 0; k < rank && lb != 0ull; ++k) lb &= lb - 1ull;
+        const unsigned int j = have ? (unsigned int)__builtin_ctzll(lb) : 0u;
         /* the piece led by token t = r0 + j (lane j + 1): the next tokens of its slot off a
          * multiple of QT, up to QT in all */
         const unsigned int lead_lane = j + 1u;
@@ -460,28 +475,31 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
         const unsigned int qpos = (unsigned int)__shfl((int)ps, (int)(lead_lane + r / (unsigned int)G), 64);
         const unsigned int plim = r / (unsigned int)G < nq ? qpos + 1u : 1u;
         const unsigned int p0 = 0u;
-        const unsigned int b0 = 0u, b1 = (n + 15u) / 16u;
+        const unsigned int nb = (n + 15u) / 16u;
+        const unsigned int mid = (nb + 1u) / 2u;
+        const unsigned int b0 = half == 0u ? 0u : mid;
+        const unsigned int b1 = !have ? b0 : (half == 0u ? mid : nb);
 
-        aotx_h8a qb[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            aotx_u4a w = {0u, 0u, 0u, 0u};
-            const unsigned int qi = r / (unsigned int)G, hh = r % (unsigned int)G;
-            if (qi < nq)
-                w = co_load4(a.q + ((unsigned long long)(t + qi) * a.heads + kh * G + hh) * D
-                                 + 32 * kk + 8 * g);
-            qb[kk] = __builtin_bit_cast(aotx_h8a, w);
-        }
         float mrun = -INFINITY, lrun = 0.0f;
         aotx_f4a o[NS];
 #pragma unroll
         for (int cc = 0; cc < NS; ++cc) o[cc] = (aotx_f4a){0.0f, 0.0f, 0.0f, 0.0f};
         int missing = 0;
-        aotx_u4a kr[2][KK], vr[2][VP];
-        bool absent[2];
-        unsigned long long pages = 0ull;
-        unsigned int wbase = b0;
-        {
+        if (b0 < b1) {
+            aotx_h8a qb[KK];
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                aotx_u4a w = {0u, 0u, 0u, 0u};
+                const unsigned int qi = r / (unsigned int)G, hh = r % (unsigned int)G;
+                if (qi < nq)
+                    w = co_load4(a.q + ((unsigned long long)(t + qi) * a.heads + kh * G + hh) * D
+                                     + 32 * kk + 8 * g);
+                qb[kk] = __builtin_bit_cast(aotx_h8a, w);
+            }
+            aotx_u4a kr[2][KK], vr[2][VP];
+            bool absent[2];
+            unsigned long long pages = 0ull;
+            unsigned int wbase = b0;
             unsigned int b = b0;
             MMA_WINDOW(b0);
             MMA_LOAD(0, b);
@@ -496,26 +514,56 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
                 if (b >= b1) break;
             }
         }
-        /* a head's mass over its 4 lane groups; column c's mass sits in lane c */
+        /* a head's mass over its 4 lane groups; column c's max and mass sit in lane c */
         lrun += __shfl_xor(lrun, 16, 64);
         lrun += __shfl_xor(lrun, 32, 64);
         missing = __any(missing);
         if (missing && lane == 0u) atomicAdd(&a.state->faults, 1u);
+        if (half == 1u) {
+            if (lane < 16u) {
+                hm[wp][lane] = mrun;
+                hl[wp][lane] = lrun;
+            }
+            if (lane == 0u) hmiss[wp] = missing;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const unsigned int col = 4u * g + (unsigned int)i;
-            const float l = __shfl(lrun, (int)col, 64);
-            const float back = !missing && l > 0.0f ? 1.0f / l : 0.0f;
-            const unsigned int qc = col / (unsigned int)G, hc = col % (unsigned int)G;
+            for (int cc = 0; cc < NS; ++cc)
 #pragma unroll
-            for (int cc = 0; cc < NS; ++cc) {
-                const float v = o[cc][i] * back;
-                const float v1 = __shfl_down(v, 1, 64);
-                if (qc < nq && (r & 1u) == 0u)
-                    co_store2h(a.out + aotx_attn_out_at(a, t + qc, kh * G + hc, 16u * cc + r, D),
-                               aotx_f2h(v), aotx_f2h(v1));
+                for (int i = 0; i < 4; ++i) ho[wp][cc][i][lane] = o[cc][i];
+        }
+        __syncthreads();
+        if (have && half == 0u) {
+            /* the halves in block order: M = max(m0, m1), o = o0 2^(m0 - M) + o1 2^(m1 - M),
+             * the masses likewise (a half with no position yet has m = -inf: factor 0) */
+            const float m1 = hm[wp][r], l1 = hl[wp][r];
+            const float top = fmaxf(mrun, m1);
+            const float f0 = mrun == -INFINITY ? 0.0f : aotx_exp2(mrun - top);
+            const float f1 = m1 == -INFINITY ? 0.0f : aotx_exp2(m1 - top);
+            lrun = lrun * f0 + l1 * f1;
+            missing = missing || hmiss[wp] != 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned int col = 4u * g + (unsigned int)i;
+                const float c0 = __shfl(f0, (int)col, 64), c1 = __shfl(f1, (int)col, 64);
+#pragma unroll
+                for (int cc = 0; cc < NS; ++cc) o[cc][i] = o[cc][i] * c0 + ho[wp][cc][i][lane] * c1;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned int col = 4u * g + (unsigned int)i;
+                const float l = __shfl(lrun, (int)col, 64);
+                const float back = !missing && l > 0.0f ? 1.0f / l : 0.0f;
+                const unsigned int qc = col / (unsigned int)G, hc = col % (unsigned int)G;
+#pragma unroll
+                for (int cc = 0; cc < NS; ++cc) {
+                    const float v = o[cc][i] * back;
+                    const float v1 = __shfl_down(v, 1, 64);
+                    if (qc < nq && (r & 1u) == 0u)
+                        co_store2h(a.out + aotx_attn_out_at(a, t + qc, kh * G + hc, 16u * cc + r, D),
+                                   aotx_f2h(v), aotx_f2h(v1));
+                }
             }
         }
+        __syncthreads();        /* the second halves' slots are free for the next round */
     }
 }
 
