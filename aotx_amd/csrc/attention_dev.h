@@ -8,6 +8,7 @@
 
 typedef unsigned int aotx_u4a __attribute__((ext_vector_type(4)));
 typedef _Float16 aotx_h4a __attribute__((ext_vector_type(4)));
+typedef short aotx_s4a __attribute__((ext_vector_type(4)));
 typedef _Float16 aotx_h8a __attribute__((ext_vector_type(8)));
 typedef float aotx_f4a __attribute__((ext_vector_type(4)));
 
@@ -84,7 +85,7 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
 
 /* The block loop shared by the attention bodies. They expect, in scope: a, kv, agent, b1,
  * lane, r, g, kbyte, vbyte, wbase, pages, kr, vr, absent, CPOL, KK, VP, NS, VS, D, qb, o,
- * mrun, lrun, missing, scale, p0, plim and vw (this wave's LDS value slot).
+ * mrun, lrun, missing, scale, p0, plim, vw (this wave's LDS value slot) and vtr.
  * MMA_WINDOW(B0): the page addresses of blocks B0 .. B0 + 63 (one per lane).
  * MMA_LOAD(BUF, B): block B's keys and values into register buffer BUF.
  * MMA_COMPUTE(BUF, B): block B's scores, online softmax and P . V. */
@@ -153,11 +154,12 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
                 _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
         }                                                                                   \
         _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
-            const unsigned short *col = vw + (4u * g) * VS + 16u * (unsigned int)cc + r;    \
-            aotx_h4a vb;                                                                    \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                   \
-                vb[i] = __builtin_bit_cast(_Float16, col[(unsigned int)i * VS]);            \
-            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, o[cc], 0, 0, 0);          \
+            /* B[k = 4g + i][n = r] = V[row 4g + i][16 cc + r]: one transposing read, each \
+             * lane addressing 4 halves of a row (aotx_vtr) */                               \
+            const aotx_s4a t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(                    \
+                (__attribute__((address_space(3))) aotx_s4a *)(vw + vtr + 16u * (unsigned int)cc)); \
+            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(aotx_h4a, t4), \
+                                                          o[cc], 0, 0, 0);                  \
         }                                                                                   \
     } while (0)
 
@@ -250,6 +252,10 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
     const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + r) * D + 8u * g) * 2u;
     const unsigned int vbyte = ((a.kv_heads + kh) * AOTX_KVL_BLOCK * D + lane * 8u) * 2u;
     unsigned short *vw = vl[wave];
+    /* ds_read_tr16_b64: lane j of a 16-lane group gets halves j % 4 of the chunks that
+     * lanes 4e + j / 4 address, e = 0..3; lane (r, g) = 16 g + 4 i + q addresses row 4g + i,
+     * halves 4q..4q+3 of a 16-column slice, so that it gets column r of rows 4g..4g+3 */
+    const unsigned int vtr = (4u * g + (lane & 15u) / 4u) * VS + 4u * (lane & 3u);
 
     aotx_u4a kr[2][KK], vr[2][VP];
     bool absent[2];
@@ -451,6 +457,10 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
     const unsigned int kbyte = ((kh * AOTX_KVL_BLOCK + r) * D + 8u * g) * 2u;
     const unsigned int vbyte = ((a.kv_heads + kh) * AOTX_KVL_BLOCK * D + lane * 8u) * 2u;
     unsigned short *vw = vl[wave];
+    /* ds_read_tr16_b64: lane j of a 16-lane group gets halves j % 4 of the chunks that
+     * lanes 4e + j / 4 address, e = 0..3; lane (r, g) = 16 g + 4 i + q addresses row 4g + i,
+     * halves 4q..4q+3 of a 16-column slice, so that it gets column r of rows 4g..4g+3 */
+    const unsigned int vtr = (4u * g + (lane & 15u) / 4u) * VS + 4u * (lane & 3u);
     constexpr int CPOL = 0;
 
     for (unsigned int round = 0; round * WP < npieces; ++round) {
