@@ -366,7 +366,6 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
      * there */
     const bool frag_dims = d->hidden % 128u == 0u && wide % 128u == 0u && d->ffn % 128u == 0u;
     const bool frag = scaled_x && T <= AOTX_XFRAG_ROWS && frag_dims;
-    const bool head_frag = d->hidden % 128u == 0u && R > AOTX_NARROW_ROWS && R <= AOTX_XFRAG_ROWS;
     const int xmode_in = frag ? AOTX_X_FRAG : AOTX_X_F16;
 
     if (tk != nullptr) {
@@ -613,11 +612,13 @@ static void aotx_record_step(aotx_hold *h, unsigned int sel_all, unsigned int bt
             on.x = nullptr;
             on.x_frag = 0u;
             on.sel = h->sel;
-            on.sel_frag = head_frag ? 1u : 0u;
             on.last = h->last;
             on.step = h->step;
             aotx_launch_norm(on, T, s);
-            t.xmode = head_frag ? AOTX_X_FRAG : AOTX_X_F16;
+            /* the head's rows as plain fp16 for the wide kernel (5-32 rows: 1002 workgroups
+             * of 8 tiles with x through LDS measured 15 us faster per batch-32 step than the
+             * fragment product's 2004 of 4 tiles) */
+            t.xmode = AOTX_X_F16;
             t.x = h->sel;
             t.ldx = d->hidden;
         }

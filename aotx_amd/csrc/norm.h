@@ -23,7 +23,6 @@ struct aotx_norm_args {
     const unsigned int *last;     /* last token row of each sequence */
     const aotx_step *step;        /* seqs and row selection of the call */
     unsigned int x_frag;          /* x in the fragment layout (aotx_xfrag_at) */
-    unsigned int sel_frag;        /* sel in the fragment layout */
 };
 
 struct aotx_expert_resid_args {

@@ -178,9 +178,7 @@ __global__ __launch_bounds__(256) void aotx_norm_kernel(aotx_norm_args a)
         unsigned short hv = aotx_f2h(scale * r[d] * a.norm_w[d]);
         if (a.x != nullptr)
             a.x[a.x_frag ? aotx_xfrag_at(t, d) : (unsigned long long)t * h + d] = hv;
-        if (selected >= 0)
-            a.sel[a.sel_frag ? aotx_xfrag_at((unsigned int)selected, d)
-                             : (unsigned long long)selected * h + d] = hv;
+        if (selected >= 0) a.sel[(unsigned long long)selected * h + d] = hv;
     }
 }
 

@@ -262,6 +262,35 @@ def test_8b_width_wide_batch_vs_oracle(torch, orc, rows):
         rt.close()
 
 
+@pytest.mark.parametrize("rows", [32, 8])
+def test_wide_qkv_fragment_four_tiles_vs_oracle(torch, orc, rows):
+    """64 query heads x 128 over d_model 1024: a QKV product of 10240 rows (640 tiles), which
+    the fragment-layout product takes at 4 tiles per workgroup (at the 8B shape only up to
+    512 tiles occur), and an O product with k = 8192. A prompt pass of 4 tokens per slot,
+    then a decode step, logits vs the oracle."""
+    shape = Shape(layers=1, hidden=1024, ffn=1024, heads=64, kv_heads=8, head_dim=128,
+                  vocab=1024)
+    region_dev, region, lay = _device_model(torch, shape, 9)
+    rt = Runtime(region_dev, lay.desc, max_tokens=128, pool_pages=128)
+    try:
+        ref = orc.Model(lay.desc, region, slots=rows, max_context=64, threads=8)
+        rng = np.random.default_rng(11)
+        ids = rng.integers(0, shape.vocab, 4 * rows).tolist()
+        offs = [4 * i for i in range(rows + 1)]
+        agents = list(range(rows))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        ids = rng.integers(0, shape.vocab, rows).tolist()
+        offs = list(range(rows + 1))
+        _, _, lg = rt.step(ids, offs, agents)
+        want = ref.step(ids, offs, agents)
+        assert rel_rms(lg, want) < 1e-2
+        assert rt.faulted() == 0
+    finally:
+        rt.close()
+
+
 @pytest.mark.parametrize("rows", [24, 40])
 def test_8b_width_experts_wide_batch_vs_oracle(torch, orc, rows):
     """Routed experts at d_model 4096 with 24 and 40 rows: the expert down product (k = 4096)
