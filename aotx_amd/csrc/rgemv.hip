@@ -560,10 +560,12 @@ __global__ __launch_bounds__(64 * NW) void aotx_rgemv_frag(aotx_rgemv_args a)
  * together on one XCD (dispatch goes round the 8 XCDs by workgroup index): they read each
  * weight quad at about the same time, and the XCD's L2 serves all but the first read, so
  * the weights take plain loads. An LDS x buffer holds two quads: one barrier per pair.
- * One workgroup per CU (2 waves per SIMD, up to 256 registers each): at 128 registers (two
- * workgroups per CU) the loop's operands spilled and the prompt chunks ran 2-9 % slower. */
-template <int MB>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void aotx_rgemm(aotx_rgemv_args a0, unsigned int ny)
+ * WIDE_REGS: one workgroup per CU (2 waves per SIMD, up to 256 registers each), for grids
+ * of at most one workgroup per CU; larger grids run two per CU at 128 registers, where
+ * the second workgroup hides the first one's waits (gate/up at 512 rows: 163 against
+ * 181 us), and the MFMA loop reads one x fragment at a time. */
+template <int MB, bool WIDE_REGS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WIDE_REGS ? 2 : 4))) void aotx_rgemm(aotx_rgemv_args a0, unsigned int ny)
 {
     aotx_args_touch(a0);
     constexpr int RT = RGM_RT;                    /* weight tiles per workgroup */
@@ -690,17 +692,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void a
                 A[t][s] = __builtin_bit_cast(rg_h8, av);                                 \
             }                                                                            \
         }                                                                                \
-        /* k step outermost: the step's x fragments are read together and its 8 MFMAs */ \
-        /* write 8 different accumulators, none waiting for the one before it */      \
-        _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                  \
-            rg_h8 B[CB];                                                                 \
-            _Pragma("unroll") for (int c = 0; c < CB; ++c)                               \
-                B[c] = *(const rg_h8 *)(xb + ((unsigned int)c * 16u + r) * XS            \
-                                        + 32u * g + 8u * (unsigned int)s);               \
-            _Pragma("unroll") for (int c = 0; c < CB; ++c) {                             \
-                acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][s], B[c], acc[0][c], 0, 0, 0); \
-                acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][s], B[c], acc[1][c], 0, 0, 0); \
+        if constexpr (WIDE_REGS) {                                                       \
+            /* k step outermost: the step's x fragments are read together and its 8 */  \
+            /* MFMAs write 8 different accumulators, none waiting for the one before */  \
+            _Pragma("unroll") for (int s = 0; s < 4; ++s) {                              \
+                rg_h8 B[CB];                                                             \
+                _Pragma("unroll") for (int c = 0; c < CB; ++c)                           \
+                    B[c] = *(const rg_h8 *)(xb + ((unsigned int)c * 16u + r) * XS        \
+                                            + 32u * g + 8u * (unsigned int)s);           \
+                _Pragma("unroll") for (int c = 0; c < CB; ++c) {                         \
+                    acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][s], B[c], acc[0][c], 0, 0, 0); \
+                    acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][s], B[c], acc[1][c], 0, 0, 0); \
+                }                                                                        \
             }                                                                            \
+        } else {                                                                         \
+            /* one x fragment at a time (fits 128 registers) */                          \
+            _Pragma("unroll") for (int c = 0; c < CB; ++c)                               \
+                _Pragma("unroll") for (int s = 0; s < 4; ++s) {                          \
+                    const rg_h8 B = *(const rg_h8 *)(xb + ((unsigned int)c * 16u + r) * XS \
+                                                     + 32u * g + 8u * (unsigned int)s);  \
+                    acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0][s], B, acc[0][c], 0, 0, 0); \
+                    acc[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1][s], B, acc[1][c], 0, 0, 0); \
+                }                                                                        \
         }                                                                                \
         __builtin_amdgcn_sched_barrier(0);     /* the MFMAs before the new loads */      \
         RGM_WLOAD(BUF, qc_ + 2u);                                                        \
@@ -988,7 +1001,10 @@ int aotx_rgemv_launch(const aotx_rgemv_args &a0, hipStream_t s)
         const unsigned int ny = (a.m + RGM_MB - 1u) / RGM_MB;
         const dim3 g1(((a.groups + 7u) / 8u) * 8u * ny * a.splits);
         const size_t x2 = 2u * RGM_MB * (256u + 8u) * 2u, res = RGM_RT * 16u * RGM_MB * 4u;
-        hipLaunchKernelGGL((aotx_rgemm<RGM_MB>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
+        if (g1.x <= 256u)
+            hipLaunchKernelGGL((aotx_rgemm<RGM_MB, true>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
+        else
+            hipLaunchKernelGGL((aotx_rgemm<RGM_MB, false>), g1, dim3(512), x2 > res ? x2 : res, s, a, ny);
         AOTX_LAUNCH_CHECK();
         return 0;
     }
