@@ -13,7 +13,7 @@ import pytest
 import aotx_amd
 from aotx_amd.model import TINY, Shape, Runtime, build_host
 from oracle.kvpolicy import KvPolicy, layout_pages
-from tests.gpu_util import rel_rms
+from tests.gpu_util import read_device, rel_rms
 
 pytestmark = pytest.mark.gpu
 
@@ -295,7 +295,9 @@ def test_wide_qkv_fragment_four_tiles_vs_oracle(torch, orc, rows):
 def test_8b_width_experts_wide_batch_vs_oracle(torch, orc, rows):
     """Routed experts at d_model 4096 with 24 and 40 rows: the expert down product (k = 4096)
     takes the wide kernel through the expert row lists; at 40 rows the dense products run
-    two 32-row passes in one launch, the second with 8 rows."""
+    two 32-row passes in one launch, the second with 8 rows. At 40 rows the first step's 80
+    tokens give some expert more than 32 rows, so the routed products' second 32-row pass
+    computes rows too."""
     shape = Shape(layers=1, hidden=4096, ffn=4096, heads=32, kv_heads=8, head_dim=128,
                   vocab=1024, experts=4, used=2)
     region_dev, region, lay = _device_model(torch, shape, 6)
@@ -309,6 +311,9 @@ def test_8b_width_experts_wide_batch_vs_oracle(torch, orc, rows):
         _, _, lg = rt.step(ids, offs, agents)
         want = ref.step(ids, offs, agents)
         assert rel_rms(lg, want) < 1e-2
+        per_expert = read_device(rt.L.aotx_model_buffer(rt.role, 4), np.uint32, shape.experts)
+        assert per_expert.sum() == 2 * rows * shape.used
+        assert rows < 40 or per_expert.max() > 32
         ids = rng.integers(0, shape.vocab, rows).tolist()
         offs = list(range(rows + 1))
         _, _, lg = rt.step(ids, offs, agents)
