@@ -163,6 +163,51 @@ static __device__ __forceinline__ unsigned int aotx_attn_chunk(unsigned int n, u
         }                                                                                   \
     } while (0)
 
+/* MMA_COMPUTE_SH(KL, VL, B, LIVE, ABS): MMA_COMPUTE over a block its workgroup staged in
+ * LDS (keys at KL, values at VL, rows of VS halves); LIVE: the block is in this wave's
+ * range; ABS: its page is missing. */
+#define MMA_COMPUTE_SH(KL, VL, B, LIVE, ABS)                                                \
+    do {                                                                                    \
+        aotx_f4a sc = {0.0f, 0.0f, 0.0f, 0.0f};                                             \
+        _Pragma("unroll") for (int kk = 0; kk < KK; ++kk)                                   \
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                    \
+                *(const aotx_h8a *)((KL) + r * VS + 32u * (unsigned int)kk + 8u * g), qb[kk], sc, 0, 0, 0); \
+        float pr[4];                                                                        \
+        float mb = -INFINITY;                                                               \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const unsigned int p = (B) * 16u + 4u * g + (unsigned int)i;                    \
+            const bool ok = (LIVE) && p >= p0 && p < plim && !(ABS);                        \
+            pr[i] = ok ? sc[i] * scale : -INFINITY;                                         \
+            mb = fmaxf(mb, pr[i]);                                                          \
+        }                                                                                   \
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));                                             \
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));                                             \
+        const float mnew = fmaxf(mrun, mb);                                                 \
+        const float shift = mnew == -INFINITY ? 1.0f : aotx_exp2(mrun - mnew);              \
+        mrun = mnew;                                                                        \
+        aotx_h4a pa;                                                                        \
+        float mass = 0.0f;                                                                  \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+            const _Float16 ph = mnew == -INFINITY ? (_Float16)0.0f                          \
+                              : (_Float16)aotx_exp2(pr[i] - mnew);                          \
+            pa[i] = ph;                                                                     \
+            mass += (float)ph;                                                              \
+        }                                                                                   \
+        lrun = lrun * shift + mass;                                                         \
+        if (__any(shift != 1.0f)) {                                                         \
+            float sh[4];                                                                    \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) sh[i] = __shfl(shift, (int)(4u * g) + i, 64); \
+            _Pragma("unroll") for (int cc = 0; cc < NS; ++cc)                               \
+                _Pragma("unroll") for (int i = 0; i < 4; ++i) o[cc][i] *= sh[i];            \
+        }                                                                                   \
+        _Pragma("unroll") for (int cc = 0; cc < NS; ++cc) {                                 \
+            const aotx_s4a t4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(                    \
+                (__attribute__((address_space(3))) aotx_s4a *)((VL) + vtr + 16u * (unsigned int)cc)); \
+            o[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(aotx_h4a, t4), \
+                                                          o[cc], 0, 0, 0);                  \
+        }                                                                                   \
+    } while (0)
+
 /* One workgroup = W waves = one (token, KV head, context chunk); each wave takes a
  * contiguous run of 16-position layout blocks. Per wave and block, on the matrix cores:
  *   - scores S[pos][head] = K . q^T: one v_mfma_f32_16x16x32_f16 per 32 of d, keys as the A
@@ -404,9 +449,11 @@ static __device__ __forceinline__ void aotx_attend_body(const aotx_attn_args &a,
  * Wave k < 4 runs one ordered pass of online softmax (the reference's pass per query,
  * cuda/model/attention.cu:22-154) over the first half of the blocks its round's piece sees,
  * wave k + 4 over the second half; the second half's maxima, masses and accumulators pass
- * through LDS and the first wave adds them in block order and writes the outputs. The
- * waves of one sequence read the same blocks at about the same time, which the caches
- * serve. */
+ * through LDS and the first wave adds them in block order and writes the outputs. When
+ * a round's pieces are all of one sequence, the halves split the blocks of its longest
+ * piece instead, and each half's four waves load every block once, into LDS (double
+ * buffered, one barrier per block), where all four read their keys and values; otherwise
+ * each wave loads its own blocks (the same blocks as its neighbours, from the caches). */
 #define AOTX_RUN_RANGE 16u
 template <int D, int G, int W>
 static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a, unsigned int bx)
@@ -425,6 +472,7 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
     __shared__ float hm[WP][16], hl[WP][16];
     __shared__ int hmiss[WP];
     __shared__ float ho[WP][NS][4][64];
+    __shared__ unsigned int rag[WP], rn[WP];
 
     const unsigned int lane = threadIdx.x & 63u;
     const unsigned int wave = threadIdx.x >> 6;
@@ -495,7 +543,103 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
 #pragma unroll
         for (int cc = 0; cc < NS; ++cc) o[cc] = (aotx_f4a){0.0f, 0.0f, 0.0f, 0.0f};
         int missing = 0;
-        if (b0 < b1) {
+        /* the round's sequences and lengths: when its pieces are of one sequence (every
+         * range of a prompt but those holding a sequence boundary), each half's four waves
+         * stage every block once in LDS and all read it there */
+        if (half == 0u && lane == 0u) {
+            rag[wp] = have ? agent : 0xFFFFFFFFu;
+            rn[wp] = have ? n : 0u;
+        }
+        __syncthreads();
+        unsigned int sag = 0xFFFFFFFFu, nmax = 0u;
+        bool one = true;
+#pragma unroll
+        for (unsigned int i = 0; i < WP; ++i) {
+            const unsigned int ai = rag[i];
+            if (ai == 0xFFFFFFFFu) continue;
+            one = one && (sag == 0xFFFFFFFFu || sag == ai);
+            sag = ai;
+            nmax = rn[i] > nmax ? rn[i] : nmax;
+        }
+        if (one && sag != 0xFFFFFFFFu) {
+            aotx_h8a qb[KK];
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                aotx_u4a w = {0u, 0u, 0u, 0u};
+                const unsigned int qi = r / (unsigned int)G, hh = r % (unsigned int)G;
+                if (have && qi < nq)
+                    w = co_load4(a.q + ((unsigned long long)(t + qi) * a.heads + kh * G + hh) * D
+                                     + 32 * kk + 8 * g);
+                qb[kk] = __builtin_bit_cast(aotx_h8a, w);
+            }
+            /* blocks [0, smid) to the first half, [smid, nbm) to the second; both halves
+             * run smid steps (the second's last one, when nbm is odd, adds nothing) */
+            const unsigned int nbm = (nmax + 15u) / 16u;
+            const unsigned int smid = (nbm + 1u) / 2u;
+            const unsigned int sb0 = half == 0u ? 0u : smid;
+            const unsigned int sb1 = half == 0u ? smid : nbm;
+            const unsigned int hid = wp * 64u + lane;          /* loader lane of the half */
+            constexpr unsigned int LP = (unsigned int)D / 64u;  /* 16-byte pieces per lane */
+            const unsigned int kbase = kh * AOTX_KVL_BLOCK * D * 2u;
+            const unsigned int vbase = (a.kv_heads + kh) * AOTX_KVL_BLOCK * D * 2u;
+            unsigned short *const sl = &vl[half * 4u][0];       /* [buf][K, V][16][VS] */
+            unsigned long long spages = 0ull;
+            unsigned int swbase = 0xFFFFFFFFu;
+            aotx_u4a ld[LP];
+            bool sabs[2] = {false, false};
+            bool labs = false;
+            /* block SB's keys and values into the registers ld (a block past the
+             * sequence's last reads the last one) */
+#define SH_LOAD(SB)                                                                         \
+            do {                                                                            \
+                const unsigned int bb_ = (SB) < nbm ? (SB) : nbm - 1u;                      \
+                if (swbase == 0xFFFFFFFFu || bb_ - swbase >= 64u) {                         \
+                    swbase = bb_;                                                           \
+                    const unsigned int bl_ = swbase + lane;                                 \
+                    spages = bl_ < nbm ? (unsigned long long)aotx_kvl_block(a.shape, kv, sag, a.layer, bl_ * 16u) \
+                                       : 0ull;                                              \
+                }                                                                           \
+                unsigned long long pb_ = __shfl(spages, (int)(bb_ - swbase), 64);           \
+                pb_ = ((unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)(pb_ >> 32)) << 32) \
+                    | (unsigned long long)(unsigned int)__builtin_amdgcn_readfirstlane((unsigned int)pb_); \
+                labs = pb_ == 0ull;                                                         \
+                const __amdgpu_buffer_rsrc_t rs_ = __builtin_amdgcn_make_buffer_rsrc(       \
+                    (void *)pb_, (short)0, labs ? 0 : (int)a.shape.block_bytes, 0x00020000); \
+                _Pragma("unroll") for (unsigned int u = 0; u < LP; ++u) {                   \
+                    const unsigned int pc = hid + u * 256u;                                 \
+                    const unsigned int off = pc < 2u * D ? kbase + pc * 16u : vbase + (pc - 2u * D) * 16u; \
+                    ld[u] = __builtin_amdgcn_raw_buffer_load_b128(rs_, (int)off, 0, CPOL);  \
+                }                                                                           \
+            } while (0)
+            /* the registers into LDS buffer BUF (rows padded to VS halves) */
+#define SH_STORE(BUF)                                                                       \
+            do {                                                                            \
+                _Pragma("unroll") for (unsigned int u = 0; u < LP; ++u) {                   \
+                    const unsigned int pc = hid + u * 256u;                                 \
+                    const unsigned int isv = pc < 2u * D ? 0u : 1u;                         \
+                    const unsigned int e = pc - isv * 2u * D;                               \
+                    *(aotx_u4a *)(sl + ((BUF) * 2u + isv) * (16u * VS) + (e / (D / 8u)) * VS \
+                                  + (e % (D / 8u)) * 8u) = ld[u];                           \
+                }                                                                           \
+                sabs[BUF] = labs;                                                           \
+            } while (0)
+            SH_LOAD(sb0);
+            SH_STORE(0u);
+            __syncthreads();
+            for (unsigned int i = 0; i < smid; ++i) {
+                const unsigned int bcur = sb0 + i;
+                SH_LOAD(bcur + 1u);
+                const unsigned int cb = i & 1u;
+                const bool live = bcur < sb1;
+                if (have && live && sabs[cb] && bcur * 16u < n) missing = 1;
+                MMA_COMPUTE_SH(sl + (cb * 2u) * (16u * VS), sl + (cb * 2u + 1u) * (16u * VS), bcur,
+                               live, sabs[cb]);
+                if ((i & 1u) == 0u) SH_STORE(1u); else SH_STORE(0u);
+                __syncthreads();
+            }
+#undef SH_LOAD
+#undef SH_STORE
+        } else if (b0 < b1) {
             aotx_h8a qb[KK];
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk) {
@@ -580,5 +724,6 @@ static __device__ __forceinline__ void aotx_attend_runs(const aotx_attn_args &a,
 #undef MMA_WINDOW
 #undef MMA_LOAD
 #undef MMA_COMPUTE
+#undef MMA_COMPUTE_SH
 
 #endif
